@@ -1,0 +1,149 @@
+/*
+ * moearc_attn.h -- C ABI of libmoearc_attn.so, the MI355X (gfx950) build of MoEArc's attention
+ * hot path.
+ *
+ * Names, argument order, argument types and return codes are those of the reference's FFI
+ * (crates/moearc-kernels/src/ffi.rs), so the reference's Rust wrapper binds this library by
+ * linking it in place of libmoearc_kernels.so. Paths cited are relative to the reference repo.
+ *
+ * Return codes (ffi.rs:8-10, kernels.cpp:470-476):
+ *    0  accepted. Kernels are enqueued on the context's stream and not waited for: "0" means
+ *       the work was accepted, not that it completed. A device fault surfaces at the next
+ *       moearc_sync or moearc_copy_d2h.
+ *   -1  a null argument, or a HIP call failed.
+ *   -2  an argument out of range; nothing was enqueued.
+ *
+ * Types: `unsigned long` is 64-bit (LP64), as in the reference (ffi.rs:263). kv_type is the GGUF
+ * type id: 0 = f32, 1 = f16.
+ *
+ * Threading: one context = one HIP stream, in order; every entry point taking a context enqueues
+ * on that stream. A context is not safe to share across threads (lib.rs:1251-1253).
+ */
+#ifndef MOEARC_ATTN_H
+#define MOEARC_ATTN_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moearc_ctx moearc_ctx;
+
+/* ---- lifecycle and memory (ffi.rs:20-51; kernels.cpp:804-966) ------------------------------- */
+
+/* ffi.rs:20, kernels.cpp:804-828. Opens a stream on the current HIP device and loads the
+ * kernels' code object with hipModuleLoad. NULL when no device or the code object is missing.
+ * MOEARC_PROFILE_EVENTS=1 records a HIP event pair around every attention launch. */
+moearc_ctx *moearc_ctx_create(void);
+/* ffi.rs:21, kernels.cpp:830. Waits for the stream, then frees everything the context owns. */
+void moearc_ctx_destroy(moearc_ctx *c);
+/* ffi.rs:22, kernels.cpp:839. 1 if the context records per-launch device times. */
+int moearc_profile_events_enabled(moearc_ctx *c);
+/* ffi.rs:23, kernels.cpp:841-846. Forget recorded times. */
+int moearc_profile_events_reset(moearc_ctx *c);
+/* ffi.rs:24-28, kernels.cpp:852-871. One "key nanoseconds calls" line per kernel shape; waits for
+ * the recorded launches. Keys are "attn_decode r{n_heads} m{head_dim}" (kernels.cpp:1905-1916),
+ * "attn_prefill r{n_heads} m{head_dim}" and "kv_append r{n_kv_heads} m{head_dim}". */
+int moearc_profile_events_report(moearc_ctx *c, char *out, unsigned long cap);
+/* ffi.rs:29, kernels.cpp:879-882. Block until the stream drains; reports a device fault. */
+int moearc_sync(moearc_ctx *c);
+/* ffi.rs:30. dst[0..n) = 0.0f. */
+int moearc_zero(moearc_ctx *c, float *dst, unsigned long n);
+/* ffi.rs:31, kernels.cpp:884-892. */
+int moearc_device_name(moearc_ctx *c, char *out, unsigned long cap);
+/* ffi.rs:32, kernels.cpp:895-898. NULL on failure. 256-byte aligned. */
+void *moearc_alloc_device(moearc_ctx *c, unsigned long bytes);
+/* ffi.rs:33, kernels.cpp:900-902. Waits for the stream before freeing. */
+void moearc_free_device(moearc_ctx *c, void *p);
+/* ffi.rs:34-39, kernels.cpp:904-907. Blocking. */
+int moearc_copy_h2d(moearc_ctx *c, void *dst, const void *src, unsigned long bytes);
+/* ffi.rs:40-45, kernels.cpp:962-965. Enqueued; src must stay valid until the stream passes it. */
+int moearc_copy_h2d_async(moearc_ctx *c, void *dst, const void *src, unsigned long bytes);
+/* ffi.rs:46-51, kernels.cpp:909-912. Blocking; waits for everything enqueued before it. */
+int moearc_copy_d2h(moearc_ctx *c, void *dst, const void *src, unsigned long bytes);
+
+/* ---- f16 codec (ffi.rs:189-194, kernels.cpp:1727-1735) ----------------------------------------
+ * dst[i] = binary16(src[i]), IEEE round-to-nearest-even, subnormals rounded, overflow to +-inf,
+ * NaN kept NaN with payload 0x200 | mant>>13 (kernels.cpp:152-186). Bit-exact to the reference. */
+int moearc_quantize_f16(moearc_ctx *c, void *dst, const float *src, unsigned long n);
+
+/* ---- paged KV cache write (ffi.rs:204-216, kernels.cpp:1782-1799) -----------------------------
+ * Writes one token's K and V (f32 [n_kv_heads][head_dim]) into page `page_id`, slot `slot` of the
+ * pools, layout [page][slot][kv_head][head_dim], stored as kv_type (f16 by the codec above).
+ * Refusals: null pointer -> -1; kv_type not 0/1, page_tokens == 0, slot >= page_tokens,
+ * n_kv_heads == 0 or head_dim == 0 -> -2. */
+int moearc_kv_append(moearc_ctx *c, void *k_pages, void *v_pages, const float *k, const float *v,
+                     unsigned int page_id, unsigned int slot, unsigned long n_kv_heads,
+                     unsigned long head_dim, unsigned long page_tokens, unsigned int kv_type);
+
+/* ---- single-query paged attention (ffi.rs:218-234, kernels.cpp:1837-1919) ---------------------
+ * For each query head h (KV head h / (n_heads / n_kv_heads)), over logical keys
+ * j in [kv_begin, n_kv) read through block_table (page block_table[j / page_tokens], slot
+ * j % page_tokens):
+ *     s_j = scale * (q_h . K_j)
+ *     out_h = sum_j e^(s_j - M) V_j / (e^(sink_h - M) + sum_j e^(s_j - M)),  M = max(sink_h, max s_j)
+ * with the sink term dropped when `sinks` is NULL. q and out are f32 [n_heads][head_dim].
+ * Refusals, in this order (kernels.cpp:1842-1852): any of c, out, q, k_pages, v_pages, block_table
+ * null -> -1; kv_type not 0/1 -> -2; n_heads, n_kv_heads, head_dim, n_kv or page_tokens zero -> -2;
+ * n_heads % n_kv_heads != 0 -> -2; kv_begin >= n_kv -> -2; head_dim > 1024 -> -2.
+ * Paths: f16 KV with head_dim 64, a group of at most 16 heads and a power-of-two page size run the
+ * split-K MFMA kernel; every other accepted shape runs a general f32 kernel. */
+int moearc_attn_decode(moearc_ctx *c, float *out, const float *q, const void *k_pages,
+                       const void *v_pages, const unsigned int *block_table, const float *sinks,
+                       unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
+                       unsigned long kv_begin, unsigned long n_kv, unsigned long page_tokens,
+                       float scale, unsigned int kv_type);
+
+/* ---- extensions (no single counterpart in the reference; same conventions) -------------------- */
+
+/* Output element type of the extensions below. */
+#define MOEARC_OUT_F32 0u
+#define MOEARC_OUT_F16 1u
+
+/* Batched ragged decode: n_seqs independent moearc_attn_decode calls in one launch.
+ * Sequence b reads q[b][n_heads][head_dim], writes out[b][n_heads][head_dim] (f32 or f16 by
+ * out_type), attends [kv_begin[b], n_kv[b]) through block-table row
+ * block_tables[b * bt_stride ...]. kv_begin and n_kv are HOST arrays of n_seqs entries (the
+ * engine keeps sequence lengths on the host, moe.rs:1890-1912); every other pointer is device
+ * memory. Each sequence must equal the single call with the same arguments.
+ * Refusals: as moearc_attn_decode per sequence (an empty span in any sequence -> -2), plus
+ * n_seqs == 0, out_type not 0/1, or bt_stride < ceil(n_kv[b] / page_tokens) -> -2. */
+int moearc_attn_decode_batched(moearc_ctx *c, void *out, unsigned int out_type, const float *q,
+                               const void *k_pages, const void *v_pages,
+                               const unsigned int *block_tables, unsigned long bt_stride,
+                               const unsigned int *kv_begin, const unsigned int *n_kv,
+                               const float *sinks, unsigned long n_seqs, unsigned long n_heads,
+                               unsigned long n_kv_heads, unsigned long head_dim,
+                               unsigned long page_tokens, float scale, unsigned int kv_type);
+
+/* Chunked prefill over a paged f16 KV cache. The chunk's n_q tokens sit at absolute positions
+ * pos0 .. pos0+n_q-1 and their K/V are already in the cache (logical keys 0 .. pos0+n_q-1 through
+ * block_table). Row i is, exactly, moearc_attn_decode at n_kv = pos0+i+1 with
+ * kv_begin = (n_swa > 0 ? max(0, pos0+i+1-n_swa) : 0) -- the reference engine's prefill, one
+ * decode per prompt token (moe.rs:1856-1862, moe.rs:2020-2027).
+ * q: f16 [n_q][n_heads][head_dim]; out: [n_q][n_heads][head_dim] f32 or f16 by out_type.
+ * Requires kv_type 1 (f16), head_dim 64, a group n_heads/n_kv_heads of 1, 2, 4 or 8 and a
+ * power-of-two page_tokens; other shapes -> -2. */
+int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const void *q,
+                        const void *k_pages, const void *v_pages, const unsigned int *block_table,
+                        const float *sinks, unsigned long n_q, unsigned long pos0,
+                        unsigned long n_swa, unsigned long n_heads, unsigned long n_kv_heads,
+                        unsigned long head_dim, unsigned long page_tokens, float scale,
+                        unsigned int kv_type);
+
+/* Chunk append: writes n_tok tokens' K and V (f32 [n_tok][n_kv_heads][head_dim]) at
+ * (page_ids[t], slots[t]) (device u32 arrays). Equal to n_tok moearc_kv_append calls in order
+ * (moe.rs:2029-2042 once per token); two tokens naming the same slot are a caller error.
+ * Refusals as moearc_kv_append (slot range is not checked on the host: slots are device data). */
+int moearc_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
+                           const float *v, const unsigned int *page_ids, const unsigned int *slots,
+                           unsigned long n_tok, unsigned long n_kv_heads, unsigned long head_dim,
+                           unsigned long page_tokens, unsigned int kv_type);
+
+/* The stream the context enqueues on (a hipStream_t), so a caller can order its own work. */
+void *moearc_ctx_stream(moearc_ctx *c);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOEARC_ATTN_H */

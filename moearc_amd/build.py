@@ -1,0 +1,62 @@
+"""Builds the native library in-tree.
+
+Two artefacts, both written next to this file:
+
+* ``moearc_attn_gfx950.co`` -- the device code object (every kernel, one translation unit), built
+  by ``hipcc --genco`` for gfx950 only and loaded at context creation with ``hipModuleLoad``;
+* ``libmoearc_attn.so`` -- the host runtime behind the C ABI in ``include/moearc_attn.h``, built by
+  the host compiler against the HIP runtime API (no device code in it).
+
+Run ``python -m moearc_amd.build`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+CODE_OBJECT = os.path.join(HERE, "moearc_attn_gfx950.co")
+LIBRARY = os.path.join(HERE, "libmoearc_attn.so")
+
+# Packed-FP32 instructions stay disabled (v_pk_fma_f32 and friends are not emitted).
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-O3", "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}")
+    return res
+
+
+def build(verbose: bool = False) -> None:
+    hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    tmp_co = CODE_OBJECT + ".tmp"
+    _run([hipcc, *HIPCC_FLAGS, "-I", CSRC, os.path.join(CSRC, "moearc_kernels.hip"), "-o", tmp_co],
+         verbose)
+    os.replace(tmp_co, CODE_OBJECT)
+    cxx = os.environ.get("CXX", "g++")
+    tmp_so = LIBRARY + ".tmp"
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+          "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", CSRC, "-I", os.path.join(ROCM, "include"),
+          os.path.join(CSRC, "runtime.cpp"), "-o", tmp_so,
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl",
+          "-Wl,-rpath," + os.path.join(ROCM, "lib")], verbose)
+    os.replace(tmp_so, LIBRARY)
+
+
+if __name__ == "__main__":
+    build(verbose=True)

@@ -1,0 +1,301 @@
+"""Python mirror of the reference's safe wrapper (crates/moearc-kernels/src/lib.rs) over the C ABI.
+
+Same names, argument meaning and error behaviour as the Rust ``Context``: a wrapper submits and
+returns; a non-zero return code drains the stream before it is reported (lib.rs:198-215); ``-2``
+is ``BadArgument`` and any other failure ``Failed`` (lib.rs:157-165); buffer sizes are checked
+before the call (``BufferTooSmall``, lib.rs:1216-1221); ``MOEARC_SYNC_EACH=1`` waits after every
+launch (lib.rs:183-195). Device memory is owned by ``DeviceBuffer`` and freed when it is dropped.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from typing import Optional
+
+import numpy as np
+
+from . import native
+
+
+class KernelError(Exception):
+    """Base of the wrapper's errors (lib.rs ``KernelError``)."""
+
+
+class NoDevice(KernelError):
+    pass
+
+
+class OutOfMemory(KernelError):
+    def __init__(self, nbytes: int):
+        super().__init__(f"device allocation of {nbytes} bytes failed")
+        self.nbytes = nbytes
+
+
+class BadArgument(KernelError):
+    pass
+
+
+class Failed(KernelError):
+    pass
+
+
+class BufferTooSmall(KernelError):
+    def __init__(self, what: str, need: int, have: int):
+        super().__init__(f"{what}: need {need} bytes, have {have}")
+        self.what, self.need, self.have = what, need, have
+
+
+class KvType(enum.IntEnum):
+    """How a KV page stores its numbers; the value is the GGUF type id (reference.rs:728-752)."""
+    F32 = 0
+    F16 = 1
+
+    @property
+    def elem_bytes(self) -> int:
+        return 4 if self is KvType.F32 else 2
+
+
+OUT_F32 = 0
+OUT_F16 = 1
+
+
+class DeviceBuffer:
+    """An owned device allocation (lib.rs ``DeviceBuffer``)."""
+
+    def __init__(self, ctx: "Context", ptr: int, nbytes: int):
+        self.ctx, self.ptr, self.len = ctx, ptr, nbytes
+
+    def require(self, what: str, need: int) -> None:
+        if self.len < need:
+            raise BufferTooSmall(what, need, self.len)
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx._lib.moearc_free_device(self.ctx.raw, self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self.ctx.raw:
+                self.free()
+        except Exception:
+            pass
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    if rc == -2:
+        raise BadArgument(what)
+    raise Failed(what)
+
+
+class Context:
+    """A HIP stream on the current device plus the loaded kernels (lib.rs ``Context``)."""
+
+    def __init__(self):
+        self._lib = native.load()
+        self.raw = self._lib.moearc_ctx_create()
+        if not self.raw:
+            raise NoDevice("moearc_ctx_create returned NULL (no HIP device, or code object missing)")
+        self.sync_each = os.environ.get("MOEARC_SYNC_EACH") == "1"
+
+    # ---- lifecycle ----------------------------------------------------------------------------
+    def close(self) -> None:
+        if self.raw:
+            self._lib.moearc_ctx_destroy(self.raw)
+            self.raw = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def finish(self, rc: int, what: str) -> None:
+        """Drain before reporting an error, so nothing in flight outlives the caller's buffers."""
+        if rc != 0:
+            self._lib.moearc_sync(self.raw)
+            _check(rc, what)
+        elif self.sync_each:
+            self.sync()
+
+    def sync(self) -> None:
+        _check(self._lib.moearc_sync(self.raw), "stream synchronisation")
+
+    @property
+    def stream(self) -> int:
+        return self._lib.moearc_ctx_stream(self.raw) or 0
+
+    def device_name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        if self._lib.moearc_device_name(self.raw, buf, 256) != 0:
+            raise Failed("querying the device name")
+        return buf.value.decode(errors="replace")
+
+    # ---- profiling ----------------------------------------------------------------------------
+    def profile_events_enabled(self) -> bool:
+        return bool(self._lib.moearc_profile_events_enabled(self.raw))
+
+    def profile_events_reset(self) -> None:
+        _check(self._lib.moearc_profile_events_reset(self.raw), "profile reset")
+
+    def profile_events_report(self) -> dict:
+        """{key: (nanoseconds, calls)} from ``moearc_profile_events_report``."""
+        buf = ctypes.create_string_buffer(1 << 16)
+        _check(self._lib.moearc_profile_events_report(self.raw, buf, 1 << 16), "profile report")
+        out = {}
+        for line in buf.value.decode().splitlines():
+            parts = line.rsplit(" ", 2)
+            if len(parts) == 3:
+                out[parts[0]] = (int(parts[1]), int(parts[2]))
+        return out
+
+    # ---- memory -------------------------------------------------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        ptr = self._lib.moearc_alloc_device(self.raw, int(nbytes))
+        if not ptr:
+            raise OutOfMemory(nbytes)
+        return DeviceBuffer(self, ptr, int(nbytes))
+
+    def alloc_n(self, dtype, n: int) -> DeviceBuffer:
+        return self.alloc(int(n) * np.dtype(dtype).itemsize)
+
+    def upload_slice(self, dst: DeviceBuffer, src: np.ndarray) -> None:
+        src = np.ascontiguousarray(src)
+        dst.require("upload destination", src.nbytes)
+        _check(self._lib.moearc_copy_h2d(self.raw, dst.ptr, src.ctypes.data, src.nbytes), "upload")
+
+    def upload(self, src: np.ndarray) -> DeviceBuffer:
+        src = np.ascontiguousarray(src)
+        buf = self.alloc(max(1, src.nbytes))
+        self.upload_slice(buf, src)
+        return buf
+
+    def download_slice(self, dst: np.ndarray, src: DeviceBuffer) -> np.ndarray:
+        assert dst.flags.c_contiguous
+        src.require("download source", dst.nbytes)
+        _check(self._lib.moearc_copy_d2h(self.raw, dst.ctypes.data, src.ptr, dst.nbytes), "download")
+        return dst
+
+    def download(self, src: DeviceBuffer, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        return self.download_slice(out, src)
+
+    def zero(self, dst: DeviceBuffer, n: int) -> None:
+        dst.require("zero destination", n * 4)
+        self.finish(self._lib.moearc_zero(self.raw, dst.ptr, n), "zero")
+
+    # ---- kernels ------------------------------------------------------------------------------
+    def quantize_f16(self, dst: DeviceBuffer, src: DeviceBuffer, n: int) -> None:
+        """f32 -> f16 RNE (kernels.cpp:1727-1735)."""
+        src.require("f32 source", n * 4)
+        dst.require("f16 destination", n * 2)
+        self.finish(self._lib.moearc_quantize_f16(self.raw, dst.ptr, src.ptr, n), "f16 narrowing")
+
+    def kv_append(self, k_pages: DeviceBuffer, v_pages: DeviceBuffer, k: DeviceBuffer,
+                  v: DeviceBuffer, page_id: int, slot: int, n_kv_heads: int, head_dim: int,
+                  page_tokens: int, kv: KvType) -> None:
+        """One token's K and V into a page slot (lib.rs:1079-1114)."""
+        kv = KvType(kv)
+        row = n_kv_heads * head_dim
+        k.require("key vector", row * 4)
+        v.require("value vector", row * 4)
+        need = (page_id * page_tokens + slot + 1) * row * kv.elem_bytes
+        k_pages.require("key pages", need)
+        v_pages.require("value pages", need)
+        rc = self._lib.moearc_kv_append(self.raw, k_pages.ptr, v_pages.ptr, k.ptr, v.ptr, page_id,
+                                        slot, n_kv_heads, head_dim, page_tokens, int(kv))
+        self.finish(rc, "KV append")
+
+    def kv_append_chunk(self, k_pages: DeviceBuffer, v_pages: DeviceBuffer, k: DeviceBuffer,
+                        v: DeviceBuffer, page_ids: DeviceBuffer, slots: DeviceBuffer, n_tok: int,
+                        n_kv_heads: int, head_dim: int, page_tokens: int, kv: KvType) -> None:
+        """n_tok tokens' K and V at (page_ids[t], slots[t]); equal to n_tok kv_append calls."""
+        row = n_kv_heads * head_dim
+        k.require("key rows", n_tok * row * 4)
+        v.require("value rows", n_tok * row * 4)
+        page_ids.require("page ids", n_tok * 4)
+        slots.require("slots", n_tok * 4)
+        rc = self._lib.moearc_kv_append_chunk(self.raw, k_pages.ptr, v_pages.ptr, k.ptr, v.ptr,
+                                              page_ids.ptr, slots.ptr, n_tok, n_kv_heads,
+                                              head_dim, page_tokens, int(KvType(kv)))
+        self.finish(rc, "KV chunk append")
+
+    def attn_decode(self, out, q, k_pages, v_pages, block_table, n_heads, n_kv_heads, head_dim,
+                    n_kv, page_tokens, scale, kv) -> None:
+        """Full causal attention over every cached key (lib.rs:1135-1171)."""
+        self.attn_decode_ext(out, q, k_pages, v_pages, block_table, None, n_heads, n_kv_heads,
+                             head_dim, 0, n_kv, page_tokens, scale, kv)
+
+    def attn_decode_ext(self, out: DeviceBuffer, q: DeviceBuffer, k_pages: DeviceBuffer,
+                        v_pages: DeviceBuffer, block_table: DeviceBuffer,
+                        sinks: Optional[DeviceBuffer], n_heads: int, n_kv_heads: int,
+                        head_dim: int, kv_begin: int, n_kv: int, page_tokens: int, scale: float,
+                        kv: KvType) -> None:
+        """Attention with sinks and an explicit key span [kv_begin, n_kv) (lib.rs:1188-1242)."""
+        if n_kv_heads == 0 or n_heads % n_kv_heads != 0:
+            raise BadArgument("n_heads is not a multiple of n_kv_heads")
+        if page_tokens == 0:
+            raise BadArgument("page_tokens must be non-zero")
+        if kv_begin >= n_kv:
+            raise BadArgument("kv_begin is not before n_kv")
+        q.require("query", n_heads * head_dim * 4)
+        out.require("attention output", n_heads * head_dim * 4)
+        block_table.require("block table", -(-n_kv // page_tokens) * 4)
+        if sinks is not None:
+            sinks.require("attention sinks", n_heads * 4)
+        rc = self._lib.moearc_attn_decode(self.raw, out.ptr, q.ptr, k_pages.ptr, v_pages.ptr,
+                                          block_table.ptr, sinks.ptr if sinks is not None else None,
+                                          n_heads, n_kv_heads, head_dim, kv_begin, n_kv,
+                                          page_tokens, float(scale), int(KvType(kv)))
+        self.finish(rc, "paged attention")
+
+    def attn_decode_batched(self, out: DeviceBuffer, q: DeviceBuffer, k_pages: DeviceBuffer,
+                            v_pages: DeviceBuffer, block_tables: DeviceBuffer, bt_stride: int,
+                            kv_begin, n_kv, sinks: Optional[DeviceBuffer], n_heads: int,
+                            n_kv_heads: int, head_dim: int, page_tokens: int, scale: float,
+                            kv: KvType, out_type: int = OUT_F32) -> None:
+        """Ragged batch of decode calls; kv_begin/n_kv are host sequences of per-sequence ints."""
+        kb = np.ascontiguousarray(kv_begin, np.uint32)
+        nk = np.ascontiguousarray(n_kv, np.uint32)
+        n_seqs = kb.size
+        if nk.size != n_seqs:
+            raise BadArgument("kv_begin and n_kv differ in length")
+        out_bytes = 2 if out_type == OUT_F16 else 4
+        q.require("query", n_seqs * n_heads * head_dim * 4)
+        out.require("attention output", n_seqs * n_heads * head_dim * out_bytes)
+        block_tables.require("block tables", n_seqs * bt_stride * 4)
+        if sinks is not None:
+            sinks.require("attention sinks", n_heads * 4)
+        rc = self._lib.moearc_attn_decode_batched(
+            self.raw, out.ptr, out_type, q.ptr, k_pages.ptr, v_pages.ptr, block_tables.ptr,
+            bt_stride, kb.ctypes.data, nk.ctypes.data, sinks.ptr if sinks is not None else None,
+            n_seqs, n_heads, n_kv_heads, head_dim, page_tokens, float(scale), int(KvType(kv)))
+        self.finish(rc, "batched paged attention")
+
+    def attn_prefill(self, out: DeviceBuffer, q: DeviceBuffer, k_pages: DeviceBuffer,
+                     v_pages: DeviceBuffer, block_table: DeviceBuffer,
+                     sinks: Optional[DeviceBuffer], n_q: int, pos0: int, n_swa: int,
+                     n_heads: int, n_kv_heads: int, head_dim: int, page_tokens: int,
+                     scale: float, kv: KvType = KvType.F16, out_type: int = OUT_F32) -> None:
+        """Chunked prefill: row i equals decode at n_kv = pos0+i+1 (moe.rs:1856-1862)."""
+        out_bytes = 2 if out_type == OUT_F16 else 4
+        q.require("query (f16)", n_q * n_heads * head_dim * 2)
+        out.require("attention output", n_q * n_heads * head_dim * out_bytes)
+        block_table.require("block table", -(-(pos0 + n_q) // max(1, page_tokens)) * 4)
+        if sinks is not None:
+            sinks.require("attention sinks", n_heads * 4)
+        rc = self._lib.moearc_attn_prefill(self.raw, out.ptr, out_type, q.ptr, k_pages.ptr,
+                                           v_pages.ptr, block_table.ptr,
+                                           sinks.ptr if sinks is not None else None, n_q, pos0,
+                                           n_swa, n_heads, n_kv_heads, head_dim, page_tokens,
+                                           float(scale), int(KvType(kv)))
+        self.finish(rc, "chunked prefill attention")

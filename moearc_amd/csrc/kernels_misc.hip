@@ -1,0 +1,67 @@
+// Element-wise kernels of the attention path: zero fill, f32 -> f16 narrowing and the paged KV
+// append (one token, or a chunk of tokens). All are HBM-bound streaming kernels; each thread
+// handles one element and the grids are sized on the host.
+#include "common.h"
+
+// Binary32 -> binary16 with the reference's rounding contract (kernels.cpp:152-186): IEEE
+// round-to-nearest-even, subnormals rounded, overflow to +-inf. The hardware conversion
+// (v_cvt_f16_f32 in the default RNE mode, f16 denormals preserved) implements exactly that; the
+// one case it leaves open is a NaN's payload, which the reference defines as quiet bit | the top
+// mantissa bits, so NaNs are encoded explicitly.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    const uint32_t x = __float_as_uint(f);
+    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu) != 0u)
+        return (uint16_t) (((x >> 16) & 0x8000u) | 0x7E00u | ((x & 0x7FFFFFu) >> 13));
+    _Float16 h = (_Float16) f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+extern "C" __global__ void moearc_zero_k(float *dst, uint64_t n) {
+    for (uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t) gridDim.x * blockDim.x)
+        dst[i] = 0.0f;
+}
+
+extern "C" __global__ void moearc_quantize_f16_k(uint16_t *dst, const float *src, uint64_t n) {
+    for (uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t) gridDim.x * blockDim.x)
+        dst[i] = f32_to_f16_bits(src[i]);
+}
+
+// One token: element i of the [n_kv_heads][head_dim] row lands at base + i
+// (layout [page][slot][kv_head][head_dim], kernels.cpp:1782-1799).
+extern "C" __global__ void moearc_kv_append_k(void *k_pages, void *v_pages, const float *k,
+                                              const float *v, uint64_t base, uint64_t row,
+                                              uint32_t kv_type) {
+    const uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= row) return;
+    if (kv_type == MOEARC_KV_F16) {
+        ((uint16_t *) k_pages)[base + i] = f32_to_f16_bits(k[i]);
+        ((uint16_t *) v_pages)[base + i] = f32_to_f16_bits(v[i]);
+    } else {
+        ((float *) k_pages)[base + i] = k[i];
+        ((float *) v_pages)[base + i] = v[i];
+    }
+}
+
+// A chunk of tokens: token t goes to (page_ids[t], slots[t]). A slot outside the page is skipped
+// (the host cannot see device-resident slots, so the bound is enforced here).
+extern "C" __global__ void moearc_kv_append_chunk_k(void *k_pages, void *v_pages, const float *k,
+                                                    const float *v, const uint32_t *page_ids,
+                                                    const uint32_t *slots, uint64_t n_tok,
+                                                    uint64_t row, uint64_t page_tokens,
+                                                    uint32_t kv_type) {
+    const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_tok * row) return;
+    const uint64_t t = g / row, i = g - t * row;
+    const uint32_t slot = slots[t];
+    if (slot >= page_tokens) return;
+    const uint64_t dst = ((uint64_t) page_ids[t] * page_tokens + slot) * row + i;
+    if (kv_type == MOEARC_KV_F16) {
+        ((uint16_t *) k_pages)[dst] = f32_to_f16_bits(k[g]);
+        ((uint16_t *) v_pages)[dst] = f32_to_f16_bits(v[g]);
+    } else {
+        ((float *) k_pages)[dst] = k[g];
+        ((float *) v_pages)[dst] = v[g];
+    }
+}

@@ -1,0 +1,607 @@
+// Host side of libmoearc_attn.so: the C ABI declared in include/moearc_attn.h.
+//
+// A context owns one HIP stream and the kernels' code object (moearc_attn_gfx950.co, beside this
+// library), loaded with hipModuleLoad; every entry point validates its arguments on the host, in
+// the reference's order, before anything is enqueued, then launches with hipModuleLaunchKernel
+// on the context's stream and returns without waiting (the reference's "0 = accepted" contract,
+// kernels.cpp:875-880).
+//
+// Built with the host compiler against the HIP runtime API only; no device code lives here.
+#include "moearc_attn.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "launch_args.h"
+
+namespace {
+
+constexpr int OK = 0;
+constexpr int ERR = -1;
+constexpr int ERR_ARG = -2;
+
+struct Pending {
+    std::string key;
+    hipEvent_t start, stop;
+};
+
+struct KernelTime {
+    std::string key;
+    unsigned long long ns;
+    unsigned long long calls;
+};
+
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr((void *) &library_dir, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        const size_t s = p.rfind('/');
+        if (s != std::string::npos) return p.substr(0, s);
+    }
+    return ".";
+}
+
+bool is_pow2(unsigned long x) { return x && !(x & (x - 1)); }
+
+uint32_t log2u(unsigned long x) {
+    uint32_t s = 0;
+    while ((1ul << s) < x) ++s;
+    return s;
+}
+
+}  // namespace
+
+struct moearc_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
+    hipFunction_t f_dec_general = nullptr;
+    hipFunction_t f_dec_fast[5] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2
+    hipFunction_t f_dec_merge = nullptr;
+    hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
+    bool profiling = false;
+    std::vector<Pending> pending;
+    std::vector<KernelTime> totals;
+    std::vector<hipEvent_t> event_pool;
+    hipEvent_t open_start = nullptr;  // start event of a bracket spanning two launches
+    // split-K workspace: one partial record per work-group of the split kernel
+    float *ws = nullptr;
+    size_t ws_floats = 0;
+    int decode_variant_override = -1;  // MOEARC_DECODE_VARIANT, e.g. "4x4"
+    unsigned long split_override = 0;  // MOEARC_DECODE_SPLIT (keys per split)
+};
+
+namespace {
+
+hipEvent_t take_event(moearc_ctx *c) {
+    if (!c->event_pool.empty()) {
+        hipEvent_t e = c->event_pool.back();
+        c->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void flush_events(moearc_ctx *c) {
+    for (auto &p : c->pending) {
+        float ms = 0.f;
+        if (hipEventSynchronize(p.stop) == hipSuccess &&
+            hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+            const unsigned long long ns = (unsigned long long) (ms * 1.0e6);
+            bool found = false;
+            for (auto &t : c->totals)
+                if (t.key == p.key) {
+                    t.ns += ns;
+                    t.calls += 1;
+                    found = true;
+                    break;
+                }
+            if (!found) c->totals.push_back(KernelTime{p.key, ns, 1});
+        }
+        c->event_pool.push_back(p.start);
+        c->event_pool.push_back(p.stop);
+    }
+    c->pending.clear();
+}
+
+// Launch `f` with one by-value argument block. With profiling on, a HIP event pair brackets
+// the work under one key: phase 0 brackets this launch alone; phase 1 opens a bracket that the
+// next launch, with phase 2, closes (an attention call that is two kernels is timed as one).
+template <typename Args>
+int launch(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned block, const Args &args,
+           const char *what, unsigned long r, unsigned long m, int phase = 0) {
+    if (!f) return ERR;
+    if (c->profiling && phase != 2) {
+        c->open_start = take_event(c);
+        if (c->open_start) hipEventRecord(c->open_start, c->stream);
+    }
+    size_t size = sizeof(Args);
+    void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *) &args, HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                      &size, HIP_LAUNCH_PARAM_END};
+    const hipError_t err =
+        hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, c->stream, nullptr, config);
+    if (c->profiling && phase != 1 && c->open_start) {
+        hipEvent_t e1 = take_event(c);
+        if (e1) {
+            hipEventRecord(e1, c->stream);
+            char key[96];
+            std::snprintf(key, sizeof(key), "%s r%lu m%lu", what, r, m);
+            c->pending.push_back(Pending{key, c->open_start, e1});
+            if (c->pending.size() >= 16384) flush_events(c);
+        }
+        c->open_start = nullptr;
+    }
+    return err == hipSuccess ? OK : ERR;
+}
+
+int ensure_workspace(moearc_ctx *c, size_t floats) {
+    if (floats <= c->ws_floats) return OK;
+    if (c->ws) {
+        hipStreamSynchronize(c->stream);  // the previous workspace may still be in use
+        hipFree(c->ws);
+        c->ws = nullptr;
+        c->ws_floats = 0;
+    }
+    if (hipMalloc((void **) &c->ws, floats * sizeof(float)) != hipSuccess) return ERR;
+    c->ws_floats = floats;
+    return OK;
+}
+
+// ---- decode dispatch ----------------------------------------------------------------------------
+
+struct SeqSpan {
+    uint32_t begin, end;
+};
+
+bool fast_decode_ok(unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
+                    unsigned long page_tokens, unsigned int kv_type) {
+    return kv_type == 1u && head_dim == 64 && n_heads / n_kv_heads <= 16 && is_pow2(page_tokens) &&
+           page_tokens <= (1ul << 30);
+}
+
+// Block-table entries the split-K kernel stages in LDS per work-group (PT_CAP in the kernel).
+constexpr uint64_t kPageTableCap = 1024;
+
+// Split-K decode variants: KV heads per work-group x waves per KV head (moearc_attn_decode_f16d64_*).
+struct DecodeVariant {
+    const char *name;
+    unsigned kb, wpk;
+};
+constexpr DecodeVariant kDecodeVariants[5] = {{"1x4", 1, 4}, {"1x16", 1, 16}, {"2x8", 2, 8},
+                                              {"4x4", 4, 4}, {"8x2", 8, 2}};
+
+// Variant and keys per split. A work-group reads kb*128 bytes of each key row (kb KV heads; four
+// keep HBM accesses row-local) with wpk waves per head; the split is sized so that the launch has
+// about 384 work-groups of 16 waves (1.5 per CU on 256 CUs), each wave taking at least one 32-key
+// tile. Returns false when a split would span more pages than the kernel stages.
+bool plan_split(moearc_ctx *c, const std::vector<SeqSpan> &spans, unsigned long G,
+                unsigned long page_tokens, int &variant, std::vector<uint32_t> &split_len) {
+    variant = G >= 4 ? 3 : (G == 2 ? 2 : (G == 1 ? 1 : 3));
+    if (c->decode_variant_override >= 0) variant = c->decode_variant_override;
+    const unsigned kb = kDecodeVariants[variant].kb, wpk = kDecodeVariants[variant].wpk;
+    const uint64_t nkb = (G + kb - 1) / kb;
+    const uint64_t quantum = 32ull * wpk;  // one tile per wave
+    uint64_t total = 0;
+    for (auto &s : spans) total += (uint64_t) (s.end - s.begin) * nkb;
+    const uint64_t target_wgs = 384;
+    uint64_t base = (total + target_wgs - 1) / target_wgs;
+    split_len.resize(spans.size());
+    for (size_t i = 0; i < spans.size(); ++i) {
+        uint64_t len = c->split_override ? c->split_override : base;
+        len = std::max<uint64_t>(len, quantum);
+        len = (len + quantum - 1) / quantum * quantum;
+        if (len / page_tokens + 2 > kPageTableCap) return false;
+        split_len[i] = (uint32_t) std::min<uint64_t>(len, 0x40000000ull);
+    }
+    return true;
+}
+
+int decode_launch(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
+                  const void *k_pages, const void *v_pages, const unsigned int *block_tables,
+                  unsigned long bt_stride, const std::vector<SeqSpan> &spans, const float *sinks,
+                  unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
+                  unsigned long page_tokens, float scale, unsigned int kv_type) {
+    const size_t nseq = spans.size();
+    const size_t per = MOEARC_MAX_SEQS_PER_LAUNCH;
+    const bool fast_shape = fast_decode_ok(n_heads, n_kv_heads, head_dim, page_tokens, kv_type);
+    for (size_t s0 = 0; s0 < nseq; s0 += per) {
+        const size_t cnt = std::min(per, nseq - s0);
+        const float *qb = q + s0 * n_heads * head_dim;
+        const size_t out_off = s0 * n_heads * head_dim * (out_f16 ? 2 : 4);
+        void *ob = (char *) out + out_off;
+        const unsigned int *btb = block_tables + s0 * bt_stride;
+        std::vector<SeqSpan> sub(spans.begin() + s0, spans.begin() + s0 + cnt);
+        int variant = 3;
+        std::vector<uint32_t> split_len;
+        const bool fast = fast_shape && plan_split(c, sub, n_kv_heads, page_tokens, variant, split_len);
+        if (!fast) {
+            DecodeGeneralArgs a{};
+            a.q = qb;
+            a.k_pages = k_pages;
+            a.v_pages = v_pages;
+            a.block_tables = btb;
+            a.sinks = sinks;
+            a.out = ob;
+            a.bt_stride = bt_stride;
+            a.n_heads = (uint32_t) n_heads;
+            a.n_kv_heads = (uint32_t) n_kv_heads;
+            a.head_dim = (uint32_t) head_dim;
+            a.page_tokens = (uint32_t) page_tokens;
+            a.kv_type = kv_type;
+            a.out_f16 = out_f16;
+            a.scale = scale;
+            a.n_seqs = (uint32_t) cnt;
+            for (size_t i = 0; i < cnt; ++i) {
+                a.kv_begin[i] = spans[s0 + i].begin;
+                a.n_kv[i] = spans[s0 + i].end;
+            }
+            const int rc = launch(c, c->f_dec_general, (unsigned) (cnt * n_heads), 256, a,
+                                  "attn_decode", n_heads, head_dim);
+            if (rc) return rc;
+            continue;
+        }
+        DecodeArgs a{};
+        a.q = qb;
+        a.k_pages = (const uint16_t *) k_pages;
+        a.v_pages = (const uint16_t *) v_pages;
+        a.block_tables = btb;
+        a.sinks = sinks;
+        a.out = ob;
+        a.bt_stride = bt_stride;
+        a.n_heads = (uint32_t) n_heads;
+        a.n_kv_heads = (uint32_t) n_kv_heads;
+        a.group = (uint32_t) (n_heads / n_kv_heads);
+        a.pt_shift = log2u(page_tokens);
+        a.out_f16 = out_f16;
+        a.scale_log2e = scale * 1.4426950408889634f;
+        a.n_seqs = (uint32_t) cnt;
+        uint32_t items = 0;
+        for (size_t i = 0; i < cnt; ++i) {
+            a.item_begin[i] = items;
+            a.kv_begin[i] = sub[i].begin;
+            a.n_kv[i] = sub[i].end;
+            a.split_len[i] = split_len[i];
+            items += (sub[i].end - sub[i].begin + split_len[i] - 1) / split_len[i];
+        }
+        for (size_t i = cnt; i <= MOEARC_MAX_SEQS_PER_LAUNCH; ++i) a.item_begin[i] = items;
+        const unsigned kb = kDecodeVariants[variant].kb, wpk = kDecodeVariants[variant].wpk;
+        const size_t nkb = (n_kv_heads + kb - 1) / kb;
+        const size_t wgs = (size_t) items * nkb;
+        if (wgs > 0x7FFFFFFFull) return ERR_ARG;
+        if (ensure_workspace(c, (size_t) items * n_kv_heads * MOEARC_PARTIAL_FLOATS)) return ERR;
+        a.ws = c->ws;
+        const bool any_split = items > cnt;  // some sequence has more than one split
+        const int rc = launch(c, c->f_dec_fast[variant], (unsigned) wgs, 64u * kb * wpk, a,
+                              "attn_decode", n_heads, head_dim, any_split ? 1 : 0);
+        if (rc) return rc;
+        if (any_split) {
+            const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads), 256, a,
+                                  "attn_decode", n_heads, head_dim, 2);
+            if (rm) return rm;
+        }
+    }
+    return OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+moearc_ctx *moearc_ctx_create(void) {
+    auto *c = new moearc_ctx();
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        delete c;
+        return nullptr;
+    }
+    if (hipGetDevice(&c->device) != hipSuccess) {
+        delete c;
+        return nullptr;
+    }
+    // Default priority, in-order (the reference's in-order queue, kernels.cpp:806-810).
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return nullptr;
+    }
+    const char *co_env = std::getenv("MOEARC_CODE_OBJECT");
+    const std::string co = co_env ? std::string(co_env) : library_dir() + "/moearc_attn_gfx950.co";
+    if (hipModuleLoad(&c->module, co.c_str()) != hipSuccess) {
+        std::fprintf(stderr, "moearc: cannot load code object %s\n", co.c_str());
+        hipStreamDestroy(c->stream);
+        delete c;
+        return nullptr;
+    }
+    struct {
+        hipFunction_t *slot;
+        const char *name;
+    } fns[] = {
+        {&c->f_zero, "moearc_zero_k"},
+        {&c->f_quant, "moearc_quantize_f16_k"},
+        {&c->f_append, "moearc_kv_append_k"},
+        {&c->f_append_chunk, "moearc_kv_append_chunk_k"},
+        {&c->f_dec_general, "moearc_attn_decode_general_k"},
+        {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k1w4"},
+        {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w16"},
+        {&c->f_dec_fast[2], "moearc_attn_decode_f16d64_k2w8"},
+        {&c->f_dec_fast[3], "moearc_attn_decode_f16d64_k4w4"},
+        {&c->f_dec_fast[4], "moearc_attn_decode_f16d64_k8w2"},
+        {&c->f_dec_merge, "moearc_attn_decode_merge"},
+    };
+    for (auto &f : fns) {
+        if (hipModuleGetFunction(f.slot, c->module, f.name) != hipSuccess) {
+            std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), f.name);
+            hipModuleUnload(c->module);
+            hipStreamDestroy(c->stream);
+            delete c;
+            return nullptr;
+        }
+    }
+    const char *pf[4] = {"moearc_attn_prefill_g1", "moearc_attn_prefill_g2", "moearc_attn_prefill_g4",
+                         "moearc_attn_prefill_g8"};
+    for (int i = 0; i < 4; ++i)
+        if (hipModuleGetFunction(&c->f_prefill[i], c->module, pf[i]) != hipSuccess) c->f_prefill[i] = nullptr;
+    const char *ev = std::getenv("MOEARC_PROFILE_EVENTS");
+    c->profiling = ev && ev[0] == '1';
+    if (const char *w = std::getenv("MOEARC_DECODE_VARIANT")) {
+        for (int i = 0; i < 5; ++i)
+            if (std::strcmp(w, kDecodeVariants[i].name) == 0) c->decode_variant_override = i;
+    }
+    if (const char *s = std::getenv("MOEARC_DECODE_SPLIT")) c->split_override = std::strtoul(s, nullptr, 10);
+    return c;
+}
+
+void moearc_ctx_destroy(moearc_ctx *c) {
+    if (!c) return;
+    hipStreamSynchronize(c->stream);
+    for (auto &p : c->pending) {
+        hipEventDestroy(p.start);
+        hipEventDestroy(p.stop);
+    }
+    for (auto e : c->event_pool) hipEventDestroy(e);
+    if (c->ws) hipFree(c->ws);
+    if (c->module) hipModuleUnload(c->module);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+void *moearc_ctx_stream(moearc_ctx *c) { return c ? (void *) c->stream : nullptr; }
+
+int moearc_profile_events_enabled(moearc_ctx *c) { return (c && c->profiling) ? 1 : 0; }
+
+int moearc_profile_events_reset(moearc_ctx *c) {
+    if (!c) return ERR;
+    flush_events(c);
+    c->totals.clear();
+    return OK;
+}
+
+int moearc_profile_events_report(moearc_ctx *c, char *out, unsigned long cap) {
+    if (!c || !out || cap == 0) return ERR;
+    if (!c->profiling) {
+        out[0] = '\0';
+        return OK;
+    }
+    flush_events(c);
+    unsigned long used = 0;
+    for (const auto &t : c->totals) {
+        char line[160];
+        const int n = std::snprintf(line, sizeof(line), "%s %llu %llu\n", t.key.c_str(), t.ns, t.calls);
+        if (n <= 0 || used + (unsigned long) n + 1 > cap) break;
+        std::memcpy(out + used, line, (size_t) n);
+        used += (unsigned long) n;
+    }
+    out[used] = '\0';
+    return OK;
+}
+
+int moearc_sync(moearc_ctx *c) {
+    if (!c) return ERR;
+    return hipStreamSynchronize(c->stream) == hipSuccess ? OK : ERR;
+}
+
+int moearc_zero(moearc_ctx *c, float *dst, unsigned long n) {
+    if (!c || !dst) return ERR;
+    if (n == 0) return OK;
+    const unsigned grid = (unsigned) std::min<unsigned long>((n + 255) / 256, 65536ul);
+    struct {
+        float *d;
+        uint64_t n;
+    } a{dst, n};
+    return launch(c, c->f_zero, grid, 256, a, "zero", n, 0);
+}
+
+int moearc_device_name(moearc_ctx *c, char *out, unsigned long cap) {
+    if (!c || !out || cap == 0) return ERR;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, c->device) != hipSuccess) return ERR;
+    std::snprintf(out, cap, "%s (%s)", p.name, p.gcnArchName);
+    return OK;
+}
+
+void *moearc_alloc_device(moearc_ctx *c, unsigned long bytes) {
+    if (!c) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) return nullptr;
+    return p;
+}
+
+void moearc_free_device(moearc_ctx *c, void *p) {
+    if (!c || !p) return;
+    hipStreamSynchronize(c->stream);
+    hipFree(p);
+}
+
+int moearc_copy_h2d(moearc_ctx *c, void *dst, const void *src, unsigned long bytes) {
+    if (!c) return ERR;
+    if (bytes == 0) return OK;
+    if (!dst || !src) return ERR;
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess) return ERR;
+    return hipStreamSynchronize(c->stream) == hipSuccess ? OK : ERR;
+}
+
+int moearc_copy_h2d_async(moearc_ctx *c, void *dst, const void *src, unsigned long bytes) {
+    if (!c) return ERR;
+    if (bytes == 0) return OK;
+    if (!dst || !src) return ERR;
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess ? OK : ERR;
+}
+
+int moearc_copy_d2h(moearc_ctx *c, void *dst, const void *src, unsigned long bytes) {
+    if (!c) return ERR;
+    if (bytes == 0) return OK;
+    if (!dst || !src) return ERR;
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return ERR;
+    return hipStreamSynchronize(c->stream) == hipSuccess ? OK : ERR;
+}
+
+int moearc_quantize_f16(moearc_ctx *c, void *dst, const float *src, unsigned long n) {
+    if (!c || !dst || !src) return ERR;
+    if (n == 0) return OK;
+    const unsigned grid = (unsigned) std::min<unsigned long>((n + 255) / 256, 65536ul);
+    struct {
+        void *d;
+        const float *s;
+        uint64_t n;
+    } a{dst, src, n};
+    return launch(c, c->f_quant, grid, 256, a, "quantize_f16", n, 0);
+}
+
+int moearc_kv_append(moearc_ctx *c, void *k_pages, void *v_pages, const float *k, const float *v,
+                     unsigned int page_id, unsigned int slot, unsigned long n_kv_heads,
+                     unsigned long head_dim, unsigned long page_tokens, unsigned int kv_type) {
+    if (!c || !k_pages || !v_pages || !k || !v) return ERR;
+    if (kv_type != 0u && kv_type != 1u) return ERR_ARG;
+    if (page_tokens == 0 || slot >= page_tokens) return ERR_ARG;
+    if (n_kv_heads == 0 || head_dim == 0) return ERR_ARG;
+    const uint64_t row = (uint64_t) n_kv_heads * head_dim;
+    struct {
+        void *kp, *vp;
+        const float *k, *v;
+        uint64_t base, row;
+        uint32_t kv_type;
+    } a{k_pages, v_pages, k, v, ((uint64_t) page_id * page_tokens + slot) * row, row, kv_type};
+    return launch(c, c->f_append, (unsigned) ((row + 255) / 256), 256, a, "kv_append", n_kv_heads,
+                  head_dim);
+}
+
+int moearc_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
+                           const float *v, const unsigned int *page_ids, const unsigned int *slots,
+                           unsigned long n_tok, unsigned long n_kv_heads, unsigned long head_dim,
+                           unsigned long page_tokens, unsigned int kv_type) {
+    if (!c || !k_pages || !v_pages || !k || !v || !page_ids || !slots) return ERR;
+    if (kv_type != 0u && kv_type != 1u) return ERR_ARG;
+    if (page_tokens == 0 || n_kv_heads == 0 || head_dim == 0) return ERR_ARG;
+    if (n_tok == 0) return OK;
+    const uint64_t row = (uint64_t) n_kv_heads * head_dim;
+    const uint64_t total = row * n_tok;
+    if (total / 256 >= 0xFFFFFFFFull) return ERR_ARG;
+    struct {
+        void *kp, *vp;
+        const float *k, *v;
+        const uint32_t *pages, *slots;
+        uint64_t n_tok, row, pt;
+        uint32_t kv_type;
+    } a{k_pages, v_pages, k, v, page_ids, slots, n_tok, row, page_tokens, kv_type};
+    return launch(c, c->f_append_chunk, (unsigned) ((total + 255) / 256), 256, a, "kv_append_chunk",
+                  n_kv_heads, head_dim);
+}
+
+int moearc_attn_decode(moearc_ctx *c, float *out, const float *q, const void *k_pages,
+                       const void *v_pages, const unsigned int *block_table, const float *sinks,
+                       unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
+                       unsigned long kv_begin, unsigned long n_kv, unsigned long page_tokens,
+                       float scale, unsigned int kv_type) {
+    // Validation order of kernels.cpp:1842-1852.
+    if (!c || !out || !q || !k_pages || !v_pages || !block_table) return ERR;
+    if (kv_type != 0u && kv_type != 1u) return ERR_ARG;
+    if (n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_kv == 0 || page_tokens == 0)
+        return ERR_ARG;
+    if (n_heads % n_kv_heads != 0) return ERR_ARG;
+    if (kv_begin >= n_kv) return ERR_ARG;
+    if (head_dim > 1024) return ERR_ARG;
+    if (n_kv > 0xFFFFFFFFul) return ERR_ARG;  // keys are indexed in 32 bits on the device
+    std::vector<SeqSpan> spans{SeqSpan{(uint32_t) kv_begin, (uint32_t) n_kv}};
+    const unsigned long bt_stride = (n_kv + page_tokens - 1) / page_tokens;
+    return decode_launch(c, out, 0u, q, k_pages, v_pages, block_table, bt_stride, spans, sinks,
+                         n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type);
+}
+
+int moearc_attn_decode_batched(moearc_ctx *c, void *out, unsigned int out_type, const float *q,
+                               const void *k_pages, const void *v_pages,
+                               const unsigned int *block_tables, unsigned long bt_stride,
+                               const unsigned int *kv_begin, const unsigned int *n_kv,
+                               const float *sinks, unsigned long n_seqs, unsigned long n_heads,
+                               unsigned long n_kv_heads, unsigned long head_dim,
+                               unsigned long page_tokens, float scale, unsigned int kv_type) {
+    if (!c || !out || !q || !k_pages || !v_pages || !block_tables || !kv_begin || !n_kv) return ERR;
+    if (kv_type != 0u && kv_type != 1u) return ERR_ARG;
+    if (out_type != MOEARC_OUT_F32 && out_type != MOEARC_OUT_F16) return ERR_ARG;
+    if (n_seqs == 0 || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || page_tokens == 0)
+        return ERR_ARG;
+    if (n_heads % n_kv_heads != 0) return ERR_ARG;
+    if (head_dim > 1024) return ERR_ARG;
+    std::vector<SeqSpan> spans(n_seqs);
+    for (unsigned long b = 0; b < n_seqs; ++b) {
+        if (n_kv[b] == 0 || kv_begin[b] >= n_kv[b]) return ERR_ARG;
+        if ((n_kv[b] + page_tokens - 1) / page_tokens > bt_stride) return ERR_ARG;
+        spans[b] = SeqSpan{kv_begin[b], n_kv[b]};
+    }
+    return decode_launch(c, out, out_type, q, k_pages, v_pages, block_tables, bt_stride, spans,
+                         sinks, n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type);
+}
+
+int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const void *q,
+                        const void *k_pages, const void *v_pages, const unsigned int *block_table,
+                        const float *sinks, unsigned long n_q, unsigned long pos0,
+                        unsigned long n_swa, unsigned long n_heads, unsigned long n_kv_heads,
+                        unsigned long head_dim, unsigned long page_tokens, float scale,
+                        unsigned int kv_type) {
+    if (!c || !out || !q || !k_pages || !v_pages || !block_table) return ERR;
+    if (kv_type != 1u) return ERR_ARG;
+    if (out_type != MOEARC_OUT_F32 && out_type != MOEARC_OUT_F16) return ERR_ARG;
+    if (n_q == 0 || n_heads == 0 || n_kv_heads == 0 || head_dim != 64 || !is_pow2(page_tokens))
+        return ERR_ARG;
+    if (n_heads % n_kv_heads != 0) return ERR_ARG;
+    const unsigned long group = n_heads / n_kv_heads;
+    if (group != 1 && group != 2 && group != 4 && group != 8) return ERR_ARG;
+    if (pos0 + n_q > 0xFFFFFFFFul) return ERR_ARG;
+    const int gi = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : 3;
+    if (!c->f_prefill[gi]) return ERR;
+    PrefillArgs a{};
+    a.q = (const uint16_t *) q;
+    a.k_pages = (const uint16_t *) k_pages;
+    a.v_pages = (const uint16_t *) v_pages;
+    a.block_table = block_table;
+    a.sinks = sinks;
+    a.out = out;
+    a.n_q = (uint32_t) n_q;
+    a.pos0 = (uint32_t) pos0;
+    a.n_swa = (uint32_t) std::min<unsigned long>(n_swa, 0xFFFFFFFFul);
+    a.n_heads = (uint32_t) n_heads;
+    a.n_kv_heads = (uint32_t) n_kv_heads;
+    a.group = (uint32_t) group;
+    a.pt_shift = log2u(page_tokens);
+    a.out_f16 = out_type;
+    a.scale_log2e = scale * 1.4426950408889634f;
+    const uint32_t rows_per_tile = MOEARC_PREFILL_ROWS;  // query rows (token x head) per work-group
+    const uint64_t rows = (uint64_t) n_q * group;
+    a.n_qtiles = (uint32_t) ((rows + rows_per_tile - 1) / rows_per_tile);
+    const uint64_t wgs = (uint64_t) a.n_qtiles * n_kv_heads;
+    if (wgs > 0x7FFFFFFFull) return ERR_ARG;
+    return launch(c, c->f_prefill[gi], (unsigned) wgs, MOEARC_PREFILL_THREADS, a, "attn_prefill",
+                  n_heads, head_dim);
+}
+
+}  // extern "C"

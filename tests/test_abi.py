@@ -1,0 +1,71 @@
+"""The C ABI library loads and exports every symbol include/moearc_attn.h declares (CPU only).
+
+No compute call is made: only entry points refused on the host before any device work (a null
+context returns -1, the reference's null-argument code) are called.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from moearc_amd import native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "moearc_attn.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(moearc_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_reference_surface():
+    names = declared_symbols()
+    # the attention + lifecycle subset of crates/moearc-kernels/src/ffi.rs:20-234
+    for n in ("moearc_ctx_create", "moearc_ctx_destroy", "moearc_profile_events_enabled",
+              "moearc_profile_events_reset", "moearc_profile_events_report", "moearc_sync",
+              "moearc_zero", "moearc_device_name", "moearc_alloc_device", "moearc_free_device",
+              "moearc_copy_h2d", "moearc_copy_h2d_async", "moearc_copy_d2h",
+              "moearc_quantize_f16", "moearc_kv_append", "moearc_attn_decode"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = native.load()
+    for n in declared_symbols():
+        assert hasattr(lib, n), f"{n} is declared but not exported"
+        assert n in native.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_code_object_holds_every_kernel_the_runtime_loads():
+    blob = open(native.CODE_OBJECT, "rb").read()
+    src = open(os.path.join(ROOT, "moearc_amd", "csrc", "runtime.cpp")).read()
+    kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge|moearc_attn_prefill_g\d)"', src))
+    assert kernels
+    for k in kernels:
+        assert k.encode() in blob, f"kernel {k} missing from the code object"
+
+
+def test_null_context_is_refused_with_minus_one():
+    lib = native.load()
+    assert lib.moearc_sync(None) == -1
+    assert lib.moearc_profile_events_reset(None) == -1
+    assert lib.moearc_profile_events_enabled(None) == 0
+    assert lib.moearc_attn_decode(None, None, None, None, None, None, None, 64, 8, 64, 0, 10, 32,
+                                  ctypes.c_float(0.125), 1) == -1
+    assert lib.moearc_kv_append(None, None, None, None, None, 0, 0, 8, 64, 32, 1) == -1
+    assert lib.moearc_attn_prefill(None, None, 0, None, None, None, None, None, 8, 0, 0, 64, 8,
+                                   64, 32, ctypes.c_float(0.125), 1) == -1
+    assert lib.moearc_alloc_device(None, 16) is None
+    assert lib.moearc_copy_h2d(None, None, None, 0) == -1
+    assert lib.moearc_quantize_f16(None, None, None, 4) == -1
+
+
+def test_missing_build_fails_loudly(monkeypatch):
+    monkeypatch.setattr(native, "_lib", None)
+    monkeypatch.setattr(native, "LIBRARY", "/nonexistent/libmoearc_attn.so")
+    with pytest.raises(native.NativeLibraryMissing):
+        native.load()
