@@ -3,3 +3,4 @@
 #include "kernels_misc.hip"
 #include "decode_general.hip"
 #include "decode_splitk.hip"
+#include "prefill.hip"

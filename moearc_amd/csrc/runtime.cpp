@@ -595,6 +595,13 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     a.pt_shift = log2u(page_tokens);
     a.out_f16 = out_type;
     a.scale_log2e = scale * 1.4426950408889634f;
+    // Each work-group stages the block-table entries of its key span in LDS (PF_PT_CAP = 2048).
+    {
+        const unsigned long tok = MOEARC_PREFILL_ROWS / group;
+        const unsigned long full = (pos0 + n_q - 1) / page_tokens + 1;
+        const unsigned long win = n_swa ? (tok + n_swa + 64) / page_tokens + 2 : full;
+        if (std::min(full, win) > 2048ul) return ERR_ARG;
+    }
     const uint32_t rows_per_tile = MOEARC_PREFILL_ROWS;  // query rows (token x head) per work-group
     const uint64_t rows = (uint64_t) n_q * group;
     a.n_qtiles = (uint32_t) ((rows + rows_per_tile - 1) / rows_per_tile);

@@ -1,0 +1,104 @@
+"""Chunked-prefill parity on the GPU against the oracle (row i == decode at n_kv = pos0+i+1).
+
+Golden fixtures pin a small gpt-oss-shaped chunk; the oracle covers every GQA group the kernel
+supports, windowed and full layers, ragged chunk ends and page sizes; at BASELINE config 4's full
+size (2048 new tokens after 2048 cached) rows are sampled for the oracle and every row is checked
+for finiteness. The bar is the north star's: max-abs error <= 2e-3 on the output.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import fixtures as fx
+from moearc_amd import BadArgument, KvType, OUT_F16, OUT_F32
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _report(label, got, want, tol=TOL):
+    err = float(np.nanmax(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))))
+    print(f"{label}: max |gpu - oracle| = {err:.3e} (tolerance {tol:.3e})", flush=True)
+    assert err <= tol, f"{label}: {err:.3e} > {tol:.3e}"
+
+
+def _run(ctx, pc, n_swa, out_type=OUT_F32, sinks=True):
+    dk, dv, dbt = ctx.upload(pc.k_raw), ctx.upload(pc.v_raw), ctx.upload(pc.bt)
+    ds = ctx.upload(pc.sinks) if sinks else None
+    dq = ctx.upload(np.ascontiguousarray(pc.qp).view(np.uint16))
+    nb = 2 if out_type == OUT_F16 else 4
+    dout = ctx.alloc(pc.n_q * pc.H * pc.D * nb)
+    ctx.attn_prefill(dout, dq, dk, dv, dbt, ds, pc.n_q, pc.pos0, n_swa, pc.H, pc.G, pc.D, pc.pt,
+                     float(pc.scale), KvType.F16, out_type=out_type)
+    return ctx.download(dout, np.float16 if out_type == OUT_F16 else np.float32,
+                        (pc.n_q, pc.H, pc.D)).astype(np.float32)
+
+
+@pytest.mark.parametrize("golden,n_swa", [("ns_prefill_full", 0), ("ns_prefill_swa16", 16)])
+def test_against_golden(ctx, golden, n_swa):
+    pc = fx.prefill_case(0x9F11, n_q=48, pos0=80)
+    g = fx.load_golden(golden)
+    assert str(g["digest"]) == fx.prefill_digest(pc)
+    got = _run(ctx, pc, n_swa)
+    _report(f"prefill {golden}", got[g["rows"]], g["expected"])
+
+
+@pytest.mark.parametrize("group,n_q,pos0,pt,n_swa", [
+    (8, 100, 37, 32, 0), (8, 100, 37, 32, 128), (8, 17, 0, 16, 0), (8, 70, 300, 64, 5),
+    (4, 90, 11, 32, 0), (2, 40, 64, 8, 33), (1, 150, 9, 32, 0), (1, 150, 9, 32, 64),
+])
+def test_shapes_against_oracle(ctx, group, n_q, pos0, pt, n_swa):
+    G = 8 if group > 1 else 4
+    pc = fx.prefill_case(0x700 + n_q + pos0 + group, n_q=n_q, pos0=pos0, pt=pt, H=G * group, G=G)
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, n_q, pos0, n_swa,
+                               pc.H, pc.G, pc.D, pt, float(pc.scale), sinks=pc.sinks, n_threads=8)
+    got = _run(ctx, pc, n_swa)
+    _report(f"prefill group={group} n_q={n_q} pos0={pos0} pt={pt} n_swa={n_swa}", got, want)
+    nosink = _run(ctx, pc, n_swa, sinks=False)
+    want_ns = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, n_q, pos0,
+                                  n_swa, pc.H, pc.G, pc.D, pt, float(pc.scale), n_threads=8)
+    _report("  without sinks", nosink, want_ns)
+
+
+def test_rows_equal_decode_calls(ctx):
+    # the defining property: row i == moearc_attn_decode at n_kv = pos0 + i + 1 (f16 q widened)
+    pc = fx.prefill_case(0x3D, n_q=40, pos0=200, pt=32)
+    got = _run(ctx, pc, 128)
+    dk, dv, dbt, ds = ctx.upload(pc.k_raw), ctx.upload(pc.v_raw), ctx.upload(pc.bt), ctx.upload(pc.sinks)
+    dq, dout = ctx.alloc(pc.H * pc.D * 4), ctx.alloc(pc.H * pc.D * 4)
+    for i in (0, 13, 39):
+        n_kv = pc.pos0 + i + 1
+        ctx.upload_slice(dq, pc.qp[i].astype(np.float32))
+        ctx.attn_decode_ext(dout, dq, dk, dv, dbt, ds, pc.H, pc.G, pc.D, max(0, n_kv - 128), n_kv,
+                            pc.pt, float(pc.scale), KvType.F16)
+        dec = ctx.download(dout, np.float32, (pc.H, pc.D))
+        _report(f"  prefill row {i} vs decode", got[i], dec, 1e-5)
+
+
+@pytest.mark.parametrize("n_swa", [0, 128])
+def test_config4_full_size(ctx, n_swa):
+    # 2048 new tokens after 2048 cached, 64q/8kv, d64, f16, sinks
+    pc = fx.prefill_case(0xC4, n_q=2048, pos0=2048, pt=256)
+    for out_type in (OUT_F32, OUT_F16):
+        got = _run(ctx, pc, n_swa, out_type=out_type)
+        assert np.isfinite(got).all()
+        want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q,
+                                   pc.pos0, n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale),
+                                   sinks=pc.sinks, rows=(3, 2048, 97), n_threads=8)
+        rows = np.arange(3, 2048, 97)
+        _report(f"config 4 n_swa={n_swa} out={'f16' if out_type else 'f32'} ({rows.size} rows)",
+                got[rows], want[rows])
+
+
+def test_refusals(ctx):
+    buf, bt = ctx.alloc(1 << 16), ctx.alloc(64)
+    with pytest.raises(BadArgument):  # head_dim 128 is not the prefill kernel's
+        ctx.attn_prefill(buf, buf, buf, buf, bt, None, 4, 0, 0, 8, 8, 128, 32, 0.1, KvType.F16)
+    with pytest.raises(BadArgument):  # group 3
+        ctx.attn_prefill(buf, buf, buf, buf, bt, None, 4, 0, 0, 6, 2, 64, 32, 0.1, KvType.F16)
+    with pytest.raises(BadArgument):  # f32 KV
+        ctx.attn_prefill(buf, buf, buf, buf, bt, None, 4, 0, 0, 8, 8, 64, 32, 0.1, KvType.F32)
+    ctx.sync()
