@@ -1,0 +1,390 @@
+"""Benchmark of the attention hot path on one MI355X; prints one JSON line.
+
+Workload (the config the metric is quoted on): single-sequence decode,
+B=1, 32768 keys, 64 query heads over 8 KV heads, head_dim 64, f16 KV in 256-token pages through a
+random page permutation, per-head f32 sinks, full causal, f16 output. A step is one attention layer
+call. Inputs are N(0,1) from a seed (synthetic data; there is no model).
+
+* Timed region: K steps captured in one HIP graph on the library's stream and replayed once,
+  bracketed by stream synchronisations; every step reads a different one of 6 KV copies (384 MiB)
+  so the 256 MB Infinity Cache cannot serve repeats. value = algorithmic bytes per step / step time.
+* roofline: the dominant kernel (the split-K kernel) timed with HIP events on the library stream
+  over K eager steps; achieved = algorithmic bytes per launch / its average duration, against
+  8 TB/s. traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+  summary (profiles/decode_c2_pmc.md), when present.
+* prefill: BASELINE config 4 (2048 new + 2048 cached tokens), full causal and SWA-128, MFMA
+  utilisation = algorithmic flops / time / 2.5 PFLOP/s (dense f16).
+* cpu_baseline: the CPU oracle (a C restatement of the reference's f64 CPU twin,
+  reference.rs:821-873, plus the sink) timed on this host on a bounded sample of the same decode.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
+H, G, D, PT = 64, 8, 64, 256
+N_KV = 32768
+COPIES = 6
+
+# algorithmic bytes per C2 step: K + V (f16) + q (f32) + sinks (f32) + out (f16)
+C2_BYTES = 2 * N_KV * G * D * 2 + H * D * 4 + H * 4 + H * D * 2
+# config 4: 2048 new tokens after 2048 cached
+PF_NQ, PF_POS0 = 2048, 2048
+PF_PAIRS_FULL = sum(PF_POS0 + i + 1 for i in range(PF_NQ))
+PF_FLOPS_FULL = PF_PAIRS_FULL * H * D * 4           # QK^T and PV, 2 flops per MAC
+PF_FLOPS_SWA = PF_NQ * 128 * H * D * 4
+PF_BYTES_SWA = PF_NQ * H * D * 2 + (PF_POS0 + PF_NQ - (PF_POS0 - 127)) * G * D * 2 * 2 + \
+    PF_NQ * H * D * 2 + H * 4
+
+
+class Hip:
+    """The few HIP runtime calls the timing needs (graph capture and events), via ctypes."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipGetErrorString.restype = ctypes.c_char_p
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.lib.hipGetErrorString(rc).decode()}")
+
+    def event(self):
+        e = ctypes.c_void_p()
+        self.ok(self.lib.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e
+
+    def record(self, e, stream):
+        self.ok(self.lib.hipEventRecord(e, ctypes.c_void_p(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, e0, e1):
+        self.ok(self.lib.hipEventSynchronize(e1), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self.ok(self.lib.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
+        return ms.value
+
+    def capture(self, stream, fn):
+        """Capture fn()'s work on `stream` into an executable graph."""
+        s = ctypes.c_void_p(stream)
+        self.ok(self.lib.hipStreamBeginCapture(s, 1), "hipStreamBeginCapture")  # thread-local mode
+        try:
+            fn()
+        finally:
+            graph = ctypes.c_void_p()
+            rc = self.lib.hipStreamEndCapture(s, ctypes.byref(graph))
+        self.ok(rc, "hipStreamEndCapture")
+        exe = ctypes.c_void_p()
+        self.ok(self.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)),
+                "hipGraphInstantiate")
+        return graph, exe
+
+    def launch(self, exe, stream):
+        self.ok(self.lib.hipGraphLaunch(exe, ctypes.c_void_p(stream)), "hipGraphLaunch")
+
+    def destroy(self, graph, exe):
+        self.lib.hipGraphExecDestroy(exe)
+        self.lib.hipGraphDestroy(graph)
+
+
+def decode_inputs(seed=0xC2):
+    from moearc_amd import synth
+    row = G * D
+    pages = N_KV // PT
+    k = synth.f16_bits(synth.normal(seed, N_KV * row))
+    v = synth.f16_bits(synth.normal(seed + 1, N_KV * row))
+    bt = synth.random_block_table(seed + 5, pages)
+    # scatter logical keys into their physical pages
+    kp = np.empty_like(k).reshape(pages, PT, row)
+    vp = np.empty_like(v).reshape(pages, PT, row)
+    kp[bt] = k.reshape(pages, PT, row)
+    vp[bt] = v.reshape(pages, PT, row)
+    q = synth.normal(seed + 3, H * D)
+    sinks = synth.normal(seed + 4, H)
+    return kp.ravel(), vp.ravel(), bt, q, sinks
+
+
+def pmc_traffic(path):
+    """HBM bytes per launch of the split kernel from the committed rocprofv3 summary."""
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split()[1])
+    return vals or None
+
+
+def run(steps, warmup, skip_cpu=False, skip_prefill=False):
+    from moearc_amd import Context, KvType, OUT_F16
+
+    hip = Hip()
+    kp, vp, bt, q, sinks = decode_inputs()
+    result = {}
+
+    with Context() as ctx:
+        stream = ctx.stream
+        dks = [ctx.upload(kp) for _ in range(COPIES)]
+        dvs = [ctx.upload(vp) for _ in range(COPIES)]
+        dq, dbt, ds = ctx.upload(q), ctx.upload(bt), ctx.upload(sinks)
+        dout = ctx.alloc(H * D * 2)
+        kb, nk = np.zeros(1, np.uint32), np.full(1, N_KV, np.uint32)
+
+        def step(i):
+            ctx.attn_decode_batched(dout, dq, dks[i % COPIES], dvs[i % COPIES], dbt, N_KV // PT, kb,
+                                    nk, ds, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+
+        for i in range(warmup):
+            step(i)
+        ctx.sync()
+        eager_out = ctx.download(dout, np.float16, (H, D)).astype(np.float32)
+        graph, exe = hip.capture(stream, lambda: [step(i) for i in range(steps)])
+        e0, e1 = hip.event(), hip.event()
+        hip.launch(exe, stream)  # one untimed replay
+        ctx.sync()
+        ctx.sync()
+        t0 = time.perf_counter()
+        hip.record(e0, stream)
+        hip.launch(exe, stream)
+        hip.record(e1, stream)
+        ctx.sync()
+        t1 = time.perf_counter()
+        gpu_ms = hip.elapsed_ms(e0, e1)
+        hip.destroy(graph, exe)
+        graph_out = ctx.download(dout, np.float16, (H, D)).astype(np.float32)
+        wall_ms = (t1 - t0) * 1e3
+        result["step_us_gpu"] = gpu_ms * 1e3 / steps
+        result["step_us_wall"] = wall_ms * 1e3 / steps
+        result["graph_equals_eager"] = bool(np.array_equal(graph_out, eager_out))
+        result["out"] = graph_out
+
+    # per-kernel event timing (eager, profiling context)
+    os.environ["MOEARC_PROFILE_EVENTS"] = "1"
+    try:
+        with Context() as ctx:
+            dks = [ctx.upload(kp) for _ in range(COPIES)]
+            dvs = [ctx.upload(vp) for _ in range(COPIES)]
+            dq, dbt, ds = ctx.upload(q), ctx.upload(bt), ctx.upload(sinks)
+            dout = ctx.alloc(H * D * 2)
+            kb, nk = np.zeros(1, np.uint32), np.full(1, N_KV, np.uint32)
+            for i in range(warmup + steps):
+                if i == warmup:
+                    ctx.sync()
+                    ctx.profile_events_reset()
+                ctx.attn_decode_batched(dout, dq, dks[i % COPIES], dvs[i % COPIES], dbt, N_KV // PT,
+                                        kb, nk, ds, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+            ctx.sync()
+            rep = ctx.profile_events_report()
+            result["events"] = {k: v[0] / v[1] / 1e3 for k, v in rep.items()}
+
+            if not skip_prefill:
+                result["prefill"] = bench_prefill(ctx, steps=max(5, steps // 5), warmup=3)
+    finally:
+        os.environ.pop("MOEARC_PROFILE_EVENTS", None)
+
+    if not skip_cpu:
+        result["cpu"] = cpu_baseline(kp, vp, bt, q, sinks)
+    return result
+
+
+def bench_prefill(ctx, steps, warmup):
+    import fixtures as fx  # tests/fixtures.py: the same seeded prefill inputs the parity tests use
+    from moearc_amd import KvType, OUT_F16
+    pc = fx.prefill_case(0xC4, n_q=PF_NQ, pos0=PF_POS0, pt=PT)
+    copies = 4
+    dks = [ctx.upload(pc.k_raw) for _ in range(copies)]
+    dvs = [ctx.upload(pc.v_raw) for _ in range(copies)]
+    dqs = [ctx.upload(np.ascontiguousarray(pc.qp).view(np.uint16)) for _ in range(copies)]
+    dbt, ds = ctx.upload(pc.bt), ctx.upload(pc.sinks)
+    dout = ctx.alloc(PF_NQ * H * D * 2)
+    out = {}
+    for name, n_swa in (("full", 0), ("swa128", 128)):
+        for i in range(warmup + steps):
+            if i == warmup:
+                ctx.sync()
+                ctx.profile_events_reset()
+            ctx.attn_prefill(dout, dqs[i % copies], dks[i % copies], dvs[i % copies], dbt, ds, PF_NQ,
+                             PF_POS0, n_swa, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+        ctx.sync()
+        rep = ctx.profile_events_report()
+        us = rep["attn_prefill r64 m64"][0] / rep["attn_prefill r64 m64"][1] / 1e3
+        flops = PF_FLOPS_FULL if n_swa == 0 else PF_FLOPS_SWA
+        tflops = flops / us / 1e6
+        entry = {"us": round(us, 2), "tflops": round(tflops, 1),
+                 "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                 "tokens_per_s": round(PF_NQ * 1e6 / us, 0)}
+        if n_swa:
+            gbs = PF_BYTES_SWA / us / 1e3
+            bound_us = max(PF_BYTES_SWA / (HBM_PEAK_GBS * 1e3), flops / (MFMA_F16_PEAK_TFLOPS * 1e6))
+            entry.update({"hbm_gbs": round(gbs, 0), "roofline_frac": round(bound_us / us, 4)})
+        out[name] = entry
+    return out
+
+
+def cpu_baseline(kp, vp, bt, q, sinks):
+    """The oracle (f64, two-pass, sequential heads: the reference's CPU twin) on this host."""
+    from oracle import oracle
+    oracle.lib()
+    bt1 = np.ascontiguousarray(bt, np.uint32)
+    t0 = time.perf_counter()
+    n = 0
+    while True:  # single thread, as the reference runs it; a bounded ~10 s sample
+        oracle.attn_decode(q, kp, vp, bt1, H, G, D, 0, N_KV, PT, 0.125, kv_type=1, sinks=sinks)
+        n += 1
+        if time.perf_counter() - t0 > 10.0 or n >= 40:
+            break
+    st_s = (time.perf_counter() - t0) / n
+    threads = min(16, os.cpu_count() or 1)
+    qb = q.reshape(1, H, D)
+    kb, nk = np.zeros(1, np.uint32), np.full(1, N_KV, np.uint32)
+    t0 = time.perf_counter()
+    m = 0
+    while True:
+        oracle.attn_decode_batched(qb, kp, vp, bt1.reshape(1, -1), kb, nk, H, G, D, PT, 0.125,
+                                   sinks=sinks, n_threads=threads)
+        m += 1
+        if time.perf_counter() - t0 > 5.0 or m >= 200:
+            break
+    mt_s = (time.perf_counter() - t0) / m
+    return {"single_us": st_s * 1e6, "single_calls": n, "mt_us": mt_s * 1e6, "mt_calls": m,
+            "threads": threads}
+
+
+def only(what, steps, warmup):
+    """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
+    decode (C2), prefill (C4 full then SWA-128), or copy (a 256 MiB device-to-device copy, the
+    reference size for scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
+    from moearc_amd import Context, KvType, OUT_F16
+    with Context() as ctx:
+        if what == "decode":
+            kp, vp, bt, q, sinks = decode_inputs()
+            dks = [ctx.upload(kp) for _ in range(COPIES)]
+            dvs = [ctx.upload(vp) for _ in range(COPIES)]
+            dq, dbt, ds = ctx.upload(q), ctx.upload(bt), ctx.upload(sinks)
+            dout = ctx.alloc(H * D * 2)
+            kb, nk = np.zeros(1, np.uint32), np.full(1, N_KV, np.uint32)
+            for i in range(warmup + steps):
+                ctx.attn_decode_batched(dout, dq, dks[i % COPIES], dvs[i % COPIES], dbt, N_KV // PT,
+                                        kb, nk, ds, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+        elif what == "prefill":
+            import fixtures as fx
+            pc = fx.prefill_case(0xC4, n_q=PF_NQ, pos0=PF_POS0, pt=PT)
+            dk, dv, dbt, ds = ctx.upload(pc.k_raw), ctx.upload(pc.v_raw), ctx.upload(pc.bt), ctx.upload(pc.sinks)
+            dq = ctx.upload(np.ascontiguousarray(pc.qp).view(np.uint16))
+            dout = ctx.alloc(PF_NQ * H * D * 2)
+            for n_swa in (0, 128):
+                for i in range(warmup + steps):
+                    ctx.attn_prefill(dout, dq, dk, dv, dbt, ds, PF_NQ, PF_POS0, n_swa, H, G, D, PT,
+                                     0.125, KvType.F16, out_type=OUT_F16)
+        elif what == "copy":
+            hip = Hip()
+            n = 256 << 20
+            src, dst = ctx.alloc(n), ctx.alloc(n)
+            ctx.zero(src, n // 4)
+            for i in range(warmup + steps):
+                hip.ok(hip.lib.hipMemcpyDtoDAsync(ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr),
+                                                  ctypes.c_size_t(n), ctypes.c_void_p(ctx.stream)),
+                       "hipMemcpyDtoDAsync")
+        ctx.sync()
+    print(f"ran {what}: {warmup + steps} launches", flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--only", choices=["decode", "prefill", "copy"],
+                    help="run one workload without timing, for rocprofv3 to wrap")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
+              f"{args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("RANK", "0")) != 0:
+        return
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    if args.only:
+        only(args.only, args.steps, args.warmup)
+        return
+    r = run(args.steps, args.warmup, args.skip_cpu, args.skip_prefill)
+
+    step_us = r["step_us_gpu"]
+    gbs = C2_BYTES / step_us / 1e3
+    split_us = r["events"].get("attn_decode.split r64 m64")
+    ach = C2_BYTES / split_us / 1e3 if split_us else None
+    # parity spot check against the oracle (f64) on the same inputs
+    from oracle import oracle
+    kp, vp, bt, q, sinks = decode_inputs()
+    want = oracle.attn_decode(q, kp, vp, bt, H, G, D, 0, N_KV, PT, 0.125, kv_type=1, sinks=sinks)
+    err = float(np.max(np.abs(r["out"].ravel() - want)))
+    traffic = pmc_traffic(os.path.join(ROOT, "profiles", "decode_c2_pmc.md"))
+    line = {
+        "metric": "decode attn µs/layer + HBM GB/s (% peak) at B=1, 32K ctx; prefill MFMA util",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) q/K/V, f16 KV; no model)",
+        "config": {
+            "workload": "C2 decode: B=1, 32768 keys, 64q/8kv heads, head_dim 64, f16 KV in 256-token "
+                        "pages (random permutation), per-head f32 sinks, full causal, f16 out",
+            "global_batch": 1, "seq_len": N_KV, "parallelism": "single GPU",
+        },
+        "us_per_layer": round(step_us, 2),
+        "us_per_layer_wall": round(r["step_us_wall"], 2),
+        "pct_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "tokens_per_s": round(1e6 / step_us, 0),
+        "kernel_us": {k: round(v, 2) for k, v in r["events"].items()},
+        "graph_replay_equals_eager": r["graph_equals_eager"],
+        "parity_max_abs_err": err,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(ach, 1) if ach else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4) if ach else None,
+            "traffic": traffic,
+            "kernel": "moearc_attn_decode_f16d64 (split-K)",
+            "bytes_per_launch": C2_BYTES,
+        },
+    }
+    if "prefill" in r:
+        line["prefill"] = r["prefill"]
+    if "cpu" in r:
+        c = r["cpu"]
+        line["cpu_baseline"] = {
+            "value": round(C2_BYTES / c["single_us"] / 1e3, 3),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"C2 decode, {c['single_calls']} calls of the f64 oracle, one thread "
+                      f"({c['single_us'] / 1e3:.1f} ms/call)",
+            "multithread": {"threads": c["threads"], "us_per_call": round(c["mt_us"], 1),
+                            "value": round(C2_BYTES / c["mt_us"] / 1e3, 3)},
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

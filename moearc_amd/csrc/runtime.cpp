@@ -73,7 +73,6 @@ struct moearc_ctx {
     std::vector<Pending> pending;
     std::vector<KernelTime> totals;
     std::vector<hipEvent_t> event_pool;
-    hipEvent_t open_start = nullptr;  // start event of a bracket spanning two launches
     // split-K workspace: one partial record per work-group of the split kernel
     float *ws = nullptr;
     size_t ws_floats = 0;
@@ -116,33 +115,31 @@ void flush_events(moearc_ctx *c) {
     c->pending.clear();
 }
 
-// Launch `f` with one by-value argument block. With profiling on, a HIP event pair brackets
-// the work under one key: phase 0 brackets this launch alone; phase 1 opens a bracket that the
-// next launch, with phase 2, closes (an attention call that is two kernels is timed as one).
+void record_bracket(moearc_ctx *c, hipEvent_t start, const char *what, unsigned long r,
+                    unsigned long m) {
+    hipEvent_t e1 = take_event(c);
+    if (!e1) return;
+    hipEventRecord(e1, c->stream);
+    char key[96];
+    std::snprintf(key, sizeof(key), "%s r%lu m%lu", what, r, m);
+    c->pending.push_back(Pending{key, start, e1});
+    if (c->pending.size() >= 16384) flush_events(c);
+}
+
+// Launch `f` with one by-value argument block. With profiling on, a HIP event pair brackets the
+// launch under the key "<what> r<r> m<m>" (the reference's key format, kernels.cpp:1905-1916).
 template <typename Args>
 int launch(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned block, const Args &args,
-           const char *what, unsigned long r, unsigned long m, int phase = 0) {
+           const char *what, unsigned long r, unsigned long m) {
     if (!f) return ERR;
-    if (c->profiling && phase != 2) {
-        c->open_start = take_event(c);
-        if (c->open_start) hipEventRecord(c->open_start, c->stream);
-    }
+    hipEvent_t e0 = nullptr;
+    if (c->profiling && (e0 = take_event(c))) hipEventRecord(e0, c->stream);
     size_t size = sizeof(Args);
     void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *) &args, HIP_LAUNCH_PARAM_BUFFER_SIZE,
                       &size, HIP_LAUNCH_PARAM_END};
     const hipError_t err =
         hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, c->stream, nullptr, config);
-    if (c->profiling && phase != 1 && c->open_start) {
-        hipEvent_t e1 = take_event(c);
-        if (e1) {
-            hipEventRecord(e1, c->stream);
-            char key[96];
-            std::snprintf(key, sizeof(key), "%s r%lu m%lu", what, r, m);
-            c->pending.push_back(Pending{key, c->open_start, e1});
-            if (c->pending.size() >= 16384) flush_events(c);
-        }
-        c->open_start = nullptr;
-    }
+    if (e0) record_bracket(c, e0, what, r, m);
     return err == hipSuccess ? OK : ERR;
 }
 
@@ -208,6 +205,13 @@ bool plan_split(moearc_ctx *c, const std::vector<SeqSpan> &spans, unsigned long 
     return true;
 }
 
+int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
+                       const void *k_pages, const void *v_pages, const unsigned int *block_tables,
+                       unsigned long bt_stride, const std::vector<SeqSpan> &spans,
+                       const float *sinks, unsigned long n_heads, unsigned long n_kv_heads,
+                       unsigned long head_dim, unsigned long page_tokens, float scale,
+                       unsigned int kv_type, size_t nseq, size_t per);
+
 int decode_launch(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
                   const void *k_pages, const void *v_pages, const unsigned int *block_tables,
                   unsigned long bt_stride, const std::vector<SeqSpan> &spans, const float *sinks,
@@ -215,6 +219,23 @@ int decode_launch(moearc_ctx *c, void *out, unsigned int out_f16, const float *q
                   unsigned long page_tokens, float scale, unsigned int kv_type) {
     const size_t nseq = spans.size();
     const size_t per = MOEARC_MAX_SEQS_PER_LAUNCH;
+    // With profiling on, the whole call is one bracket under the reference's key; the kernels it
+    // launches are also timed under their own keys.
+    hipEvent_t call0 = nullptr;
+    if (c->profiling && (call0 = take_event(c))) hipEventRecord(call0, c->stream);
+    const int rc_all = decode_launch_body(c, out, out_f16, q, k_pages, v_pages, block_tables,
+                                          bt_stride, spans, sinks, n_heads, n_kv_heads, head_dim,
+                                          page_tokens, scale, kv_type, nseq, per);
+    if (call0) record_bracket(c, call0, "attn_decode", n_heads, head_dim);
+    return rc_all;
+}
+
+int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
+                       const void *k_pages, const void *v_pages, const unsigned int *block_tables,
+                       unsigned long bt_stride, const std::vector<SeqSpan> &spans,
+                       const float *sinks, unsigned long n_heads, unsigned long n_kv_heads,
+                       unsigned long head_dim, unsigned long page_tokens, float scale,
+                       unsigned int kv_type, size_t nseq, size_t per) {
     const bool fast_shape = fast_decode_ok(n_heads, n_kv_heads, head_dim, page_tokens, kv_type);
     for (size_t s0 = 0; s0 < nseq; s0 += per) {
         const size_t cnt = std::min(per, nseq - s0);
@@ -248,7 +269,7 @@ int decode_launch(moearc_ctx *c, void *out, unsigned int out_f16, const float *q
                 a.n_kv[i] = spans[s0 + i].end;
             }
             const int rc = launch(c, c->f_dec_general, (unsigned) (cnt * n_heads), 256, a,
-                                  "attn_decode", n_heads, head_dim);
+                                  "attn_decode.general", n_heads, head_dim);
             if (rc) return rc;
             continue;
         }
@@ -284,11 +305,11 @@ int decode_launch(moearc_ctx *c, void *out, unsigned int out_f16, const float *q
         a.ws = c->ws;
         const bool any_split = items > cnt;  // some sequence has more than one split
         const int rc = launch(c, c->f_dec_fast[variant], (unsigned) wgs, 64u * kb * wpk, a,
-                              "attn_decode", n_heads, head_dim, any_split ? 1 : 0);
+                              "attn_decode.split", n_heads, head_dim);
         if (rc) return rc;
         if (any_split) {
             const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads), 256, a,
-                                  "attn_decode", n_heads, head_dim, 2);
+                                  "attn_decode.merge", n_heads, head_dim);
             if (rm) return rm;
         }
     }
