@@ -26,8 +26,11 @@ CODE_OBJECT = os.path.join(HERE, "moearc_attn_gfx950.co")
 LIBRARY = os.path.join(HERE, "libmoearc_attn.so")
 
 # Packed-FP32 instructions stay disabled (v_pk_fma_f32 and friends are not emitted).
+# -fno-honor-nans: no kernel tests for NaN (the f16 codec classifies NaNs by their bits), and
+# without it every fmaxf is preceded by a NaN-quieting v_max x,x.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-O3", "-std=c++17",
+    "-fno-honor-nans",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

@@ -69,6 +69,7 @@ struct moearc_ctx {
     hipFunction_t f_dec_fast[5] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2
     hipFunction_t f_dec_merge = nullptr;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
+    bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
     bool profiling = false;
     std::vector<Pending> pending;
     std::vector<KernelTime> totals;
@@ -369,10 +370,19 @@ moearc_ctx *moearc_ctx_create(void) {
             return nullptr;
         }
     }
-    const char *pf[4] = {"moearc_attn_prefill_g1", "moearc_attn_prefill_g2", "moearc_attn_prefill_g4",
-                         "moearc_attn_prefill_g8"};
-    for (int i = 0; i < 4; ++i)
-        if (hipModuleGetFunction(&c->f_prefill[i], c->module, pf[i]) != hipSuccess) c->f_prefill[i] = nullptr;
+    if (const char *pp = std::getenv("MOEARC_PREFILL_PRECISE")) c->prefill_precise = pp[0] == '1';
+    for (int i = 0; i < 4; ++i) {
+        char name[64];
+        std::snprintf(name, sizeof(name), "moearc_attn_prefill_%sg%d", c->prefill_precise ? "precise_" : "",
+                      1 << i);
+        if (hipModuleGetFunction(&c->f_prefill[i], c->module, name) != hipSuccess) {
+            std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), name);
+            hipModuleUnload(c->module);
+            hipStreamDestroy(c->stream);
+            delete c;
+            return nullptr;
+        }
+    }
     const char *ev = std::getenv("MOEARC_PROFILE_EVENTS");
     c->profiling = ev && ev[0] == '1';
     if (const char *w = std::getenv("MOEARC_DECODE_VARIANT")) {

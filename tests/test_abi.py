@@ -43,7 +43,8 @@ def test_library_exports_every_declared_symbol():
 def test_code_object_holds_every_kernel_the_runtime_loads():
     blob = open(native.CODE_OBJECT, "rb").read()
     src = open(os.path.join(ROOT, "moearc_amd", "csrc", "runtime.cpp")).read()
-    kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge|moearc_attn_prefill_g\d)"', src))
+    kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge)"', src))
+    kernels |= {f"moearc_attn_prefill_{v}g{g}" for v in ("", "precise_") for g in (1, 2, 4, 8)}
     assert kernels
     for k in kernels:
         assert k.encode() in blob, f"kernel {k} missing from the code object"

@@ -63,8 +63,13 @@ def test_shapes_against_oracle(ctx, group, n_q, pos0, pt, n_swa):
     _report("  without sinks", nosink, want_ns)
 
 
-def test_rows_equal_decode_calls(ctx):
-    # the defining property: row i == moearc_attn_decode at n_kv = pos0 + i + 1 (f16 q widened)
+@pytest.mark.parametrize("precise", [False, True])
+def test_rows_equal_decode_calls(monkeypatch, precise):
+    # the defining property: row i == moearc_attn_decode at n_kv = pos0 + i + 1 (f16 q widened).
+    # The precise variant carries p to ~22 bits like decode; the default one p in f16.
+    from moearc_amd import Context
+    monkeypatch.setenv("MOEARC_PREFILL_PRECISE", "1" if precise else "0")
+    ctx = Context()
     pc = fx.prefill_case(0x3D, n_q=40, pos0=200, pt=32)
     got = _run(ctx, pc, 128)
     dk, dv, dbt, ds = ctx.upload(pc.k_raw), ctx.upload(pc.v_raw), ctx.upload(pc.bt), ctx.upload(pc.sinks)
@@ -75,7 +80,19 @@ def test_rows_equal_decode_calls(ctx):
         ctx.attn_decode_ext(dout, dq, dk, dv, dbt, ds, pc.H, pc.G, pc.D, max(0, n_kv - 128), n_kv,
                             pc.pt, float(pc.scale), KvType.F16)
         dec = ctx.download(dout, np.float32, (pc.H, pc.D))
-        _report(f"  prefill row {i} vs decode", got[i], dec, 1e-5)
+        _report(f"  prefill row {i} vs decode (precise={precise})", got[i], dec, 1e-5 if precise else TOL)
+    ctx.close()
+
+
+def test_precise_variant_against_oracle(monkeypatch):
+    from moearc_amd import Context
+    monkeypatch.setenv("MOEARC_PREFILL_PRECISE", "1")
+    with Context() as cx:
+        for n_swa in (0, 16):
+            pc = fx.prefill_case(0x9F11, n_q=48, pos0=80)
+            g = fx.load_golden("ns_prefill_full" if n_swa == 0 else "ns_prefill_swa16")
+            got = _run(cx, pc, n_swa)
+            _report(f"precise prefill n_swa={n_swa}", got[g["rows"]], g["expected"], 1e-5)
 
 
 @pytest.mark.parametrize("n_swa", [0, 128])
