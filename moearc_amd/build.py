@@ -28,9 +28,11 @@ LIBRARY = os.path.join(HERE, "libmoearc_attn.so")
 # Packed-FP32 instructions stay disabled (v_pk_fma_f32 and friends are not emitted).
 # -fno-honor-nans: no kernel tests for NaN (the f16 codec classifies NaNs by their bits), and
 # without it every fmaxf is preceded by a NaN-quieting v_max x,x.
+# MFMA accumulators stay in VGPRs: with the AGPR form the compiler copies every accumulator to
+# VGPRs and back around each rescale branch of the prefill loop.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-O3", "-std=c++17",
-    "-fno-honor-nans",
+    "-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

@@ -8,30 +8,44 @@
 //
 // Work decomposition. A work-group owns one KV head and 128 query rows, a row being one
 // (token, head) pair of that KV head's group -- GQA packing, so every K/V tile staged in LDS serves
-// all the group's heads. Four waves take 32 rows each. Keys stream through LDS in 64-key tiles,
-// double-buffered: the next tile's global loads are in flight while the current one is computed.
+// all the group's heads. Four waves take 32 rows each. Query tiles are dispatched latest first:
+// under the causal mask the latest tokens have the most keys, and the short tiles fill in behind.
 //
-// LDS layouts (per buffer, 16 KiB):
-//   K  [64 keys][64 ch] f16, 16-byte chunks XOR-swizzled by (key & 7): the QK^T A-operand read --
-//      lane (g, m) takes channels 8g..8g+7 (+32) of key m -- is one conflict-free ds_read_b128.
-//   V^T [64 ch][64 keys] f16, 8-byte units XOR-swizzled by (ch & 15): the P.V A-operand -- lane
-//      (g, m) takes keys 4g..4g+3 and 16+4g..16+4g+3 of channel m -- is two ds_read_b64. The
-//      transpose happens on the LDS write: each thread packs two keys' values of one channel into
-//      a dword (v_perm) and stores it.
+// Keys stream through LDS in 64-key tiles, two buffers (each its own LDS object, the loop unrolled
+// by two, so the compiler can tell a read of one buffer from the copy in flight into the other):
+// at the top of tile kt every wave waits for its copies of tile kt and meets the others at a
+// barrier, issues the copies of tile kt + 1 into the other buffer, then computes tile kt.
+// The copies are global_load_lds_dwordx4 (16 bytes per lane, placed at base + 16 * lane), so tiles
+// go from the cache to LDS without passing through registers; the block-table entries a lane needs
+// for a tile are loaded one tile ahead.
+//
+// LDS layout of a buffer: K and V each [64 keys][64 ch] f16, 128-byte rows whose 16-byte chunks are
+// XOR-swizzled by (key & 7): chunk c of key k at k * 128 + ((c ^ (k & 7)) << 4).
+//   QK^T A-operand (K): lane (g, m) takes channels 8g..8g+7 (and +32) of key m -- one
+//      ds_read_b128, conflict-free.
+//   P.V A-operand (V^T): lane (g, m) needs channel m of keys {4g..4g+3} and {16+4g..16+4g+3}, the
+//      MFMA k-slot order of the P operand. ds_read_b64_tr_b16 transposes within each 16-lane group
+//      (lane r receives element r & 3 of the 8 bytes addressed by lanes 4j + (r >> 2), j = 0..3),
+//      so lane s of group g addresses key 4g + (s >> 2) (+16), channels 4(s & 3)..+3 of the block:
+//      two conflict-free reads per operand.
 // Per 32-key chunk, a wave computes S^T[32 keys x 32 rows] = K . Q^T (8 MFMAs, f16 Q is exact),
-// the online softmax in the log2 domain with a lazily moved reference max, and
-// O^T[64 ch x 32 rows] += V^T . P^T (8 MFMAs) with P as one f16 operand, f32 accumulation: the
-// weights carry f16's 11 bits, an output error of at most 2^-12 max|V| (measured ~2.5e-4 on N(0,1)
-// data). The _precise_ variants split p = p_hi + p_lo into two f16 operands (16 MFMAs), keeping
-// ~22 bits like the decode kernel. Causal/window masks are applied only in chunks that cross a
-// row's span boundary.
+// the softmax weights p = 2^(s*c + 7 - m) in the log2 domain against a lazily moved per-row
+// reference m, and O^T[64 ch x 32 rows] += V^T . P^T (8 MFMAs) with P as one f16 operand, f32
+// accumulation: the weights carry f16's 11 bits, an output error of at most 2^-12 max|V|
+// (measured ~2.5e-4 on N(0,1) data). The row sums come from the same f16 P through two more
+// MFMAs against an all-ones operand. The _precise_ variants split p = p_hi + p_lo into two f16
+// operands, keeping ~22 bits like the decode kernel.
+//
+// The reference m moves only when some score of the row exceeds it by more than 8 (log2 units),
+// which each lane detects from its own 8 scores; the cross-lane row maximum and the rescale of
+// O and the sums run only then (in practice at a row's first chunk). So p <= 2^15 fits f16.
+// Causal/window masks are applied only in chunks that cross a row's span boundary.
 #include "common.h"
 
 #define PF_LOG2_PSCALE 7.0f
 #define PF_RESCALE_SLACK 8.0f
 #define PF_M_INIT -1.0e30f  // finite "no key yet": keeps exp2(m_old - m_new) defined for rows
                             // whose keys all lie in later chunks
-#define PF_PT_CAP 2048      // block-table entries staged in LDS per work-group
 #define PF_KT 64            // keys per LDS tile
 
 __device__ __forceinline__ float4_t pf_mfma(const half8_t a, const half8_t b, const float4_t c) {
@@ -44,57 +58,95 @@ __device__ __forceinline__ float pf_max16_32(float x) {
     return x;
 }
 
-// Byte offset of K element chunk c (8 channels) of key k within a K tile.
-__device__ __forceinline__ uint32_t k_off(uint32_t k, uint32_t c) {
+__device__ __forceinline__ float pf_max8(const float4_t a, const float4_t b) {
+    return fmaxf(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])), fmaxf(fmaxf(b[0], b[1]), fmaxf(b[2], b[3])));
+}
+
+// Byte offset of 16-byte chunk c (8 channels) of key k within a K or V tile.
+__device__ __forceinline__ uint32_t kv_off(uint32_t k, uint32_t c) {
     return k * 128u + ((c ^ (k & 7u)) << 4);
 }
 
-// Byte offset of the dword holding keys (k, k+1) (k even) of channel d within a V^T tile.
-__device__ __forceinline__ uint32_t vt_off(uint32_t d, uint32_t k) {
-    return d * 128u + ((((k >> 2) ^ (d & 15u))) << 3) + ((k & 3u) << 1);
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void pf_static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        pf_static_for<B + 1, E>(f);
+    }
+}
+
+// LDS reads of the tiles are issued through asm, each group together with its wait: the tiles
+// are filled by LDS DMA, and the compiler, which cannot tell the buffer being read from the one
+// being filled, would otherwise wait for the copy in flight before every read. Offsets are
+// immediates (per-lane base address + buffer/chunk offset).
+template <int O0, int O1>
+__device__ __forceinline__ void pf_read_k(u32x4_t (&r)[4], uint32_t a0, uint32_t a1) {
+    asm volatile(
+        "ds_read_b128 %0, %4 offset:%6\n\t"
+        "ds_read_b128 %1, %5 offset:%6\n\t"
+        "ds_read_b128 %2, %4 offset:%7\n\t"
+        "ds_read_b128 %3, %5 offset:%7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(a0), "v"(a1), "i"(O0), "i"(O1)
+        : "memory");
+}
+
+// Transposing reads (ds_read_b64_tr_b16) of two V^T operands: bases a0, a1, keys +0 and +16.
+template <int O0, int O1>
+__device__ __forceinline__ void pf_read_vt(u32x2_t (&r)[4], uint32_t a0, uint32_t a1) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %4 offset:%6\n\t"
+        "ds_read_b64_tr_b16 %1, %4 offset:%7\n\t"
+        "ds_read_b64_tr_b16 %2, %5 offset:%6\n\t"
+        "ds_read_b64_tr_b16 %3, %5 offset:%7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(a0), "v"(a1), "i"(O0), "i"(O1)
+        : "memory");
 }
 
 template <int GROUP, bool SPLIT_P>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     constexpr uint32_t ROWS = MOEARC_PREFILL_ROWS;  // 128 rows per work-group
     constexpr uint32_t TOK = ROWS / GROUP;          // query tokens per work-group
-    __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2][2][PF_KT * 128];  // [buf][K, V^T]
-    __shared__ uint32_t pt_lds[PF_PT_CAP];
+    constexpr uint32_t TILE_BYTES = PF_KT * 128u;   // one K or V tile
+    constexpr uint32_t BUF_BYTES = 2u * TILE_BYTES;  // K tile, V tile
+    __shared__ __attribute__((aligned(1024))) uint8_t tiles[2 * BUF_BYTES];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t G = a.n_kv_heads;
     const uint32_t kvh = blockIdx.x % G;
-    const uint32_t qt = blockIdx.x / G;
+    const uint32_t qt = a.n_qtiles - 1u - blockIdx.x / G;
     const uint32_t q0 = qt * TOK;                   // first query token of the work-group
     const uint32_t q_end = min(q0 + TOK, a.n_q);
     const uint32_t g = lane >> 4, n = lane & 15u;
-    const uint32_t sh = a.pt_shift;
+    const uint32_t sh = a.pt_shift, pmask = (1u << sh) - 1u;
 
     // key span of the whole work-group
     const uint32_t p_first = a.pos0 + q0, p_last = a.pos0 + q_end - 1u;
     const uint32_t k_lo = a.n_swa ? (p_first + 1u > a.n_swa ? p_first + 1u - a.n_swa : 0u) : 0u;
     const uint32_t kt_first = k_lo / PF_KT, kt_last = p_last / PF_KT;
-    const uint32_t page0 = (kt_first * PF_KT) >> sh;
-    const uint32_t npages = (p_last >> sh) - page0 + 1u;  // host guarantees <= PF_PT_CAP
-    for (uint32_t i = tid; i < npages; i += 256u) pt_lds[i] = a.block_table[page0 + i];
 
     // ---- rows of this wave: local row r (0..31) -> (token, head) --------------------------------
     // Q^T operand: lane (g, n) of row block rb holds row 16*rb + n, channels 32*hf + 8g .. +7
     half8_t qop[2][2];
     uint32_t row_pos[2];   // absolute position of the row lane n holds in each row block
-    bool row_ok[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
         const uint32_t r = wave * 32u + 16u * rb + n;  // work-group row
         const uint32_t tok = q0 + r / GROUP, hd = kvh * GROUP + r % GROUP;
-        row_ok[rb] = tok < q_end;
+        const bool ok = tok < q_end;
         row_pos[rb] = a.pos0 + min(tok, q_end - 1u);
         const uint16_t *src = a.q + ((uint64_t) min(tok, a.n_q - 1u) * a.n_heads + hd) * 64u + 8u * g;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             u32x4_t v = *(const u32x4_t *) (src + 32 * hf);
-            if (!row_ok[rb]) v = (u32x4_t){0u, 0u, 0u, 0u};
+            if (!ok) v = (u32x4_t){0u, 0u, 0u, 0u};
             qop[rb][hf] = __builtin_bit_cast(half8_t, v);
         }
     }
@@ -105,151 +157,168 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint32_t w_bmin = a.n_swa ? (w_pmin + 1u > a.n_swa ? w_pmin + 1u - a.n_swa : 0u) : 0u;
     const uint32_t w_bmax = a.n_swa ? (w_pmax + 1u > a.n_swa ? w_pmax + 1u - a.n_swa : 0u) : 0u;
 
-    const float c = a.scale_log2e;
+    // s*c with c < 0 equals (-s)*(-c): negate the f16 Q operand (exact) so that c > 0 and the
+    // row maximum of s*c is c times the maximum of s
+    float c = a.scale_log2e;
+    if (c < 0.f) {
+        c = -c;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) qop[rb][hf] = -qop[rb][hf];
+    }
     float m_run[2] = {PF_M_INIT, PF_M_INIT};
-    float l_run[2] = {0.f, 0.f};
-    float4_t O[4][2];
+    float4_t O[4][2], Lsum[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        Lsum[rb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) O[mb][rb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+
+    // ---- per-lane LDS base addresses (buffer 0, chunk 0, tile offset excluded) ----------------
+    // K operand: key n, chunks g and g + 4. V^T operand of channel block mb: key 4g + (n >> 2),
+    // chunk 2mb + ((n >> 1) & 1), 8-byte half n & 1. Chunk/buffer offsets keep the swizzle (key & 7).
+    const uint32_t lds0 = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles;
+    const uint32_t k_base0 = lds0 + kv_off(n, g), k_base1 = lds0 + kv_off(n, g + 4u);
+    const uint32_t vkey = 4u * g + (n >> 2);
+    uint32_t v_base[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) O[mb][rb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+        v_base[mb] = lds0 + kv_off(vkey, 2u * mb + ((n >> 1) & 1u)) + ((n & 1u) << 3);
 
-    __syncthreads();  // page table staged
-
-    // ---- global -> registers for one tile: thread t takes K chunk (key t/8 and t/8+32, ch t%8) --
-    // and V rows (keys 2*(t/8), 2*(t/8)+1, ch t%8)
-    const uint32_t ld_k = tid >> 3, ld_c = tid & 7u;
-    const uint64_t row_elems = (uint64_t) G * 64u;
-    auto key_addr = [&](uint32_t j) -> uint64_t {
-        const uint32_t jc = min(j, p_last);
-        const uint32_t row = (pt_lds[(jc >> sh) - page0] << sh) | (jc & ((1u << sh) - 1u));
-        return (uint64_t) row * row_elems + (uint64_t) kvh * 64u + 8u * ld_c;
-    };
-    u32x4_t gk[2], gv[2];
-    auto gload = [&](uint32_t kt) {
-        const uint32_t j0 = kt * PF_KT;
-        gk[0] = *(const u32x4_t *) (a.k_pages + key_addr(j0 + ld_k));
-        gk[1] = *(const u32x4_t *) (a.k_pages + key_addr(j0 + ld_k + 32u));
-        gv[0] = *(const u32x4_t *) (a.v_pages + key_addr(j0 + 2u * ld_k));
-        gv[1] = *(const u32x4_t *) (a.v_pages + key_addr(j0 + 2u * ld_k + 1u));
-    };
-    auto lds_store = [&](int buf) {
-        uint8_t *kb = kv_lds[buf][0], *vb = kv_lds[buf][1];
-        *(u32x4_t *) (kb + k_off(ld_k, ld_c)) = gk[0];
-        *(u32x4_t *) (kb + k_off(ld_k + 32u, ld_c)) = gk[1];
-        // channel 8*ld_c + e of keys (2*ld_k, 2*ld_k + 1) -> one dword of V^T
+    // ---- tile copies: lane L of wave w fills LDS chunk slot L of keys 16w + 8i + (L >> 3) -------
+    // (i = 0, 1) of the K and the V tile; that slot holds chunk (L & 7) ^ (L >> 3) of the key.
+    // Keys past p_last (no row sees them) are clamped to p_last so every copy reads a valid row.
+    const uint32_t ld_key = 16u * wave + (lane >> 3);
+    const uint32_t ld_chunk = (lane & 7u) ^ (lane >> 3);
+    const uint64_t row_bytes = (uint64_t) G * 128u;
+    const uint8_t *k_src = (const uint8_t *) a.k_pages + kvh * 128u + ld_chunk * 16u;
+    const uint8_t *v_src = (const uint8_t *) a.v_pages + kvh * 128u + ld_chunk * 16u;
+    uint32_t pid[2];  // block-table entries of this lane's two keys of the next tile
+    auto load_pids = [&](uint32_t kt) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = __builtin_amdgcn_perm(gv[1][e], gv[0][e], 0x05040100u);  // ch 2e
-            const uint32_t hi = __builtin_amdgcn_perm(gv[1][e], gv[0][e], 0x07060302u);  // ch 2e+1
-            *(uint32_t *) (vb + vt_off(8u * ld_c + 2u * e, 2u * ld_k)) = lo;
-            *(uint32_t *) (vb + vt_off(8u * ld_c + 2u * e + 1u, 2u * ld_k)) = hi;
+        for (int i = 0; i < 2; ++i) pid[i] = a.block_table[min(kt * PF_KT + ld_key + 8u * i, p_last) >> sh];
+    };
+    auto copy_tile = [&](uint32_t kt, int buf) {
+        uint8_t *dst = tiles + buf * BUF_BYTES;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t j = min(kt * PF_KT + ld_key + 8u * i, p_last);
+            const uint64_t off = (uint64_t) ((pid[i] << sh) | (j & pmask)) * row_bytes;
+            uint8_t *d = dst + (16u * wave + 8u * i) * 128u;
+            __builtin_amdgcn_global_load_lds(k_src + off, d, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(v_src + off, d + TILE_BYTES, 16, 0, 0);
         }
     };
 
-    gload(kt_first);
-    lds_store(0);
-    __syncthreads();
-    int buf = 0;
-    for (uint32_t kt = kt_first; kt <= kt_last; ++kt) {
-        const bool more = kt < kt_last;
-        if (more) gload(kt + 1u);  // uniform branch: the last tile has nothing to prefetch
-        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-        const uint8_t *kb = kv_lds[buf][0], *vb = kv_lds[buf][1];
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {  // 32-key chunks
+    // ---- one tile: 2 chunks of 32 keys ----------------------------------------------------------
+    auto compute_tile = [&](uint32_t kt, auto buf_c) {
+        constexpr int BOFF = decltype(buf_c)::value * (int) BUF_BYTES;
+        pf_static_for<0, 2>([&](auto kc_c) {  // 32-key chunks
+            constexpr int kc = decltype(kc_c)::value;
             const uint32_t j0 = kt * PF_KT + 32u * kc;
-            if (j0 > w_pmax || j0 + 31u < w_bmin) continue;  // no row of this wave sees the chunk
+            if (j0 > w_pmax || j0 + 31u < w_bmin) return;  // no row of this wave sees the chunk
             // QK^T: S[kb2][rb] lane (g, n) reg i = key j0 + 16*kb2 + 4g + i, row 16*rb + n
+            u32x4_t kr[4];  // [kb2 * 2 + channel half]
+            pf_read_k<BOFF + 4096 * kc, BOFF + 4096 * kc + 2048>(kr, k_base0, k_base1);
             float4_t S[2][2];
 #pragma unroll
             for (int kb2 = 0; kb2 < 2; ++kb2) {
-                const uint32_t key = 32u * kc + 16u * kb2 + n;  // A-operand row = lane n
-                const half8_t k0 = __builtin_bit_cast(half8_t, *(const u32x4_t *) (kb + k_off(key, g)));
-                const half8_t k1 = __builtin_bit_cast(half8_t, *(const u32x4_t *) (kb + k_off(key, 4u + g)));
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb) {
                     float4_t s = (float4_t){0.f, 0.f, 0.f, 0.f};
-                    s = pf_mfma(k0, qop[rb][0], s);
-                    s = pf_mfma(k1, qop[rb][1], s);
+                    s = pf_mfma(__builtin_bit_cast(half8_t, kr[2 * kb2]), qop[rb][0], s);
+                    s = pf_mfma(__builtin_bit_cast(half8_t, kr[2 * kb2 + 1]), qop[rb][1], s);
                     S[kb2][rb] = s;
                 }
             }
-            // masks, only where the chunk crosses some row's span boundary (uniform branch)
+            // masks, only where the chunk crosses some row's span boundary (uniform branch):
+            // key j = j0 + 16*kb2 + 4g + i is outside row p's span [bp, p] iff
+            // (j - bp) > (p - bp) as unsigned
             if (j0 + 31u > w_pmin || (a.n_swa && j0 < w_bmax)) {
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb) {
                     const uint32_t p = row_pos[rb];
                     const uint32_t bp = a.n_swa ? (p + 1u > a.n_swa ? p + 1u - a.n_swa : 0u) : 0u;
+                    const uint32_t off = j0 + 4u * g - bp, span = p - bp;
 #pragma unroll
                     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const uint32_t j = j0 + 16u * kb2 + 4u * g + i;
-                            if (j > p || j < bp) S[kb2][rb][i] = -INFINITY;
-                        }
+                        for (int i = 0; i < 4; ++i)
+                            if (off + (16u * kb2 + i) > span) S[kb2][rb][i] = -INFINITY;
                 }
             }
-            // online softmax per row block; P^T operand item i = key 16*(i/4) + 4g + i%4
+            // softmax weights per row block; P^T operand item i = key 16*(i/4) + 4g + i%4
             half8_t phi[2], plo[2];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
-                float tmax = fmaxf(fmaxf(fmaxf(S[0][rb][0], S[0][rb][1]), fmaxf(S[0][rb][2], S[0][rb][3])),
-                                   fmaxf(fmaxf(S[1][rb][0], S[1][rb][1]), fmaxf(S[1][rb][2], S[1][rb][3])));
-                tmax = pf_max16_32(tmax) * c;
-                if (__builtin_amdgcn_ballot_w64(tmax > m_run[rb] + PF_RESCALE_SLACK) != 0) {
-                    const float m_new = fmaxf(m_run[rb], tmax);
+                const float lmax = pf_max8(S[0][rb], S[1][rb]) * c;
+                if (__builtin_amdgcn_ballot_w64(lmax > m_run[rb] + PF_RESCALE_SLACK) != 0) {
+                    const float m_new = fmaxf(m_run[rb], pf_max16_32(lmax));
                     const float corr = __builtin_amdgcn_exp2f(m_run[rb] - m_new);
                     m_run[rb] = m_new;
-                    l_run[rb] *= corr;
+                    Lsum[rb] *= corr;
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb) O[mb][rb] *= corr;
                 }
                 const float bias = PF_LOG2_PSCALE - m_run[rb];
-                float psum = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const float ps = __builtin_amdgcn_exp2f(fmaf(S[i >> 2][rb][i & 3], c, bias));
-                    psum += ps;
                     const _Float16 hi = (_Float16) ps;
                     phi[rb][i] = hi;
                     if constexpr (SPLIT_P) plo[rb][i] = (_Float16) (ps - (float) hi);
                 }
-                l_run[rb] += psum;
+                Lsum[rb] = pf_mfma(ones, phi[rb], Lsum[rb]);
+                if constexpr (SPLIT_P) Lsum[rb] = pf_mfma(ones, plo[rb], Lsum[rb]);
             }
-            // P.V: V^T operand for channel block mb: lane (g, m) = channel 16*mb + m,
-            // keys 32*kc + 4g .. +3 and 32*kc + 16 + 4g .. +3
+            // P.V: V^T operands of channel blocks 2mp, 2mp + 1, each from two transposing reads
+            pf_static_for<0, 2>([&](auto mp_c) {
+                constexpr int mp = decltype(mp_c)::value;
+                constexpr int VOFF = BOFF + (int) TILE_BYTES + 4096 * kc;
+                u32x2_t vt[4];  // [h2 * 2 + (keys +16)]
+                pf_read_vt<VOFF, VOFF + 2048>(vt, v_base[2 * mp], v_base[2 * mp + 1]);
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const uint32_t d = 16u * mb + n;
-                const uint32_t base = d * 128u;
-                const uint32_t u0 = 8u * kc + g, u1 = 8u * kc + 4u + g;  // 8-byte units (4 keys)
-                const uint64_t lo4 = *(const uint64_t *) (vb + base + ((u0 ^ (d & 15u)) << 3));
-                const uint64_t hi4 = *(const uint64_t *) (vb + base + ((u1 ^ (d & 15u)) << 3));
-                const u32x4_t vv = (u32x4_t){(uint32_t) lo4, (uint32_t) (lo4 >> 32), (uint32_t) hi4,
-                                             (uint32_t) (hi4 >> 32)};
-                const half8_t va = __builtin_bit_cast(half8_t, vv);
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    const int mb = 2 * mp + h2;
+                    const half8_t va = __builtin_bit_cast(
+                        half8_t, (u32x4_t){vt[2 * h2][0], vt[2 * h2][1], vt[2 * h2 + 1][0], vt[2 * h2 + 1][1]});
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
-                    O[mb][rb] = pf_mfma(va, phi[rb], O[mb][rb]);
-                    if constexpr (SPLIT_P) O[mb][rb] = pf_mfma(va, plo[rb], O[mb][rb]);
+                    for (int rb = 0; rb < 2; ++rb) {
+                        O[mb][rb] = pf_mfma(va, phi[rb], O[mb][rb]);
+                        if constexpr (SPLIT_P) O[mb][rb] = pf_mfma(va, plo[rb], O[mb][rb]);
+                    }
                 }
-            }
+            });
+        });
+    };
+
+    // ---- pipeline: tile kt in buffer kt & 1; tile kt + 1 is copied into the other buffer while
+    // kt is computed
+    auto step = [&](uint32_t kt, auto buf_c) {
+        constexpr int BUF = decltype(buf_c)::value;
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile kt (and the next entries)
+        __builtin_amdgcn_s_barrier();   // everyone's copies landed; everyone is done with kt - 1
+        if (kt < kt_last) {
+            copy_tile(kt + 1u, BUF ^ 1);
+            if (kt + 1u < kt_last) load_pids(kt + 2u);
         }
-        __syncthreads();  // every wave is done reading this buffer and (as of the loop head) the other
-        if (more) {
-            lds_store(buf ^ 1);
-            __syncthreads();
-            buf ^= 1;
-        }
+        compute_tile(kt, buf_c);
+    };
+    load_pids(kt_first);
+    copy_tile(kt_first, 0);
+    if (kt_first < kt_last) load_pids(kt_first + 1u);
+    for (uint32_t kt = kt_first; kt <= kt_last; kt += 2u) {
+        step(kt, std::integral_constant<int, 0>{});
+        if (kt + 1u <= kt_last) step(kt + 1u, std::integral_constant<int, 1>{});
     }
 
-    // ---- finalise: denominators over the 4 lanes of a row, the sink, the store -----------------
+    // ---- finalise: the sink, the normalisation, the store -----------------------------------
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-        float L = l_run[rb];
-        L += __shfl_xor(L, 16);
-        L += __shfl_xor(L, 32);
+        const float L = Lsum[rb][0];  // every lane of the row holds the row's sum
         const uint32_t r = wave * 32u + 16u * rb + n;
         const uint32_t tok = q0 + r / GROUP, hd = kvh * GROUP + r % GROUP;
         const float sink2 = a.sinks ? a.sinks[hd] * MOEARC_LOG2E : -INFINITY;
