@@ -11,34 +11,50 @@
 // all the group's heads. Four waves take 32 rows each. Query tiles are dispatched latest first:
 // under the causal mask the latest tokens have the most keys, and the short tiles fill in behind.
 //
-// Keys stream through LDS in 64-key tiles, two buffers (each its own LDS object, the loop unrolled
-// by two, so the compiler can tell a read of one buffer from the copy in flight into the other):
-// at the top of tile kt every wave waits for its copies of tile kt and meets the others at a
-// barrier, issues the copies of tile kt + 1 into the other buffer, then computes tile kt.
-// The copies are global_load_lds_dwordx4 (16 bytes per lane, placed at base + 16 * lane), so tiles
-// go from the cache to LDS without passing through registers; the block-table entries a lane needs
-// for a tile are loaded one tile ahead.
+// Keys stream through LDS in 64-key tiles, double-buffered: at the top of tile kt every wave waits
+// for its copies of tile kt and meets the others at a barrier, issues the copies of tile kt + 1
+// into the other buffer, then computes tile kt. The copies are global_load_lds_dwordx4 (16 bytes
+// per lane, placed at base + 16 * lane), so tiles go from the cache to LDS without passing through
+// registers. Wave w copies keys 16w..16w+15 of each tile; with pages of at least 16 tokens they
+// lie in one page, whose block-table entry is a wave-uniform scalar load, otherwise every lane
+// looks up its own key's page. Keys past the last query position are clamped to it, so no copy
+// reads a slot the cache has not written.
+//
+// Matrix layout: v_mfma_f32_32x32x16_f16 throughout (on gfx950 it leaves room for a few VALU
+// instructions beside each MFMA, where 16x16x32 leaves almost none). Per 32-key chunk a wave
+//   S^T[32 keys x 32 rows] = K . Q^T            4 MFMAs (k = 16 channels each)
+//   O^T[64 ch x 32 rows] += V^T . P^T           4 MFMAs (2 channel blocks x 2 steps of 16 keys)
+// Lane (h, n) (h = lane / 32) holds S^T rows 8j + 4h + i (j, i = 0..3) of column n: 16 keys of
+// query row n. Taken in register order, S regs 8s..8s+7 are exactly the k-slots 8h..8h+7 of the
+// P^T operand of step s -- keys 16s + 4h + i and 16s + 8 + 4h + i -- so P needs no shuffles and V^T
+// is read in that key order.
 //
 // LDS layout of a buffer: K and V each [64 keys][64 ch] f16, 128-byte rows whose 16-byte chunks are
-// XOR-swizzled by (key & 7): chunk c of key k at k * 128 + ((c ^ (k & 7)) << 4).
-//   QK^T A-operand (K): lane (g, m) takes channels 8g..8g+7 (and +32) of key m -- one
-//      ds_read_b128, conflict-free.
-//   P.V A-operand (V^T): lane (g, m) needs channel m of keys {4g..4g+3} and {16+4g..16+4g+3}, the
-//      MFMA k-slot order of the P operand. ds_read_b64_tr_b16 transposes within each 16-lane group
-//      (lane r receives element r & 3 of the 8 bytes addressed by lanes 4j + (r >> 2), j = 0..3),
-//      so lane s of group g addresses key 4g + (s >> 2) (+16), channels 4(s & 3)..+3 of the block:
-//      two conflict-free reads per operand.
-// Per 32-key chunk, a wave computes S^T[32 keys x 32 rows] = K . Q^T (8 MFMAs, f16 Q is exact),
-// the softmax weights p = 2^(s*c + 7 - m) in the log2 domain against a lazily moved per-row
-// reference m, and O^T[64 ch x 32 rows] += V^T . P^T (8 MFMAs) with P as one f16 operand, f32
-// accumulation: the weights carry f16's 11 bits, an output error of at most 2^-12 max|V|
-// (measured ~2.5e-4 on N(0,1) data). The row sums come from the same f16 P through two more
-// MFMAs against an all-ones operand. The _precise_ variants split p = p_hi + p_lo into two f16
-// operands, keeping ~22 bits like the decode kernel.
+// XOR-swizzled: chunk c of key k at k * 128 + ((c ^ f(k)) << 4). gfx950's LDS serves 256 bytes per
+// clock from 64 banks (two 128-byte rows side by side); a ds_read_b128 is served in 16-lane passes
+// that pair lanes i and i + 16, a 64-bit transposing read in 32-lane passes (as measured with
+// SQ_LDS_BANK_CONFLICT). The swizzles keep every pass on distinct banks:
+//   K: f(k) = (k & 7) ^ ((k >> 4) & 1) -- keys n and n + 16 of one pass differ in bit 4 only;
+//   V: f(k) = (k & 7) ^ (((k >> 1) & 1) << 2) -- a half-wave reads 4 keys x 4 chunks, and the
+//      term spreads them over both halves of the 8 chunk slots.
+//   K operand of MFMA t: lane (h, m) takes channels 16t + 8h..+7 of key m -- one ds_read_b128.
+//   V^T operand of (channel block mb, step s): lane (h, q, r) (q = lane / 16 & 1, r = lane & 15)
+//      needs channel 32mb + 16q + r of keys 16s + 4h + j and 16s + 8 + 4h + j. ds_read_b64_tr_b16
+//      transposes within each 16-lane group (lane r receives element r & 3 of the 8 bytes addressed
+//      by lanes 4j + (r >> 2), j = 0..3), so lane r addresses key 16s + 4h + (r >> 2) (+8),
+//      channels 32mb + 16q + 4(r & 3)..+3: two reads per operand.
+// LDS reads are issued through asm with their waits: the compiler, which cannot tell the buffer
+// being read from the one being filled by LDS DMA, would otherwise wait for the copy in flight
+// before every read.
 //
-// The reference m moves only when some score of the row exceeds it by more than 8 (log2 units),
-// which each lane detects from its own 8 scores; the cross-lane row maximum and the rescale of
-// O and the sums run only then (in practice at a row's first chunk). So p <= 2^15 fits f16.
+// Softmax. p = 2^(s*c + 7 - m) in the log2 domain (c = scale * log2 e) against a per-row reference
+// m that moves only when some score of the row exceeds it by more than 8: each lane checks its own
+// 16 scores, and the cross-lane row maximum and the rescale of O and the sums run only then (in
+// practice at a row's first chunk). So p <= 2^15 fits f16. P enters the MFMA as one f16 operand with
+// f32 accumulation: the weights carry f16's 11 bits, an output error of at most 2^-12 max|V|
+// (measured ~2.5e-4 on N(0,1) data); the row sums are dot products of the same f16 weights with
+// ones (v_dot2_f32_f16), so numerator and denominator see the same rounding. The _precise_
+// variants split p = p_hi + p_lo into two f16 operands, keeping ~22 bits like the decode kernel.
 // Causal/window masks are applied only in chunks that cross a row's span boundary.
 #include "common.h"
 
@@ -48,26 +64,24 @@
                             // whose keys all lie in later chunks
 #define PF_KT 64            // keys per LDS tile
 
-__device__ __forceinline__ float4_t pf_mfma(const half8_t a, const half8_t b, const float4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float pf_max16_32(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16));
-    x = fmaxf(x, __shfl_xor(x, 32));
-    return x;
-}
-
-__device__ __forceinline__ float pf_max8(const float4_t a, const float4_t b) {
-    return fmaxf(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])), fmaxf(fmaxf(b[0], b[1]), fmaxf(b[2], b[3])));
-}
-
-// Byte offset of 16-byte chunk c (8 channels) of key k within a K or V tile.
-__device__ __forceinline__ uint32_t kv_off(uint32_t k, uint32_t c) {
-    return k * 128u + ((c ^ (k & 7u)) << 4);
-}
-
+typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float16_t pf_mfma(const half8_t a, const half8_t b, const float16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Byte offset of 16-byte chunk c (8 channels) of key k within a K tile ...
+__device__ __forceinline__ uint32_t k_swz(uint32_t k) { return (k & 7u) ^ ((k >> 4) & 1u); }
+__device__ __forceinline__ uint32_t k_off(uint32_t k, uint32_t c) {
+    return k * 128u + ((c ^ k_swz(k)) << 4);
+}
+
+// ... and within a V tile.
+__device__ __forceinline__ uint32_t v_swz(uint32_t k) { return (k & 7u) ^ (((k >> 1) & 1u) << 2); }
+__device__ __forceinline__ uint32_t v_off(uint32_t k, uint32_t c) {
+    return k * 128u + ((c ^ v_swz(k)) << 4);
+}
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
 template <int B, int E, typename F>
@@ -78,34 +92,31 @@ __device__ __forceinline__ void pf_static_for(F &&f) {
     }
 }
 
-// LDS reads of the tiles are issued through asm, each group together with its wait: the tiles
-// are filled by LDS DMA, and the compiler, which cannot tell the buffer being read from the one
-// being filled, would otherwise wait for the copy in flight before every read. Offsets are
-// immediates (per-lane base address + buffer/chunk offset).
-template <int O0, int O1>
-__device__ __forceinline__ void pf_read_k(u32x4_t (&r)[4], uint32_t a0, uint32_t a1) {
+// K operands of one chunk: r[t] at base[t] + O (channels 16t + 8h..+7 of key m).
+template <int O>
+__device__ __forceinline__ void pf_read_k(u32x4_t (&r)[4], const uint32_t (&base)[4]) {
     asm volatile(
-        "ds_read_b128 %0, %4 offset:%6\n\t"
-        "ds_read_b128 %1, %5 offset:%6\n\t"
-        "ds_read_b128 %2, %4 offset:%7\n\t"
-        "ds_read_b128 %3, %5 offset:%7\n\t"
+        "ds_read_b128 %0, %4 offset:%8\n\t"
+        "ds_read_b128 %1, %5 offset:%8\n\t"
+        "ds_read_b128 %2, %6 offset:%8\n\t"
+        "ds_read_b128 %3, %7 offset:%8\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-        : "v"(a0), "v"(a1), "i"(O0), "i"(O1)
+        : "v"(base[0]), "v"(base[1]), "v"(base[2]), "v"(base[3]), "i"(O)
         : "memory");
 }
 
-// Transposing reads (ds_read_b64_tr_b16) of two V^T operands: bases a0, a1, keys +0 and +16.
-template <int O0, int O1>
-__device__ __forceinline__ void pf_read_vt(u32x2_t (&r)[4], uint32_t a0, uint32_t a1) {
+// V^T operands of one channel block: r[2s + e] = keys 16s + 8e + 4h + (0..3), by transposing reads.
+template <int O>
+__device__ __forceinline__ void pf_read_vt(u32x2_t (&r)[4], uint32_t base) {
     asm volatile(
-        "ds_read_b64_tr_b16 %0, %4 offset:%6\n\t"
-        "ds_read_b64_tr_b16 %1, %4 offset:%7\n\t"
-        "ds_read_b64_tr_b16 %2, %5 offset:%6\n\t"
-        "ds_read_b64_tr_b16 %3, %5 offset:%7\n\t"
+        "ds_read_b64_tr_b16 %0, %4 offset:%5\n\t"
+        "ds_read_b64_tr_b16 %1, %4 offset:%6\n\t"
+        "ds_read_b64_tr_b16 %2, %4 offset:%7\n\t"
+        "ds_read_b64_tr_b16 %3, %4 offset:%8\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-        : "v"(a0), "v"(a1), "i"(O0), "i"(O1)
+        : "v"(base), "i"(O), "i"(O + 1024), "i"(O + 2048), "i"(O + 3072)
         : "memory");
 }
 
@@ -124,7 +135,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint32_t qt = a.n_qtiles - 1u - blockIdx.x / G;
     const uint32_t q0 = qt * TOK;                   // first query token of the work-group
     const uint32_t q_end = min(q0 + TOK, a.n_q);
-    const uint32_t g = lane >> 4, n = lane & 15u;
+    const uint32_t h = lane >> 5, n = lane & 31u;
     const uint32_t sh = a.pt_shift, pmask = (1u << sh) - 1u;
 
     // key span of the whole work-group
@@ -132,22 +143,21 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint32_t k_lo = a.n_swa ? (p_first + 1u > a.n_swa ? p_first + 1u - a.n_swa : 0u) : 0u;
     const uint32_t kt_first = k_lo / PF_KT, kt_last = p_last / PF_KT;
 
-    // ---- rows of this wave: local row r (0..31) -> (token, head) --------------------------------
-    // Q^T operand: lane (g, n) of row block rb holds row 16*rb + n, channels 32*hf + 8g .. +7
-    half8_t qop[2][2];
-    uint32_t row_pos[2];   // absolute position of the row lane n holds in each row block
+    // ---- this lane's query row: local row n of the wave -> (token, head) -----------------------
+    // Q^T operand of MFMA t: row n, channels 16t + 8h .. +7
+    half8_t qop[4];
+    const uint32_t r_wg = wave * 32u + n;
+    const uint32_t tok = q0 + r_wg / GROUP, hd = kvh * GROUP + r_wg % GROUP;
+    const bool row_ok = tok < q_end;
+    const uint32_t row_pos = a.pos0 + min(tok, q_end - 1u);
+    const uint32_t row_bp = a.n_swa ? (row_pos + 1u > a.n_swa ? row_pos + 1u - a.n_swa : 0u) : 0u;
+    {
+        const uint16_t *src = a.q + ((uint64_t) min(tok, a.n_q - 1u) * a.n_heads + hd) * 64u + 8u * h;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const uint32_t r = wave * 32u + 16u * rb + n;  // work-group row
-        const uint32_t tok = q0 + r / GROUP, hd = kvh * GROUP + r % GROUP;
-        const bool ok = tok < q_end;
-        row_pos[rb] = a.pos0 + min(tok, q_end - 1u);
-        const uint16_t *src = a.q + ((uint64_t) min(tok, a.n_q - 1u) * a.n_heads + hd) * 64u + 8u * g;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            u32x4_t v = *(const u32x4_t *) (src + 32 * hf);
-            if (!ok) v = (u32x4_t){0u, 0u, 0u, 0u};
-            qop[rb][hf] = __builtin_bit_cast(half8_t, v);
+        for (int t = 0; t < 4; ++t) {
+            u32x4_t v = *(const u32x4_t *) (src + 16 * t);
+            if (!row_ok) v = (u32x4_t){0u, 0u, 0u, 0u};
+            qop[t] = __builtin_bit_cast(half8_t, v);
         }
     }
     // the wave's position range, for deciding which chunks need masks
@@ -163,135 +173,144 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     if (c < 0.f) {
         c = -c;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) qop[rb][hf] = -qop[rb][hf];
+        for (int t = 0; t < 4; ++t) qop[t] = -qop[t];
     }
-    float m_run[2] = {PF_M_INIT, PF_M_INIT};
-    float4_t O[4][2], Lsum[2];
+    float m_run = PF_M_INIT;
+    float l_run = 0.f;  // this lane's share of the row sum (its 16 keys of every chunk)
+    float16_t O[2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        Lsum[rb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) O[mb][rb] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    }
-    const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+        for (int i = 0; i < 16; ++i) O[mb][i] = 0.f;
 
     // ---- per-lane LDS base addresses (buffer 0, chunk 0, tile offset excluded) ----------------
-    // K operand: key n, chunks g and g + 4. V^T operand of channel block mb: key 4g + (n >> 2),
-    // chunk 2mb + ((n >> 1) & 1), 8-byte half n & 1. Chunk/buffer offsets keep the swizzle (key & 7).
     const uint32_t lds0 = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles;
-    const uint32_t k_base0 = lds0 + kv_off(n, g), k_base1 = lds0 + kv_off(n, g + 4u);
-    const uint32_t vkey = 4u * g + (n >> 2);
-    uint32_t v_base[4];
+    uint32_t k_base[4], v_base[2];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-        v_base[mb] = lds0 + kv_off(vkey, 2u * mb + ((n >> 1) & 1u)) + ((n & 1u) << 3);
+    for (int t = 0; t < 4; ++t) k_base[t] = lds0 + k_off(n, 2u * t + h);
+    {
+        const uint32_t r = lane & 15u, q = (lane >> 4) & 1u;
+        const uint32_t vkey = 4u * h + (r >> 2);
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+            v_base[mb] = lds0 + v_off(vkey, 4u * mb + 2u * q + ((r >> 1) & 1u)) + ((r & 1u) << 3);
+    }
 
-    // ---- tile copies: lane L of wave w fills LDS chunk slot L of keys 16w + 8i + (L >> 3) -------
-    // (i = 0, 1) of the K and the V tile; that slot holds chunk (L & 7) ^ (L >> 3) of the key.
-    // Keys past p_last (no row sees them) are clamped to p_last so every copy reads a valid row.
+    // ---- tile copies: lane L of wave w fills LDS chunk slot L & 7 of key k = 16w + 8i + (L >> 3)
+    // (i = 0, 1) of the K and the V tile; that slot holds chunk (L & 7) ^ f(k) of the key (f(k)
+    // depends on k & 7 = L >> 3 and, for K, on bit 4 of k = w & 1).
     const uint32_t ld_key = 16u * wave + (lane >> 3);
-    const uint32_t ld_chunk = (lane & 7u) ^ (lane >> 3);
+    const uint32_t ld_chunk = (lane & 7u) ^ k_swz(ld_key), ld_chunk_v = (lane & 7u) ^ v_swz(ld_key);
     const uint64_t row_bytes = (uint64_t) G * 128u;
     const uint8_t *k_src = (const uint8_t *) a.k_pages + kvh * 128u + ld_chunk * 16u;
-    const uint8_t *v_src = (const uint8_t *) a.v_pages + kvh * 128u + ld_chunk * 16u;
-    uint32_t pid[2];  // block-table entries of this lane's two keys of the next tile
+    const uint8_t *v_src = (const uint8_t *) a.v_pages + kvh * 128u + ld_chunk_v * 16u;
+    const bool wave_page = sh >= 4u;  // a wave's 16 keys of a tile lie in one page
+    // block-table entries for the next tile: wave-uniform (wave_page) or this lane's two keys
+    uint32_t pid[2];
     auto load_pids = [&](uint32_t kt) {
+        if (wave_page) {
+            const uint32_t kb = min(kt * PF_KT + 16u * wave, p_last);
+            pid[0] = __builtin_amdgcn_readfirstlane(a.block_table[__builtin_amdgcn_readfirstlane(kb >> sh)]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) pid[i] = a.block_table[min(kt * PF_KT + ld_key + 8u * i, p_last) >> sh];
+            for (int i = 0; i < 2; ++i) pid[i] = a.block_table[min(kt * PF_KT + ld_key + 8u * i, p_last) >> sh];
+        }
     };
     auto copy_tile = [&](uint32_t kt, int buf) {
-        uint8_t *dst = tiles + buf * BUF_BYTES;
+        uint8_t *dst = tiles + buf * BUF_BYTES + 16u * wave * 128u;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t j = min(kt * PF_KT + ld_key + 8u * i, p_last);
-            const uint64_t off = (uint64_t) ((pid[i] << sh) | (j & pmask)) * row_bytes;
-            uint8_t *d = dst + (16u * wave + 8u * i) * 128u;
-            __builtin_amdgcn_global_load_lds(k_src + off, d, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(v_src + off, d + TILE_BYTES, 16, 0, 0);
+            const uint32_t p = wave_page ? pid[0] : pid[i];
+            const uint64_t off = (uint64_t) ((p << sh) | (j & pmask)) * row_bytes;
+            __builtin_amdgcn_global_load_lds(k_src + off, dst + 8u * i * 128u, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(v_src + off, dst + 8u * i * 128u + TILE_BYTES, 16, 0, 0);
         }
     };
 
-    // ---- one tile: 2 chunks of 32 keys ----------------------------------------------------------
-    auto compute_tile = [&](uint32_t kt, auto buf_c) {
-        constexpr int BOFF = decltype(buf_c)::value * (int) BUF_BYTES;
-        pf_static_for<0, 2>([&](auto kc_c) {  // 32-key chunks
+    // ---- chunk stages ----------------------------------------------------------------------------
+    const half2_t ones2 = {1, 1};
+    // QK^T of chunk kc of the tile in buffer offset BOFF: S reg 4j + i = key j0 + 8j + 4h + i of row n
+    auto qk = [&](auto boff_c, auto kc_c) -> float16_t {
+        constexpr int BOFF = decltype(boff_c)::value, kc = decltype(kc_c)::value;
+        u32x4_t kr[4];
+        pf_read_k<BOFF + 4096 * kc>(kr, k_base);
+        float16_t S;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) S = pf_mfma(__builtin_bit_cast(half8_t, kr[t]), qop[t], S);
+        return S;
+    };
+    // masks for chunk keys j0..j0+31: key j is outside the row's span [bp, p] iff
+    // (j - bp) > (p - bp) as unsigned
+    auto mask = [&](float16_t &S, uint32_t j0) {
+        const uint32_t off = j0 + 4u * h - row_bp, span = row_pos - row_bp;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (off + (uint32_t) (8 * (i >> 2) + (i & 3)) > span) S[i] = -INFINITY;
+    };
+    // softmax weights; P^T operand of step s = S regs 8s..8s+7 in order
+    auto softmax = [&](const float16_t &S, half8_t (&phi)[2], half8_t (&plo)[2]) {
+        float lmax = fmaxf(S[0], S[1]);
+#pragma unroll
+        for (int i = 2; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(S[i], S[i + 1]));
+        lmax *= c;
+        if (__builtin_amdgcn_ballot_w64(lmax > m_run + PF_RESCALE_SLACK) != 0) {
+            const float m_new = fmaxf(m_run, fmaxf(lmax, __shfl_xor(lmax, 32)));
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= corr;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) O[mb] *= corr;
+        }
+        const float bias = PF_LOG2_PSCALE - m_run;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(S[i], c, bias));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(S[i + 1], c, bias));
+            const half2_t hv = {(_Float16) p0, (_Float16) p1};
+            phi[i >> 3][i & 7] = hv[0];
+            phi[i >> 3][(i & 7) + 1] = hv[1];
+            l_run = __builtin_amdgcn_fdot2(hv, ones2, l_run, false);
+            if constexpr (SPLIT_P) {
+                const half2_t lv = {(_Float16) (p0 - (float) hv[0]), (_Float16) (p1 - (float) hv[1])};
+                plo[i >> 3][i & 7] = lv[0];
+                plo[i >> 3][(i & 7) + 1] = lv[1];
+                l_run = __builtin_amdgcn_fdot2(lv, ones2, l_run, false);
+            }
+        }
+    };
+    // P.V per channel block: operands of steps 0, 1 from four transposing reads
+    auto pv = [&](auto boff_c, auto kc_c, const half8_t (&phi)[2], const half8_t (&plo)[2]) {
+        constexpr int BOFF = decltype(boff_c)::value, kc = decltype(kc_c)::value;
+        pf_static_for<0, 2>([&](auto mb_c) {
+            constexpr int mb = decltype(mb_c)::value;
+            u32x2_t vt[4];
+            pf_read_vt<BOFF + (int) TILE_BYTES + 4096 * kc>(vt, v_base[mb]);
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const half8_t va = __builtin_bit_cast(
+                    half8_t, (u32x4_t){vt[2 * s][0], vt[2 * s][1], vt[2 * s + 1][0], vt[2 * s + 1][1]});
+                O[mb] = pf_mfma(va, phi[s], O[mb]);
+                if constexpr (SPLIT_P) O[mb] = pf_mfma(va, plo[s], O[mb]);
+            }
+        });
+    };
+
+    // ---- one tile: 2 chunks of 32 keys, each skipped when no row of the wave sees it, masked when
+    // it crosses some row's span boundary (uniform branches)
+    auto compute_tile = [&](uint32_t kt, auto boff_c) {
+        const uint32_t j0 = kt * PF_KT;
+        pf_static_for<0, 2>([&](auto kc_c) {
             constexpr int kc = decltype(kc_c)::value;
-            const uint32_t j0 = kt * PF_KT + 32u * kc;
-            if (j0 > w_pmax || j0 + 31u < w_bmin) return;  // no row of this wave sees the chunk
-            // QK^T: S[kb2][rb] lane (g, n) reg i = key j0 + 16*kb2 + 4g + i, row 16*rb + n
-            u32x4_t kr[4];  // [kb2 * 2 + channel half]
-            pf_read_k<BOFF + 4096 * kc, BOFF + 4096 * kc + 2048>(kr, k_base0, k_base1);
-            float4_t S[2][2];
-#pragma unroll
-            for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
-                    float4_t s = (float4_t){0.f, 0.f, 0.f, 0.f};
-                    s = pf_mfma(__builtin_bit_cast(half8_t, kr[2 * kb2]), qop[rb][0], s);
-                    s = pf_mfma(__builtin_bit_cast(half8_t, kr[2 * kb2 + 1]), qop[rb][1], s);
-                    S[kb2][rb] = s;
-                }
-            }
-            // masks, only where the chunk crosses some row's span boundary (uniform branch):
-            // key j = j0 + 16*kb2 + 4g + i is outside row p's span [bp, p] iff
-            // (j - bp) > (p - bp) as unsigned
-            if (j0 + 31u > w_pmin || (a.n_swa && j0 < w_bmax)) {
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
-                    const uint32_t p = row_pos[rb];
-                    const uint32_t bp = a.n_swa ? (p + 1u > a.n_swa ? p + 1u - a.n_swa : 0u) : 0u;
-                    const uint32_t off = j0 + 4u * g - bp, span = p - bp;
-#pragma unroll
-                    for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (off + (16u * kb2 + i) > span) S[kb2][rb][i] = -INFINITY;
-                }
-            }
-            // softmax weights per row block; P^T operand item i = key 16*(i/4) + 4g + i%4
+            const uint32_t jc = j0 + 32u * kc;
+            if (jc > w_pmax || jc + 31u < w_bmin) return;
+            float16_t S = qk(boff_c, kc_c);
+            if (jc + 31u > w_pmin || (a.n_swa && jc < w_bmax)) mask(S, jc);
             half8_t phi[2], plo[2];
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                const float lmax = pf_max8(S[0][rb], S[1][rb]) * c;
-                if (__builtin_amdgcn_ballot_w64(lmax > m_run[rb] + PF_RESCALE_SLACK) != 0) {
-                    const float m_new = fmaxf(m_run[rb], pf_max16_32(lmax));
-                    const float corr = __builtin_amdgcn_exp2f(m_run[rb] - m_new);
-                    m_run[rb] = m_new;
-                    Lsum[rb] *= corr;
-#pragma unroll
-                    for (int mb = 0; mb < 4; ++mb) O[mb][rb] *= corr;
-                }
-                const float bias = PF_LOG2_PSCALE - m_run[rb];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float ps = __builtin_amdgcn_exp2f(fmaf(S[i >> 2][rb][i & 3], c, bias));
-                    const _Float16 hi = (_Float16) ps;
-                    phi[rb][i] = hi;
-                    if constexpr (SPLIT_P) plo[rb][i] = (_Float16) (ps - (float) hi);
-                }
-                Lsum[rb] = pf_mfma(ones, phi[rb], Lsum[rb]);
-                if constexpr (SPLIT_P) Lsum[rb] = pf_mfma(ones, plo[rb], Lsum[rb]);
-            }
-            // P.V: V^T operands of channel blocks 2mp, 2mp + 1, each from two transposing reads
-            pf_static_for<0, 2>([&](auto mp_c) {
-                constexpr int mp = decltype(mp_c)::value;
-                constexpr int VOFF = BOFF + (int) TILE_BYTES + 4096 * kc;
-                u32x2_t vt[4];  // [h2 * 2 + (keys +16)]
-                pf_read_vt<VOFF, VOFF + 2048>(vt, v_base[2 * mp], v_base[2 * mp + 1]);
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
-                    const int mb = 2 * mp + h2;
-                    const half8_t va = __builtin_bit_cast(
-                        half8_t, (u32x4_t){vt[2 * h2][0], vt[2 * h2][1], vt[2 * h2 + 1][0], vt[2 * h2 + 1][1]});
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb) {
-                        O[mb][rb] = pf_mfma(va, phi[rb], O[mb][rb]);
-                        if constexpr (SPLIT_P) O[mb][rb] = pf_mfma(va, plo[rb], O[mb][rb]);
-                    }
-                }
-            });
+            softmax(S, phi, plo);
+            pv(boff_c, kc_c, phi, plo);
         });
     };
 
@@ -305,7 +324,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
             copy_tile(kt + 1u, BUF ^ 1);
             if (kt + 1u < kt_last) load_pids(kt + 2u);
         }
-        compute_tile(kt, buf_c);
+        compute_tile(kt, std::integral_constant<int, BUF * (int) BUF_BYTES>{});
     };
     load_pids(kt_first);
     copy_tile(kt_first, 0);
@@ -315,23 +334,22 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
         if (kt + 1u <= kt_last) step(kt + 1u, std::integral_constant<int, 1>{});
     }
 
-    // ---- finalise: the sink, the normalisation, the store -----------------------------------
+    // ---- finalise: row sum over the lane pair, the sink, the normalisation, the store ---------
+    const float L = l_run + __shfl_xor(l_run, 32);
+    const float sink2 = a.sinks ? a.sinks[hd] * MOEARC_LOG2E : -INFINITY;
+    const float Mt = fmaxf(m_run, sink2);
+    const float fm = __builtin_amdgcn_exp2f(m_run - Mt);
+    const float inv = fm / (L * fm + __builtin_amdgcn_exp2f(sink2 - Mt + PF_LOG2_PSCALE));
+    if (row_ok) {
+        const uint64_t o = ((uint64_t) tok * a.n_heads + hd) * 64u;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const float L = Lsum[rb][0];  // every lane of the row holds the row's sum
-        const uint32_t r = wave * 32u + 16u * rb + n;
-        const uint32_t tok = q0 + r / GROUP, hd = kvh * GROUP + r % GROUP;
-        const float sink2 = a.sinks ? a.sinks[hd] * MOEARC_LOG2E : -INFINITY;
-        const float M = m_run[rb];
-        const float Mt = fmaxf(M, sink2);
-        const float fm = __builtin_amdgcn_exp2f(M - Mt);
-        const float inv = fm / (L * fm + __builtin_amdgcn_exp2f(sink2 - Mt + PF_LOG2_PSCALE));
-        if (tok < q_end) {
-            const uint64_t o = ((uint64_t) tok * a.n_heads + hd) * 64u;
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const float4_t v = O[mb][rb] * inv;
-                const uint32_t d = 16u * mb + 4u * g;
+            for (int j = 0; j < 4; ++j) {
+                // O reg 4j + i = channel 32mb + 8j + 4h + i of row n
+                const float4_t v = {O[mb][4 * j] * inv, O[mb][4 * j + 1] * inv, O[mb][4 * j + 2] * inv,
+                                    O[mb][4 * j + 3] * inv};
+                const uint32_t d = 32u * mb + 8u * j + 4u * h;
                 if (a.out_f16) {
                     half2_t h0 = {(_Float16) v[0], (_Float16) v[1]};
                     half2_t h1 = {(_Float16) v[2], (_Float16) v[3]};
@@ -341,7 +359,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
                     *(float4_t *) ((float *) a.out + o + d) = v;
                 }
             }
-        }
     }
 }
 
