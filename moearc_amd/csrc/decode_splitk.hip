@@ -11,9 +11,10 @@
 // wave takes 32-key tiles round-robin and keeps its own online-softmax state; the waves merge in
 // LDS. A sequence whose span fits one split is finished there (sink applied, output written);
 // otherwise each work-group writes a partial record (per-head max, denominator and unnormalised
-// output) and moearc_attn_decode_merge, the next launch on the stream, combines the splits.
-// Merging across work-groups inside one launch would need a device-scope release per
-// work-group -- an L2 write-back on every XCD, measured to cost more than the second launch.
+// output) with agent-coherent (sc1) stores. With an arrival counter per (sequence, KV-head block)
+// the last work-group to finish a block merges its splits inside the same launch (the fused
+// variant, few splits per block); otherwise moearc_attn_decode_merge, the next launch on the
+// stream, combines them.
 //
 // Per 32-key tile (one wave), all operands in registers, no LDS:
 //   loads   K and V rows go from HBM straight into MFMA A-operand layout: lane (g, m) loads 16
@@ -155,6 +156,15 @@ __device__ __forceinline__ void process_tile(SoftmaxState &st, const TileRegs &r
         st.O[mb] = mfma16(va, phi, st.O[mb]);
         st.O[mb] = mfma16(va, plo, st.O[mb]);
     }
+}
+
+// Agent-scope relaxed atomics on the partial records: global_store/load with sc1, coherent across
+// XCDs without an L2 write-back or invalidate.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store((uint32_t *) p, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __builtin_bit_cast(float, __hip_atomic_load((uint32_t *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // Final normalisation with the sink (kernels.cpp:1864-1880), in the log2 domain and the m-frame:
@@ -309,13 +319,62 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
             write_output(a, b, kv2 * group + hn, d, M, L, acc);
         } else {
             float *rec = a.ws + ((uint64_t) item * G + kv2) * MOEARC_PARTIAL_FLOATS;
-            rec[32u + e] = acc;
+            st_agent(rec + 32u + e, acc);
             if (d == 0) {
-                rec[hn] = M;
-                rec[16u + hn] = L;
+                st_agent(rec + hn, M);
+                st_agent(rec + 16u + hn, L);
             }
         }
     }
+    if (single || a.counters == nullptr) return;
+
+    // ---- fused merge: the last work-group of this (sequence, KV-head block) to arrive merges it --
+    // Every thread's record stores are complete at agent scope (sc1, waited for) before the arrival
+    // is counted; the last arrival therefore sees every record, which it reads with sc1 loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ uint32_t arrived;
+    uint32_t *ctr = a.counters + (uint64_t) b * nkb + kbi;
+    if (threadIdx.x == 0)
+        arrived = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != nsplit - 1u) return;
+    const uint64_t rstride = (uint64_t) G * MOEARC_PARTIAL_FLOATS;
+    constexpr int BATCH = 16;
+    for (uint32_t idx = threadIdx.x; idx < KB * n_out; idx += 64u * WAVES) {
+        const uint32_t k2 = idx / n_out, e = idx - k2 * n_out;
+        const uint32_t kv2 = kbi * KB + k2;
+        if (kv2 >= G) break;
+        const uint32_t hn = e >> 6, d = e & 63u;
+        const float *rec0 = a.ws + ((uint64_t) a.item_begin[b] * G + kv2) * MOEARC_PARTIAL_FLOATS;
+        float M = -INFINITY, L = 0.f, acc = 0.f;
+        for (uint32_t s0 = 0; s0 < nsplit; s0 += BATCH) {
+            float v[BATCH], ms[BATCH], ls[BATCH];
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const float *r = rec0 + min(s0 + (uint32_t) k, nsplit - 1u) * rstride;
+                v[k] = ld_agent(r + 32u + e);
+                ms[k] = ld_agent(r + hn);
+                ls[k] = ld_agent(r + 16u + hn);
+            }
+            float mr = M;
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) mr = fmaxf(mr, ms[k]);  // duplicates are harmless
+            const float corr = exp2_fast(M - mr);  // first batch: exp2(-inf) = 0
+            L *= corr;
+            acc *= corr;
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const float f = s0 + (uint32_t) k < nsplit ? exp2_fast(ms[k] - mr) : 0.f;
+                L = fmaf(ls[k], f, L);
+                acc = fmaf(v[k], f, acc);
+            }
+            M = mr;
+        }
+        write_output(a, b, kv2 * group + hn, d, M, L, acc);
+    }
+    // leave the counter at zero for the next launch (ordered before it by the kernel boundary)
+    if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Split merge: one work-group of MERGE_WAVES waves per (sequence, query head) of every sequence

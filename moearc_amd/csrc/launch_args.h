@@ -31,6 +31,8 @@ struct DecodeArgs {
     const float *sinks;           // [n_heads] or null
     void *out;                    // [n_seqs][n_heads][64], f32 or f16
     float *ws;                    // partial records, one per work-group
+    uint32_t *counters;           // [sequence][KV-head block] arrival counts, zero between launches;
+                                  // non-null: the last work-group of a block merges its splits
     uint64_t bt_stride;
     uint32_t n_heads;
     uint32_t n_kv_heads;

@@ -77,6 +77,8 @@ struct moearc_ctx {
     // split-K workspace: one partial record per work-group of the split kernel
     float *ws = nullptr;
     size_t ws_floats = 0;
+    uint32_t *counters = nullptr;  // fused-merge arrival counters
+    size_t counters_n = 0;
     int decode_variant_override = -1;  // MOEARC_DECODE_VARIANT, e.g. "4x4"
     unsigned long split_override = 0;  // MOEARC_DECODE_SPLIT (keys per split)
 };
@@ -157,6 +159,24 @@ int ensure_workspace(moearc_ctx *c, size_t floats) {
     return OK;
 }
 
+// Arrival counters of the fused decode merge. Each launch's last work-group per block resets its
+// counter, so they only need zeroing when allocated (by the zero kernel, on the stream).
+int ensure_counters(moearc_ctx *c, size_t n) {
+    if (n <= c->counters_n) return OK;
+    if (c->counters) {
+        hipStreamSynchronize(c->stream);
+        hipFree(c->counters);
+        c->counters = nullptr;
+        c->counters_n = 0;
+    }
+    n = std::max<size_t>(n, 1024);
+    if (hipMalloc((void **) &c->counters, n * sizeof(uint32_t)) != hipSuccess) return ERR;
+    const int rc = moearc_zero(c, (float *) c->counters, n);
+    if (rc) return rc;
+    c->counters_n = n;
+    return OK;
+}
+
 // ---- decode dispatch ----------------------------------------------------------------------------
 
 struct SeqSpan {
@@ -173,12 +193,20 @@ bool fast_decode_ok(unsigned long n_heads, unsigned long n_kv_heads, unsigned lo
 constexpr uint64_t kPageTableCap = 1024;
 
 // Split-K decode variants: KV heads per work-group x waves per KV head (moearc_attn_decode_f16d64_*).
+// Split-K decode variants: kb KV heads x wpk waves per work-group (kernel f_dec_fast[kernel]), the
+// work-group count the split length aims for, and whether the splits are merged inside the launch
+// (by the last work-group of each block to finish) rather than by the merge kernel.
 struct DecodeVariant {
     const char *name;
-    unsigned kb, wpk;
+    int kernel;
+    unsigned kb, wpk, target_wgs;
+    bool fused;
 };
-constexpr DecodeVariant kDecodeVariants[5] = {{"1x4", 1, 4}, {"1x16", 1, 16}, {"2x8", 2, 8},
-                                              {"4x4", 4, 4}, {"8x2", 8, 2}};
+constexpr int kNumDecodeVariants = 6;
+constexpr DecodeVariant kDecodeVariants[kNumDecodeVariants] = {
+    {"1x4", 0, 1, 4, 384, false},  {"1x16", 1, 1, 16, 384, false}, {"2x8", 2, 2, 8, 384, false},
+    {"4x4", 3, 4, 4, 384, false},  {"8x2", 4, 8, 2, 384, false},   {"1x4f", 0, 1, 4, 256, true},
+};
 
 // Variant and keys per split. A work-group reads kb*128 bytes of each key row (kb KV heads; four
 // keep HBM accesses row-local) with wpk waves per head; the split is sized so that the launch has
@@ -193,7 +221,7 @@ bool plan_split(moearc_ctx *c, const std::vector<SeqSpan> &spans, unsigned long 
     const uint64_t quantum = 32ull * wpk;  // one tile per wave
     uint64_t total = 0;
     for (auto &s : spans) total += (uint64_t) (s.end - s.begin) * nkb;
-    const uint64_t target_wgs = 384;
+    const uint64_t target_wgs = kDecodeVariants[variant].target_wgs;
     uint64_t base = (total + target_wgs - 1) / target_wgs;
     split_len.resize(spans.size());
     for (size_t i = 0; i < spans.size(); ++i) {
@@ -305,10 +333,15 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
         if (ensure_workspace(c, (size_t) items * n_kv_heads * MOEARC_PARTIAL_FLOATS)) return ERR;
         a.ws = c->ws;
         const bool any_split = items > cnt;  // some sequence has more than one split
-        const int rc = launch(c, c->f_dec_fast[variant], (unsigned) wgs, 64u * kb * wpk, a,
-                              "attn_decode.split", n_heads, head_dim);
+        const bool fused = kDecodeVariants[variant].fused && any_split;
+        if (fused) {
+            if (ensure_counters(c, cnt * nkb)) return ERR;
+            a.counters = c->counters;
+        }
+        const int rc = launch(c, c->f_dec_fast[kDecodeVariants[variant].kernel], (unsigned) wgs,
+                              64u * kb * wpk, a, "attn_decode.split", n_heads, head_dim);
         if (rc) return rc;
-        if (any_split) {
+        if (any_split && !fused) {
             const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads), 256, a,
                                   "attn_decode.merge", n_heads, head_dim);
             if (rm) return rm;
@@ -386,7 +419,7 @@ moearc_ctx *moearc_ctx_create(void) {
     const char *ev = std::getenv("MOEARC_PROFILE_EVENTS");
     c->profiling = ev && ev[0] == '1';
     if (const char *w = std::getenv("MOEARC_DECODE_VARIANT")) {
-        for (int i = 0; i < 5; ++i)
+        for (int i = 0; i < kNumDecodeVariants; ++i)
             if (std::strcmp(w, kDecodeVariants[i].name) == 0) c->decode_variant_override = i;
     }
     if (const char *s = std::getenv("MOEARC_DECODE_SPLIT")) c->split_override = std::strtoul(s, nullptr, 10);
@@ -402,6 +435,7 @@ void moearc_ctx_destroy(moearc_ctx *c) {
     }
     for (auto e : c->event_pool) hipEventDestroy(e);
     if (c->ws) hipFree(c->ws);
+    if (c->counters) hipFree(c->counters);
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;

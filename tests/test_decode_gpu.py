@@ -258,6 +258,18 @@ def test_forced_splits_and_variants(monkeypatch):
 
 
 def test_batched_ragged_decode(ctx):
+    _batched_ragged(ctx)
+
+
+def test_batched_ragged_decode_fused(monkeypatch):
+    # the same with the in-launch merge: one arrival counter per (sequence, KV head)
+    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "1x4f")
+    with Context() as cx:
+        _batched_ragged(cx)
+        _batched_ragged(cx)  # counters reset by the previous launches
+
+
+def _batched_ragged(ctx):
     # BASELINE config 3 in miniature: ragged lengths, 256-token pages in one shared pool through a
     # random page permutation, SWA-128 and full, f16 output option
     H, G, D, pt = 64, 8, 64, 256
@@ -306,3 +318,23 @@ def test_large_q_magnitudes(ctx):
         want = oracle.attn_decode(cq.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, 0, c.n_kv, c.pt,
                                   float(c.scale), kv_type=1, sinks=c.sinks)
         _report(f"q x {mult:g}", got, want, TOL_NS)
+
+
+@pytest.mark.parametrize("n_kv,kv_begin,pt,split", [(32768, 0, 256, 0), (5000, 123, 32, 0),
+                                                     (1500, 0, 16, 128), (9000, 8000, 64, 128)])
+def test_fused_merge_variant(monkeypatch, n_kv, kv_begin, pt, split):
+    """The fused variant merges the splits inside the launch (the last work-group of each KV head
+    to finish). Three calls per context, each on different data, so a stale record or a counter
+    left non-zero would show; the batched call covers several sequences' counters at once."""
+    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "1x4f")
+    if split:
+        monkeypatch.setenv("MOEARC_DECODE_SPLIT", str(split))
+    with Context() as cx:
+        for rep in range(3):
+            c = fx.north_star_case(0xF5E0 + 17 * rep + n_kv, n_kv, pt=pt)
+            b = _upload_case(cx, c)
+            got = _decode(cx, c, b, kv_begin)
+            want = oracle.attn_decode(c.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, kv_begin, n_kv, pt,
+                                      float(c.scale), kv_type=1, sinks=c.sinks)
+            _report(f"fused n_kv={n_kv} begin={kv_begin} pt={pt} split={split} rep={rep}", got, want,
+                    TOL_NS)
