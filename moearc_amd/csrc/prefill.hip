@@ -205,6 +205,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint8_t *k_src = (const uint8_t *) a.k_pages + kvh * 128u + ld_chunk * 16u;
     const uint8_t *v_src = (const uint8_t *) a.v_pages + kvh * 128u + ld_chunk_v * 16u;
     const bool wave_page = sh >= 4u;  // a wave's 16 keys of a tile lie in one page
+    // Wave-uniform KV-head bases, and this lane's byte offsets from the wave's first key of a tile
+    // (its keys (L >> 3) and 8 + (L >> 3) are consecutive slots of one page when wave_page holds).
+    const uint8_t *k_head = (const uint8_t *) a.k_pages + kvh * 128u;
+    const uint8_t *v_head = (const uint8_t *) a.v_pages + kvh * 128u;
+    const uint32_t k_lane0 = (uint32_t) ((lane >> 3) * row_bytes) + ld_chunk * 16u;
+    const uint32_t k_lane1 = k_lane0 + (uint32_t) (8u * row_bytes);
+    const uint32_t v_lane0 = (uint32_t) ((lane >> 3) * row_bytes) + ld_chunk_v * 16u;
+    const uint32_t v_lane1 = v_lane0 + (uint32_t) (8u * row_bytes);
     // block-table entries for the next tile: wave-uniform (wave_page) or this lane's two keys
     uint32_t pid[2];
     auto load_pids = [&](uint32_t kt) {
@@ -218,9 +226,21 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     };
     auto copy_tile = [&](uint32_t kt, int buf) {
         uint8_t *dst = tiles + buf * BUF_BYTES + 16u * wave * 128u;
+        const uint32_t kb = kt * PF_KT + 16u * wave;  // the wave's first key of the tile
+        if (wave_page && kb + 15u <= p_last) {
+            // all 16 keys exist and share a page: a wave-uniform base plus a fixed per-lane offset
+            const uint64_t base = (uint64_t) __builtin_amdgcn_readfirstlane((pid[0] << sh) | (kb & pmask)) * row_bytes;
+            const uint8_t *kb_ptr = k_head + base, *vb_ptr = v_head + base;
+            __builtin_amdgcn_global_load_lds(kb_ptr + k_lane0, dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vb_ptr + v_lane0, dst + TILE_BYTES, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(kb_ptr + k_lane1, dst + 8u * 128u, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vb_ptr + v_lane1, dst + 8u * 128u + TILE_BYTES, 16, 0, 0);
+            return;
+        }
+        // the last tile (keys past p_last are clamped to it) or pages of fewer than 16 tokens
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const uint32_t j = min(kt * PF_KT + ld_key + 8u * i, p_last);
+            const uint32_t j = min(kb + (lane >> 3) + 8u * i, p_last);
             const uint32_t p = wave_page ? pid[0] : pid[i];
             const uint64_t off = (uint64_t) ((p << sh) | (j & pmask)) * row_bytes;
             __builtin_amdgcn_global_load_lds(k_src + off, dst + 8u * i * 128u, 16, 0, 0);
