@@ -62,7 +62,8 @@
 #define PF_RESCALE_SLACK 8.0f
 #define PF_M_INIT -1.0e30f  // finite "no key yet": keeps exp2(m_old - m_new) defined for rows
                             // whose keys all lie in later chunks
-#define PF_KT 64            // keys per LDS tile
+#define PF_KT 32            // keys per LDS tile (one chunk)
+#define PF_NBUF 4           // tile buffers in LDS: copies run PF_NBUF - 1 tiles ahead
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -126,7 +127,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     constexpr uint32_t TOK = ROWS / GROUP;          // query tokens per work-group
     constexpr uint32_t TILE_BYTES = PF_KT * 128u;   // one K or V tile
     constexpr uint32_t BUF_BYTES = 2u * TILE_BYTES;  // K tile, V tile
-    __shared__ __attribute__((aligned(1024))) uint8_t tiles[2 * BUF_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t tiles[PF_NBUF * BUF_BYTES];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -196,56 +197,28 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
             v_base[mb] = lds0 + v_off(vkey, 4u * mb + 2u * q + ((r >> 1) & 1u)) + ((r & 1u) << 3);
     }
 
-    // ---- tile copies: lane L of wave w fills LDS chunk slot L & 7 of key k = 16w + 8i + (L >> 3)
-    // (i = 0, 1) of the K and the V tile; that slot holds chunk (L & 7) ^ f(k) of the key (f(k)
-    // depends on k & 7 = L >> 3 and, for K, on bit 4 of k = w & 1).
-    const uint32_t ld_key = 16u * wave + (lane >> 3);
+    // ---- tile copies: lane L of wave w fills LDS chunk slot L & 7 of key k = 8w + (L >> 3) of the
+    // K and the V tile; that slot holds chunk (L & 7) ^ f(k) of the key.
+    const uint32_t ld_key = 8u * wave + (lane >> 3);
     const uint32_t ld_chunk = (lane & 7u) ^ k_swz(ld_key), ld_chunk_v = (lane & 7u) ^ v_swz(ld_key);
     const uint64_t row_bytes = (uint64_t) G * 128u;
     const uint8_t *k_src = (const uint8_t *) a.k_pages + kvh * 128u + ld_chunk * 16u;
     const uint8_t *v_src = (const uint8_t *) a.v_pages + kvh * 128u + ld_chunk_v * 16u;
-    const bool wave_page = sh >= 4u;  // a wave's 16 keys of a tile lie in one page
-    // Wave-uniform KV-head bases, and this lane's byte offsets from the wave's first key of a tile
-    // (its keys (L >> 3) and 8 + (L >> 3) are consecutive slots of one page when wave_page holds).
-    const uint8_t *k_head = (const uint8_t *) a.k_pages + kvh * 128u;
-    const uint8_t *v_head = (const uint8_t *) a.v_pages + kvh * 128u;
-    const uint32_t k_lane0 = (uint32_t) ((lane >> 3) * row_bytes) + ld_chunk * 16u;
-    const uint32_t k_lane1 = k_lane0 + (uint32_t) (8u * row_bytes);
-    const uint32_t v_lane0 = (uint32_t) ((lane >> 3) * row_bytes) + ld_chunk_v * 16u;
-    const uint32_t v_lane1 = v_lane0 + (uint32_t) (8u * row_bytes);
-    // block-table entries for the next tile: wave-uniform (wave_page) or this lane's two keys
-    uint32_t pid[2];
-    auto load_pids = [&](uint32_t kt) {
-        if (wave_page) {
-            const uint32_t kb = min(kt * PF_KT + 16u * wave, p_last);
-            pid[0] = __builtin_amdgcn_readfirstlane(a.block_table[__builtin_amdgcn_readfirstlane(kb >> sh)]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) pid[i] = a.block_table[min(kt * PF_KT + ld_key + 8u * i, p_last) >> sh];
-        }
+    // Block-table entry of this lane's key of tile kt (keys past p_last are clamped to it, so no copy
+    // reads a slot the cache has not written), issued through asm: the pipeline below waits for it
+    // explicitly, and the compiler's own tracking would add conservative waits in the loop.
+    auto key_of = [&](uint32_t kt) { return min(kt * PF_KT + ld_key, p_last); };
+    auto load_pid = [&](uint32_t kt) -> uint32_t {
+        const uint32_t *p = a.block_table + (key_of(kt) >> sh);
+        uint32_t v;
+        asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+        return v;
     };
-    auto copy_tile = [&](uint32_t kt, int buf) {
-        uint8_t *dst = tiles + buf * BUF_BYTES + 16u * wave * 128u;
-        const uint32_t kb = kt * PF_KT + 16u * wave;  // the wave's first key of the tile
-        if (wave_page && kb + 15u <= p_last) {
-            // all 16 keys exist and share a page: a wave-uniform base plus a fixed per-lane offset
-            const uint64_t base = (uint64_t) __builtin_amdgcn_readfirstlane((pid[0] << sh) | (kb & pmask)) * row_bytes;
-            const uint8_t *kb_ptr = k_head + base, *vb_ptr = v_head + base;
-            __builtin_amdgcn_global_load_lds(kb_ptr + k_lane0, dst, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vb_ptr + v_lane0, dst + TILE_BYTES, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(kb_ptr + k_lane1, dst + 8u * 128u, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vb_ptr + v_lane1, dst + 8u * 128u + TILE_BYTES, 16, 0, 0);
-            return;
-        }
-        // the last tile (keys past p_last are clamped to it) or pages of fewer than 16 tokens
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t j = min(kb + (lane >> 3) + 8u * i, p_last);
-            const uint32_t p = wave_page ? pid[0] : pid[i];
-            const uint64_t off = (uint64_t) ((p << sh) | (j & pmask)) * row_bytes;
-            __builtin_amdgcn_global_load_lds(k_src + off, dst + 8u * i * 128u, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(v_src + off, dst + 8u * i * 128u + TILE_BYTES, 16, 0, 0);
-        }
+    auto copy_tile = [&](uint32_t kt, uint32_t pid, int buf) {
+        uint8_t *dst = tiles + buf * BUF_BYTES + 8u * wave * 128u;
+        const uint64_t off = (uint64_t) ((pid << sh) | (key_of(kt) & pmask)) * row_bytes;
+        __builtin_amdgcn_global_load_lds(k_src + off, dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(v_src + off, dst + TILE_BYTES, 16, 0, 0);
     };
 
     // ---- chunk stages ----------------------------------------------------------------------------
@@ -318,41 +291,58 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
         });
     };
 
-    // ---- one tile: 2 chunks of 32 keys, each skipped when no row of the wave sees it, masked when
-    // it crosses some row's span boundary (uniform branches)
+    // ---- one tile (= one chunk): skipped when no row of the wave sees it, masked when it crosses
+    // some row's span boundary (uniform branches)
     auto compute_tile = [&](uint32_t kt, auto boff_c) {
-        const uint32_t j0 = kt * PF_KT;
-        pf_static_for<0, 2>([&](auto kc_c) {
-            constexpr int kc = decltype(kc_c)::value;
-            const uint32_t jc = j0 + 32u * kc;
-            if (jc > w_pmax || jc + 31u < w_bmin) return;
-            float16_t S = qk(boff_c, kc_c);
-            if (jc + 31u > w_pmin || (a.n_swa && jc < w_bmax)) mask(S, jc);
-            half8_t phi[2], plo[2];
-            softmax(S, phi, plo);
-            pv(boff_c, kc_c, phi, plo);
-        });
+        const uint32_t jc = kt * PF_KT;
+        if (jc > w_pmax || jc + 31u < w_bmin) return;
+        using K0 = std::integral_constant<int, 0>;
+        float16_t S = qk(boff_c, K0{});
+        if (jc + 31u > w_pmin || (a.n_swa && jc < w_bmax)) mask(S, jc);
+        half8_t phi[2], plo[2];
+        softmax(S, phi, plo);
+        pv(boff_c, K0{}, phi, plo);
     };
 
-    // ---- pipeline: tile kt in buffer kt & 1; tile kt + 1 is copied into the other buffer while
-    // kt is computed
-    auto step = [&](uint32_t kt, auto buf_c) {
-        constexpr int BUF = decltype(buf_c)::value;
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile kt (and the next entries)
-        __builtin_amdgcn_s_barrier();   // everyone's copies landed; everyone is done with kt - 1
-        if (kt < kt_last) {
-            copy_tile(kt + 1u, BUF ^ 1);
-            if (kt + 1u < kt_last) load_pids(kt + 2u);
-        }
-        compute_tile(kt, std::integral_constant<int, BUF * (int) BUF_BYTES>{});
-    };
-    load_pids(kt_first);
-    copy_tile(kt_first, 0);
-    if (kt_first < kt_last) load_pids(kt_first + 1u);
-    for (uint32_t kt = kt_first; kt <= kt_last; kt += 2u) {
-        step(kt, std::integral_constant<int, 0>{});
-        if (kt + 1u <= kt_last) step(kt + 1u, std::integral_constant<int, 1>{});
+    // ---- pipeline over tiles kt_first + r, r = 0..nt-1, tile r in buffer r % PF_NBUF ------------
+    // Per step r: wait until this wave's copies of tile r (and the block-table entry for tile r + 3)
+    // have landed, meet the other waves (so every wave's copies of tile r are in, and every wave is
+    // done with tile r - 1, whose buffer is reused), copy tile r + 3 into that buffer, load the entry
+    // for tile r + 6, compute tile r. Indices past the last tile are clamped: those copies go to
+    // buffers no later step reads, and every step issues the same three memory operations, so the
+    // wait is a constant -- the six operations issued after the entry of tile r + 3 may be pending.
+    const uint32_t nt = kt_last - kt_first + 1u;
+    auto tile = [&](uint32_t r) { return kt_first + min(r, nt - 1u); };
+    uint32_t pid[PF_NBUF];  // entries of tiles r + 3, r + 4, r + 5 (ring indexed by r % PF_NBUF)
+    pid[0] = load_pid(tile(0));
+    pid[1] = load_pid(tile(1));
+    pid[2] = load_pid(tile(2));
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(pid[0]), "+v"(pid[1]), "+v"(pid[2]) : : "memory");
+    copy_tile(tile(0), pid[0], 0);
+    pid[3] = load_pid(tile(3));
+    copy_tile(tile(1), pid[1], 1);
+    pid[0] = load_pid(tile(4));
+    copy_tile(tile(2), pid[2], 2);
+    pid[1] = load_pid(tile(5));
+    for (uint32_t r = 0; r < nt; r += PF_NBUF) {
+        bool done = false;
+        pf_static_for<0, PF_NBUF>([&](auto k_c) {
+            constexpr int k = decltype(k_c)::value;
+            if (done || r + k >= nt) {
+                done = true;
+                return;
+            }
+            // vmcnt(6), tied to the entry it makes valid so no use of it is scheduled above the wait
+            asm volatile("s_waitcnt vmcnt(6)" : "+v"(pid[(k + 3) % PF_NBUF]) : : "memory");
+            __builtin_amdgcn_s_barrier();
+            copy_tile(tile(r + k + 3u), pid[(k + 3) % PF_NBUF], (k + 3) % PF_NBUF);
+            pid[(k + 2) % PF_NBUF] = load_pid(tile(r + k + 6u));
+            compute_tile(tile(r + k), std::integral_constant<int, k * (int) BUF_BYTES>{});
+        });
     }
+    // the clamped copies past the last tile may still be in flight: they must land before this
+    // work-group's LDS is released
+    __builtin_amdgcn_s_waitcnt(0);
 
     // ---- finalise: row sum over the lane pair, the sink, the normalisation, the store ---------
     const float L = l_run + __shfl_xor(l_run, 32);
