@@ -14,6 +14,8 @@ call. Inputs are N(0,1) from a seed (synthetic data; there is no model).
   summary (profiles/decode_c2_pmc.md), when present.
 * prefill: BASELINE config 4 (2048 new + 2048 cached tokens), full causal and SWA-128, MFMA
   utilisation = algorithmic flops / time / 2.5 PFLOP/s (dense f16).
+* rope_kv_append_chunk: the fused RoPE-K + f16 K/V append of the same config-4 chunk (HBM-bound;
+  bytes = f32 K/V in + f16 K/V out + position/page/slot per token).
 * cpu_baseline: the CPU oracle (a C restatement of the reference's f64 CPU twin,
   reference.rs:821-873, plus the sink) timed on this host on a bounded sample of the same decode.
 
@@ -230,7 +232,56 @@ def bench_prefill(ctx, steps, warmup):
             bound_us = max(PF_BYTES_SWA / (HBM_PEAK_GBS * 1e3), flops / (MFMA_F16_PEAK_TFLOPS * 1e6))
             entry.update({"hbm_gbs": round(gbs, 0), "roofline_frac": round(bound_us / us, 4)})
         out[name] = entry
+    out["rope_kv_append_chunk"] = bench_rope_append(ctx, steps, warmup)
     return out
+
+
+def rope_append_inputs(ctx, copies):
+    """Device inputs for the fused RoPE-K + K/V append of one config-4 chunk (2048 tokens after
+    2048 cached, 8 KV heads x 64, 256-token pages), in ``copies`` independent sets so that repeated
+    launches stream from HBM rather than the 256 MB Infinity Cache."""
+    n, row = PF_NQ, G * D
+    rng = np.random.default_rng(0xA11)
+    k = rng.standard_normal(n * row).astype(np.float32)
+    v = rng.standard_normal(n * row).astype(np.float32)
+    pos = (PF_POS0 + np.arange(n)).astype(np.int32)
+    n_pages = (PF_POS0 + n) // PT
+    pages, slots = (pos // PT).astype(np.uint32), (pos % PT).astype(np.uint32)
+    meta = ctx.upload(pos), ctx.upload(pages), ctx.upload(slots)
+    sets = [(ctx.upload(k), ctx.upload(v), ctx.alloc(n_pages * PT * row * 2),
+             ctx.alloc(n_pages * PT * row * 2)) for _ in range(copies)]
+    return sets, meta
+
+
+def rope_append_launch(ctx, sets, meta, i):
+    from moearc_amd import KvType, RopeKind, RopeScaling
+    dk, dv, kp, vp = sets[i % len(sets)]
+    dpos, dpg, dsl = meta
+    ctx.rope_kv_append_chunk(kp, vp, dk, dv, dpos, dpg, dsl, PF_NQ, G, D, PT, D, 150000.0,
+                             scaling=RopeScaling.yarn(D, 4096, 150000.0, 32.0), kind=RopeKind.NEOX,
+                             kv=KvType.F16)
+
+
+# algorithmic bytes of one chunk append: f32 K and V read, f16 K and V written, and the per-token
+# position, page id and slot (4 bytes each)
+RA_BYTES = PF_NQ * G * D * (4 + 4 + 2 + 2) + PF_NQ * 12
+
+
+def bench_rope_append(ctx, steps, warmup):
+    """The fused RoPE-K + f16 K/V append (HBM-bound) timed with the library's events."""
+    sets, meta = rope_append_inputs(ctx, 24)
+    for i in range(warmup + steps):
+        if i == warmup:
+            ctx.sync()
+            ctx.profile_events_reset()
+        rope_append_launch(ctx, sets, meta, i)
+    ctx.sync()
+    rep = ctx.profile_events_report()
+    key = [k2 for k2 in rep if k2.startswith("rope_kv_append_chunk")][0]
+    us = rep[key][0] / rep[key][1] / 1e3
+    gbs = RA_BYTES / us / 1e3
+    return {"us": round(us, 2), "bytes": RA_BYTES, "hbm_gbs": round(gbs, 0),
+            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline(kp, vp, bt, q, sinks):
@@ -264,7 +315,8 @@ def cpu_baseline(kp, vp, bt, q, sinks):
 
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
-    decode (C2), prefill (C4 full then SWA-128), or copy (a 256 MiB device-to-device copy, the
+    decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
+    C4 chunk), or copy (a 256 MiB device-to-device copy, the
     reference size for scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
     from moearc_amd import Context, KvType, OUT_F16
     with Context() as ctx:
@@ -288,6 +340,10 @@ def only(what, steps, warmup):
                 for i in range(warmup + steps):
                     ctx.attn_prefill(dout, dq, dk, dv, dbt, ds, PF_NQ, PF_POS0, n_swa, H, G, D, PT,
                                      0.125, KvType.F16, out_type=OUT_F16)
+        elif what == "rope_append":
+            sets, meta = rope_append_inputs(ctx, 24)
+            for i in range(warmup + steps):
+                rope_append_launch(ctx, sets, meta, i)
         elif what == "copy":
             hip = Hip()
             n = 256 << 20
@@ -308,7 +364,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy"],
+    ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -139,6 +139,32 @@ int moearc_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const fl
                            unsigned long n_tok, unsigned long n_kv_heads, unsigned long head_dim,
                            unsigned long page_tokens, unsigned int kv_type);
 
+/* Rotary position embedding, ffi.rs:236-252 / kernels.cpp:1399-1468 (ggml's rope_yarn):
+ * dst, src f32 [n_tokens][n_heads][head_dim] (dst may equal src), pos i32 [n_tokens] (device).
+ * Pairs (p, p + n_dims/2) when neox != 0, else (2p, 2p + 1), rotated by
+ * theta = pos * freq_base^(-2p/n_dims) with YaRN interpolation (freq_scale, ext_factor, corr_lo,
+ * corr_hi) and magnitude scale attn_factor (times 1 + 0.1 ln(1/freq_scale) when ext_factor != 0);
+ * channels >= n_dims pass through. freq_scale 1, ext_factor 0, attn_factor 1 is plain RoPE.
+ * Returns -1 on a null pointer; -2 when n_dims is 0, odd or larger than head_dim; 0 (nothing
+ * enqueued) for zero tokens or heads. */
+int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
+                unsigned long n_tokens, unsigned long n_heads, unsigned long head_dim,
+                unsigned long n_dims, float freq_base, float freq_scale, float ext_factor,
+                float attn_factor, float corr_lo, float corr_hi, int neox);
+
+/* Extension (no counterpart in the reference, which rotates K with moearc_rope and then appends
+ * it with moearc_kv_append once per token, moe.rs:1987-2042): K rotated exactly as moearc_rope
+ * would, then K and V written as moearc_kv_append_chunk would, in one pass over a prefill chunk.
+ * k, v f32 [n_tok][n_kv_heads][head_dim]; pos i32 [n_tok]; page_ids, slots u32 [n_tok] (all
+ * device). Refusals: those of moearc_rope, then those of moearc_kv_append_chunk. */
+int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
+                                const float *v, const int *pos, const unsigned int *page_ids,
+                                const unsigned int *slots, unsigned long n_tok,
+                                unsigned long n_kv_heads, unsigned long head_dim,
+                                unsigned long page_tokens, unsigned long n_dims, float freq_base,
+                                float freq_scale, float ext_factor, float attn_factor,
+                                float corr_lo, float corr_hi, int neox, unsigned int kv_type);
+
 /* The stream the context enqueues on (a hipStream_t), so a caller can order its own work. */
 void *moearc_ctx_stream(moearc_ctx *c);
 

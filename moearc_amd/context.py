@@ -60,6 +60,37 @@ OUT_F32 = 0
 OUT_F16 = 1
 
 
+class RopeKind(enum.IntEnum):
+    """Pairing of rotated channels (reference.rs:451-457): NORMAL (2p, 2p+1), NEOX (p, p + n_dims/2)."""
+    NORMAL = 0
+    NEOX = 1
+
+
+class RopeScaling:
+    """YaRN parameters as the RoPE kernel takes them (reference.rs:536-590)."""
+
+    def __init__(self, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, corr_lo=0.0, corr_hi=0.0):
+        self.freq_scale, self.ext_factor, self.attn_factor = freq_scale, ext_factor, attn_factor
+        self.corr_lo, self.corr_hi = corr_lo, corr_hi
+
+    @classmethod
+    def yarn(cls, n_dims, n_ctx_orig, freq_base, factor, beta_fast=32.0, beta_slow=1.0):
+        """From the GGUF keys and the model geometry: ggml_rope_yarn_corr_dims (reference.rs:573-590)."""
+        f32 = np.float32
+
+        def corr(beta):
+            return f32(f32(n_dims) * np.log(f32(n_ctx_orig) / (f32(beta) * f32(2.0) * f32(np.pi)))
+                       / (f32(2.0) * np.log(f32(freq_base))))
+        return cls(float(f32(1.0) / f32(factor)), 1.0, 1.0, float(max(np.floor(corr(beta_fast)), 0.0)),
+                   float(min(np.ceil(corr(beta_slow)), n_dims - 1.0)))
+
+    def args(self):
+        return (self.freq_scale, self.ext_factor, self.attn_factor, self.corr_lo, self.corr_hi)
+
+
+RopeScaling.NONE = RopeScaling()
+
+
 class DeviceBuffer:
     """An owned device allocation (lib.rs ``DeviceBuffer``)."""
 
@@ -228,6 +259,39 @@ class Context:
                                               page_ids.ptr, slots.ptr, n_tok, n_kv_heads,
                                               head_dim, page_tokens, int(KvType(kv)))
         self.finish(rc, "KV chunk append")
+
+    def rope(self, dst: DeviceBuffer, src: DeviceBuffer, pos: DeviceBuffer, n_tokens: int,
+             n_heads: int, head_dim: int, n_dims: int, freq_base: float,
+             scaling: Optional[RopeScaling] = None, kind: RopeKind = RopeKind.NEOX) -> None:
+        """RoPE with optional YaRN (lib.rs:834-870): dst, src f32 [n_tokens][n_heads][head_dim]."""
+        n = n_tokens * n_heads * head_dim
+        src.require("rope input", n * 4)
+        dst.require("rope output", n * 4)
+        pos.require("rope positions", n_tokens * 4)
+        sc = scaling or RopeScaling.NONE
+        rc = self._lib.moearc_rope(self.raw, dst.ptr, src.ptr, pos.ptr, n_tokens, n_heads, head_dim,
+                                   n_dims, freq_base, *sc.args(), int(RopeKind(kind)))
+        self.finish(rc, "rope")
+
+    def rope_kv_append_chunk(self, k_pages: DeviceBuffer, v_pages: DeviceBuffer, k: DeviceBuffer,
+                             v: DeviceBuffer, pos: DeviceBuffer, page_ids: DeviceBuffer,
+                             slots: DeviceBuffer, n_tok: int, n_kv_heads: int, head_dim: int,
+                             page_tokens: int, n_dims: int, freq_base: float,
+                             scaling: Optional[RopeScaling] = None,
+                             kind: RopeKind = RopeKind.NEOX, kv: KvType = KvType.F16) -> None:
+        """K rotated as rope() would, then K and V appended as kv_append_chunk() would, in one pass."""
+        row = n_kv_heads * head_dim
+        k.require("key rows", n_tok * row * 4)
+        v.require("value rows", n_tok * row * 4)
+        pos.require("rope positions", n_tok * 4)
+        page_ids.require("page ids", n_tok * 4)
+        slots.require("slots", n_tok * 4)
+        sc = scaling or RopeScaling.NONE
+        rc = self._lib.moearc_rope_kv_append_chunk(
+            self.raw, k_pages.ptr, v_pages.ptr, k.ptr, v.ptr, pos.ptr, page_ids.ptr, slots.ptr,
+            n_tok, n_kv_heads, head_dim, page_tokens, n_dims, freq_base, *sc.args(),
+            int(RopeKind(kind)), int(KvType(kv)))
+        self.finish(rc, "RoPE + KV chunk append")
 
     def attn_decode(self, out, q, k_pages, v_pages, block_table, n_heads, n_kv_heads, head_dim,
                     n_kv, page_tokens, scale, kv) -> None:

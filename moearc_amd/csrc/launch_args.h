@@ -92,3 +92,16 @@ struct PrefillArgs {
     float scale_log2e;
     uint32_t n_qtiles;            // query tiles per KV head
 };
+
+// RoPE parameters (moearc_rope, moearc_rope_kv_append_chunk): theta_scale = freq_base^(-2/n_dims),
+// computed on the host; neox selects the (p, p + n_dims/2) pairing, else (2p, 2p + 1).
+struct RopeParams {
+    uint32_t n_dims;
+    uint32_t neox;
+    float theta_scale;
+    float freq_scale;
+    float ext_factor;
+    float attn_factor;
+    float corr_lo;
+    float corr_hi;
+};

@@ -4,3 +4,4 @@
 #include "decode_general.hip"
 #include "decode_splitk.hip"
 #include "prefill.hip"
+#include "rope.hip"

@@ -1,0 +1,124 @@
+// Rotary position embedding (NeoX or adjacent-pair convention, YaRN context extension), and the
+// same rotation fused into the f16 K/V append of a prefill chunk.
+//
+// Semantics are moearc_rope's (kernels.cpp:1385-1468), which follow ggml's rope_yarn: for pair
+// index p (channels (p, p + n_dims/2) with NeoX, (2p, 2p + 1) otherwise),
+//   theta_extrap = pos * theta_scale^p,   theta_scale = freq_base^(-2/n_dims) (computed on the host)
+//   theta        = freq_scale * theta_extrap
+//   with YaRN (ext_factor != 0):  ramp  = 1 - clamp((p - corr_lo) / max(0.001, corr_hi - corr_lo), 0, 1)
+//                                 theta = theta * (1 - ramp*ext) + theta_extrap * ramp*ext
+//                                 mscale = attn_factor * (1 + 0.1 ln(1/freq_scale))
+//   (x0, x1) -> (x0 cos - x1 sin, x0 sin + x1 cos) * mscale
+// Channels at or above n_dims pass through unchanged. The angle is the closed form (each thread
+// independent), as the reference's kernel computes it; cos and sin are the accurate library
+// functions (full range reduction), since positions reach 10^5 radians.
+//
+// One thread per (token, head, pair): it computes the angle once and writes both channels of the
+// pair -- for the fused append, of K (rotated) and V (copied), as f16 with the reference's rounding.
+#include "common.h"
+
+// f32_to_f16_bits: kernels_misc.hip (same translation unit).
+
+// Rotation factors (cos, sin, both scaled by mscale) of pair p at position pos.
+__device__ __forceinline__ float2_t rope_factors(const RopeParams &r, int pos, uint32_t p) {
+    const float theta_extrap = (float) pos * powf(r.theta_scale, (float) p);
+    float theta = r.freq_scale * theta_extrap;
+    float mscale = r.attn_factor;
+    if (r.ext_factor != 0.0f) {
+        const float y = ((float) p - r.corr_lo) / fmaxf(0.001f, r.corr_hi - r.corr_lo);
+        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * r.ext_factor;
+        theta = theta * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / r.freq_scale);
+    }
+    float s, c;
+    sincosf(theta, &s, &c);
+    return (float2_t){c * mscale, s * mscale};
+}
+
+// Channels (lo, hi) handled by pair slot j of a head_dim-wide row: rotated pairs first, then the
+// pass-through channels two at a time.
+__device__ __forceinline__ void pair_channels(const RopeParams &r, uint32_t j, uint32_t &lo, uint32_t &hi) {
+    const uint32_t half = r.n_dims >> 1;
+    if (j < half) {
+        lo = r.neox ? j : 2u * j;
+        hi = r.neox ? j + half : 2u * j + 1u;
+    } else {
+        lo = r.n_dims + 2u * (j - half);
+        hi = lo + 1u;
+    }
+}
+
+// moearc_rope: src/dst f32 [n_tokens][n_heads][head_dim].
+extern "C" __global__ void moearc_rope_k(float *dst, const float *src, const int *pos,
+                                         uint64_t n_tokens, uint32_t n_heads, uint32_t head_dim,
+                                         RopeParams r) {
+    const uint32_t slots = (head_dim + 1u) >> 1;  // pair slots per head (head_dim may be odd)
+    const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_tokens * n_heads * slots) return;
+    const uint32_t j = (uint32_t) (g % slots);
+    const uint64_t th = g / slots;  // token * n_heads + head
+    const uint64_t t = th / n_heads;
+    const float *s = src + th * head_dim;
+    float *o = dst + th * head_dim;
+    uint32_t lo, hi;
+    pair_channels(r, j, lo, hi);
+    if (j < (r.n_dims >> 1)) {
+        const float2_t cs = rope_factors(r, pos[t], j);
+        const float x0 = s[lo], x1 = s[hi];
+        o[lo] = x0 * cs[0] - x1 * cs[1];
+        o[hi] = x0 * cs[1] + x1 * cs[0];
+    } else {
+        o[lo] = s[lo];
+        if (hi < head_dim) o[hi] = s[hi];
+    }
+}
+
+// A prefill chunk's K (rotated) and V to (page_ids[t], slots[t]); k, v f32 [n_tok][n_kv_heads][head_dim].
+// A slot outside the page is skipped, as in moearc_kv_append_chunk.
+extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_pages, const float *k,
+                                                         const float *v, const int *pos,
+                                                         const uint32_t *page_ids, const uint32_t *slots,
+                                                         uint64_t n_tok, uint32_t n_kv_heads,
+                                                         uint32_t head_dim, uint64_t page_tokens,
+                                                         uint32_t kv_type, RopeParams r) {
+    const uint32_t nslot = (head_dim + 1u) >> 1;
+    const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_tok * n_kv_heads * nslot) return;
+    const uint32_t j = (uint32_t) (g % nslot);
+    const uint64_t th = g / nslot;
+    const uint64_t t = th / n_kv_heads;
+    const uint32_t h = (uint32_t) (th - t * n_kv_heads);
+    const uint32_t slot = slots[t];
+    if (slot >= page_tokens) return;
+    const float *ks = k + th * head_dim;
+    const float *vs = v + th * head_dim;
+    const uint64_t dst = (((uint64_t) page_ids[t] * page_tokens + slot) * n_kv_heads + h) * head_dim;
+    uint32_t lo, hi;
+    pair_channels(r, j, lo, hi);
+    float k0 = ks[lo], k1 = 0.f;
+    const bool has_hi = hi < head_dim;
+    if (has_hi) k1 = ks[hi];
+    if (j < (r.n_dims >> 1)) {
+        const float2_t cs = rope_factors(r, pos[t], j);
+        const float x0 = k0, x1 = k1;
+        k0 = x0 * cs[0] - x1 * cs[1];
+        k1 = x0 * cs[1] + x1 * cs[0];
+    }
+    if (kv_type == MOEARC_KV_F16) {
+        uint16_t *kp = (uint16_t *) k_pages + dst, *vp = (uint16_t *) v_pages + dst;
+        kp[lo] = f32_to_f16_bits(k0);
+        vp[lo] = f32_to_f16_bits(vs[lo]);
+        if (has_hi) {
+            kp[hi] = f32_to_f16_bits(k1);
+            vp[hi] = f32_to_f16_bits(vs[hi]);
+        }
+    } else {
+        float *kp = (float *) k_pages + dst, *vp = (float *) v_pages + dst;
+        kp[lo] = k0;
+        vp[lo] = vs[lo];
+        if (has_hi) {
+            kp[hi] = k1;
+            vp[hi] = vs[hi];
+        }
+    }
+}

@@ -9,6 +9,8 @@
 // Built with the host compiler against the HIP runtime API only; no device code lives here.
 #include "moearc_attn.h"
 
+#include <cmath>
+
 #include <hip/hip_runtime_api.h>
 
 #include <dlfcn.h>
@@ -65,6 +67,7 @@ struct moearc_ctx {
     hipStream_t stream = nullptr;
     hipModule_t module = nullptr;
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
+    hipFunction_t f_rope = nullptr, f_rope_append_chunk = nullptr;
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[5] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2
     hipFunction_t f_dec_merge = nullptr;
@@ -386,6 +389,8 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_quant, "moearc_quantize_f16_k"},
         {&c->f_append, "moearc_kv_append_k"},
         {&c->f_append_chunk, "moearc_kv_append_chunk_k"},
+        {&c->f_rope, "moearc_rope_k"},
+        {&c->f_rope_append_chunk, "moearc_rope_kv_append_chunk_k"},
         {&c->f_dec_general, "moearc_attn_decode_general_k"},
         {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k1w4"},
         {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w16"},
@@ -439,6 +444,76 @@ void moearc_ctx_destroy(moearc_ctx *c) {
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
+}
+
+// The host computes theta_scale as the reference does before its launch (kernels.cpp:1406).
+static RopeParams rope_params(unsigned long n_dims, float freq_base, float freq_scale,
+                              float ext_factor, float attn_factor, float corr_lo, float corr_hi,
+                              int neox) {
+    RopeParams r{};
+    r.n_dims = (uint32_t) n_dims;
+    r.neox = neox ? 1u : 0u;
+    r.theta_scale = std::pow(freq_base, -2.0f / (float) n_dims);
+    r.freq_scale = freq_scale;
+    r.ext_factor = ext_factor;
+    r.attn_factor = attn_factor;
+    r.corr_lo = corr_lo;
+    r.corr_hi = corr_hi;
+    return r;
+}
+
+int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
+                unsigned long n_tokens, unsigned long n_heads, unsigned long head_dim,
+                unsigned long n_dims, float freq_base, float freq_scale, float ext_factor,
+                float attn_factor, float corr_lo, float corr_hi, int neox) {
+    if (!c || !dst || !src || !pos) return ERR;
+    if (n_dims == 0 || n_dims % 2 != 0 || n_dims > head_dim) return ERR_ARG;
+    if (n_tokens == 0 || n_heads == 0) return OK;
+    if (head_dim > 0xFFFFFFFFul || n_heads > 0xFFFFFFFFul) return ERR_ARG;
+    const uint64_t threads = (uint64_t) n_tokens * n_heads * ((head_dim + 1) / 2);
+    if (threads / 256 >= 0xFFFFFFFFull) return ERR_ARG;
+    struct {
+        float *dst;
+        const float *src;
+        const int *pos;
+        uint64_t n_tokens;
+        uint32_t n_heads, head_dim;
+        RopeParams r;
+    } a{dst, src, pos, n_tokens, (uint32_t) n_heads, (uint32_t) head_dim,
+        rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
+    return launch(c, c->f_rope, (unsigned) ((threads + 255) / 256), 256, a, "rope", n_heads, head_dim);
+}
+
+int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
+                                const float *v, const int *pos, const unsigned int *page_ids,
+                                const unsigned int *slots, unsigned long n_tok,
+                                unsigned long n_kv_heads, unsigned long head_dim,
+                                unsigned long page_tokens, unsigned long n_dims, float freq_base,
+                                float freq_scale, float ext_factor, float attn_factor,
+                                float corr_lo, float corr_hi, int neox, unsigned int kv_type) {
+    if (!c || !k_pages || !v_pages || !k || !v || !pos || !page_ids || !slots) return ERR;
+    if (n_dims == 0 || n_dims % 2 != 0 || n_dims > head_dim) return ERR_ARG;
+    if (kv_type != 0u && kv_type != 1u) return ERR_ARG;
+    if (page_tokens == 0 || n_kv_heads == 0 || head_dim == 0) return ERR_ARG;
+    if (n_tok == 0) return OK;
+    if (head_dim > 0xFFFFFFFFul || n_kv_heads > 0xFFFFFFFFul) return ERR_ARG;
+    const uint64_t threads = (uint64_t) n_tok * n_kv_heads * ((head_dim + 1) / 2);
+    if (threads / 256 >= 0xFFFFFFFFull) return ERR_ARG;
+    struct {
+        void *kp, *vp;
+        const float *k, *v;
+        const int *pos;
+        const uint32_t *pages, *slots;
+        uint64_t n_tok;
+        uint32_t n_kv_heads, head_dim;
+        uint64_t pt;
+        uint32_t kv_type;
+        RopeParams r;
+    } a{k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, (uint32_t) n_kv_heads,
+        (uint32_t) head_dim, page_tokens, kv_type,
+        rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
+    return launch(c, c->f_rope_append_chunk, (unsigned) ((threads + 255) / 256), 256, a,
+                  "rope_kv_append_chunk", n_kv_heads, head_dim);
 }
 
 void *moearc_ctx_stream(moearc_ctx *c) { return c ? (void *) c->stream : nullptr; }

@@ -46,6 +46,14 @@ SIGNATURES = {
     "moearc_attn_prefill": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _c_ulong,
                                            _c_ulong, _c_ulong, _c_ulong, _c_ulong, _c_ulong,
                                            _c_ulong, ctypes.c_float, _u32]),
+    "moearc_rope": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong, _c_ulong, _c_ulong, _c_ulong,
+                                   ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                   ctypes.c_float, ctypes.c_float, ctypes.c_int]),
+    "moearc_rope_kv_append_chunk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                   _c_ulong, _c_ulong, _c_ulong, _c_ulong,
+                                                   _c_ulong, ctypes.c_float, ctypes.c_float,
+                                                   ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                                   ctypes.c_float, ctypes.c_int, _u32]),
 }
 
 _lib = None

@@ -26,7 +26,14 @@
  *                                       masked softmax over the whole chunk;
  *   orc_kv_append / orc_kv_index     -- the reference test's exact-slot check (poisoned pool,
  *                                       neighbours untouched) and a numpy fancy-index gather;
- *   SplitMix64                       -- the published test vectors of the generator.
+ *   SplitMix64                       -- the published test vectors of the generator;
+ *   orc_rope / orc_rope_yarn         -- complex multiplication by e^(i theta) in numpy complex128
+ *                                       with the pairing built by slicing (halves for NeoX,
+ *                                       even/odd for the adjacent convention); position 0 is the
+ *                                       identity; rotated pairs keep their length times mscale;
+ *                                       YaRN's ramp endpoints (pure extrapolation below corr_lo,
+ *                                       freq_scale-interpolated above corr_hi); YaRN off equals
+ *                                       plain RoPE.
  */
 #include <math.h>
 #include <stddef.h>
@@ -318,4 +325,85 @@ int orc_attn_prefill(float *out, const float *q, const void *k_pages, const void
     }
     (void) n_threads;
     return rc_any;
+}
+
+/* ---- RoPE: reference.rs:468-505 (CPU twin) and kernels.cpp:1399-1468 (the kernel) -------- */
+
+/* Channels of pair p: NeoX (p, p + n_dims/2), else (2p, 2p + 1) (reference.rs:451-457). */
+static void rope_pair(size_t p, size_t n_dims, int neox, size_t *lo, size_t *hi) {
+    *lo = neox ? p : 2 * p;
+    *hi = neox ? p + n_dims / 2 : 2 * p + 1;
+}
+
+/* reference::rope: the angle table built per token by repeated f32 multiplication, as ggml's CPU
+ * path does (theta *= theta_scale), f32 cos/sin, f32 rotation; channels >= n_dims copied. */
+void orc_rope(float *out, const float *src, const int32_t *pos, size_t n_tokens, size_t n_heads,
+              size_t head_dim, size_t n_dims, float freq_base, int neox) {
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    memcpy(out, src, n_tokens * n_heads * head_dim * sizeof(float));
+    for (size_t t = 0; t < n_tokens; ++t) {
+        float theta = (float) pos[t];
+        for (size_t p = 0; p < n_dims / 2; ++p) {
+            const float ct = cosf(theta), st = sinf(theta);
+            for (size_t h = 0; h < n_heads; ++h) {
+                const size_t base = (t * n_heads + h) * head_dim;
+                size_t lo, hi;
+                rope_pair(p, n_dims, neox, &lo, &hi);
+                const float x0 = src[base + lo], x1 = src[base + hi];
+                out[base + lo] = x0 * ct - x1 * st;
+                out[base + hi] = x0 * st + x1 * ct;
+            }
+            theta *= theta_scale;
+        }
+    }
+}
+
+/* The kernel's closed form (kernels.cpp:1441-1466, ggml's rope_yarn), evaluated in f64 from the
+ * f32 parameters (theta_scale rounded to f32 as the host computes it, kernels.cpp:1406): the
+ * ground truth a f32 device implementation is compared to. out_d is f64. */
+void orc_rope_yarn(double *out_d, const float *src, const int32_t *pos, size_t n_tokens,
+                   size_t n_heads, size_t head_dim, size_t n_dims, float freq_base, float freq_scale,
+                   float ext_factor, float attn_factor, float corr_lo, float corr_hi, int neox) {
+    const double theta_scale = (double) powf(freq_base, -2.0f / (float) n_dims);
+    for (size_t i = 0; i < n_tokens * n_heads * head_dim; ++i) out_d[i] = (double) src[i];
+    for (size_t t = 0; t < n_tokens; ++t)
+        for (size_t p = 0; p < n_dims / 2; ++p) {
+            const double theta_extrap = (double) pos[t] * pow(theta_scale, (double) p);
+            double theta = (double) freq_scale * theta_extrap;
+            double mscale = (double) attn_factor;
+            if (ext_factor != 0.0f) {
+                const double y = ((double) p - corr_lo) / fmax(0.001, (double) corr_hi - corr_lo);
+                const double ramp_mix = (1.0 - fmin(1.0, fmax(0.0, y))) * ext_factor;
+                theta = theta * (1.0 - ramp_mix) + theta_extrap * ramp_mix;
+                mscale *= 1.0 + 0.1 * log(1.0 / (double) freq_scale);
+            }
+            const double ct = cos(theta) * mscale, st = sin(theta) * mscale;
+            for (size_t h = 0; h < n_heads; ++h) {
+                const size_t base = (t * n_heads + h) * head_dim;
+                size_t lo, hi;
+                rope_pair(p, n_dims, neox, &lo, &hi);
+                const double x0 = src[base + lo], x1 = src[base + hi];
+                out_d[base + lo] = x0 * ct - x1 * st;
+                out_d[base + hi] = x0 * st + x1 * ct;
+            }
+        }
+}
+
+/* The engine's per-token sequence (moe.rs:1987-2042): K rotated (closed form, rounded to f32),
+ * then K and V appended at (page_ids[t], slots[t]) as moearc_kv_append stores them. */
+void orc_rope_kv_append_chunk(void *k_pages, void *v_pages, const float *k, const float *v,
+                              const int32_t *pos, const uint32_t *page_ids, const uint32_t *slots,
+                              size_t n_tok, size_t n_kv_heads, size_t head_dim, size_t page_tokens,
+                              size_t n_dims, float freq_base, float freq_scale, float ext_factor,
+                              float attn_factor, float corr_lo, float corr_hi, int neox,
+                              uint32_t kv_type, double *scratch_d, float *scratch_f) {
+    const size_t row = n_kv_heads * head_dim;
+    for (size_t t = 0; t < n_tok; ++t) {
+        orc_rope_yarn(scratch_d, k + t * row, pos + t, 1, n_kv_heads, head_dim, n_dims, freq_base,
+                      freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox);
+        for (size_t i = 0; i < row; ++i) scratch_f[i] = (float) scratch_d[i];
+        if (slots[t] < page_tokens)
+            orc_kv_append_raw(k_pages, v_pages, scratch_f, v + t * row, page_ids[t], slots[t],
+                              n_kv_heads, head_dim, page_tokens, kv_type);
+    }
 }

@@ -27,6 +27,8 @@ _u32p = ctypes.POINTER(ctypes.c_uint32)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _u64p = ctypes.POINTER(ctypes.c_uint64)
 _sz = ctypes.c_size_t
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f = ctypes.c_float
 
 
 def build(force: bool = False) -> str:
@@ -76,6 +78,12 @@ def lib():
                                        _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz,
                                        ctypes.c_float, ctypes.c_uint32, _f64p, ctypes.c_int]
         L.orc_attn_prefill.restype = ctypes.c_int
+        L.orc_rope.argtypes = [_f32p, _f32p, _i32p, _sz, _sz, _sz, _sz, _f, ctypes.c_int]
+        L.orc_rope_yarn.argtypes = [_f64p, _f32p, _i32p, _sz, _sz, _sz, _sz, _f, _f, _f, _f, _f, _f,
+                                    ctypes.c_int]
+        L.orc_rope_kv_append_chunk.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _f32p, _f32p, _i32p,
+                                               _u32p, _u32p, _sz, _sz, _sz, _sz, _sz, _f, _f, _f, _f,
+                                               _f, _f, ctypes.c_int, ctypes.c_uint32, _f64p, _f32p]
         _lib = L
     return _lib
 
@@ -226,3 +234,45 @@ def attn_prefill(q, k_pages, v_pages, block_table, n_q, pos0, n_swa, n_heads, n_
     if rc != 0:
         raise OracleRefusal(f"orc_attn_prefill refused its arguments (rc {rc})")
     return out
+
+
+# ---- RoPE (reference.rs:468-505; kernels.cpp:1399-1468) -------------------------------------
+
+def rope(src, pos, n_tokens, n_heads, head_dim, n_dims, freq_base, neox=True):
+    """reference::rope: iterated f32 angle table, f32 rotation; returns f32."""
+    src = np.ascontiguousarray(src, np.float32).reshape(-1)
+    pos = np.ascontiguousarray(pos, np.int32)
+    out = np.empty_like(src)
+    lib().orc_rope(_p(out, _f32p), _p(src, _f32p), _p(pos, _i32p), n_tokens, n_heads, head_dim,
+                   n_dims, _f(freq_base), int(bool(neox)))
+    return out
+
+
+def rope_yarn(src, pos, n_tokens, n_heads, head_dim, n_dims, freq_base, freq_scale=1.0,
+              ext_factor=0.0, attn_factor=1.0, corr_lo=0.0, corr_hi=0.0, neox=True):
+    """The kernel's closed form with YaRN, evaluated in f64; returns f64."""
+    src = np.ascontiguousarray(src, np.float32).reshape(-1)
+    pos = np.ascontiguousarray(pos, np.int32)
+    out = np.empty(src.shape, np.float64)
+    lib().orc_rope_yarn(_p(out, _f64p), _p(src, _f32p), _p(pos, _i32p), n_tokens, n_heads, head_dim,
+                        n_dims, _f(freq_base), _f(freq_scale), _f(ext_factor), _f(attn_factor),
+                        _f(corr_lo), _f(corr_hi), int(bool(neox)))
+    return out
+
+
+def rope_kv_append_chunk(k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, n_kv_heads, head_dim,
+                         page_tokens, n_dims, freq_base, scaling=(1.0, 0.0, 1.0, 0.0, 0.0), neox=True,
+                         kv_type=KV_F16):
+    """The engine's per-token rope-then-append over a chunk, into device-format pools (in place)."""
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    pg = np.ascontiguousarray(page_ids, np.uint32)
+    sl = np.ascontiguousarray(slots, np.uint32)
+    row = n_kv_heads * head_dim
+    sd, sf = np.empty(row, np.float64), np.empty(row, np.float32)
+    fs, ext, att, clo, chi = (float(x) for x in scaling)
+    lib().orc_rope_kv_append_chunk(k_pages.ctypes.data, v_pages.ctypes.data, _p(k, _f32p), _p(v, _f32p),
+                                   _p(pos, _i32p), _p(pg, _u32p), _p(sl, _u32p), n_tok, n_kv_heads,
+                                   head_dim, page_tokens, n_dims, _f(freq_base), _f(fs), _f(ext), _f(att),
+                                   _f(clo), _f(chi), int(bool(neox)), kv_type, _p(sd, _f64p), _p(sf, _f32p))

@@ -203,3 +203,61 @@ def prefill_digest(case) -> str:
 def load_golden(name: str) -> dict:
     with np.load(os.path.join(GOLDEN_DIR, name + ".npz"), allow_pickle=False) as z:
         return {k: z[k] for k in z.files}
+
+
+# ---- RoPE ------------------------------------------------------------------------------------
+
+# crates/moearc-kernels/tests/kernels_gpu.rs:292-351: 5 tokens x 4 heads x 80 channels, 64 rotated,
+# base 10000, positions 3t, inputs Rng(0xB0BE).vec_unit.
+ROPE_REF = dict(seed=0xB0BE, tokens=5, heads=4, head_dim=80, n_dims=64, freq_base=10000.0)
+# gpt-oss's published RoPE configuration: base 150000, YaRN factor 32 over a 4096-token original
+# context, beta_fast 32, beta_slow 1 (the GGUF defaults moe.rs:582-586 falls back to).
+GPT_OSS_ROPE = dict(freq_base=150000.0, factor=32.0, n_ctx_orig=4096, beta_fast=32.0, beta_slow=1.0)
+
+
+def rope_reference_inputs():
+    from oracle import oracle
+    r = ROPE_REF
+    src = oracle.Rng(r["seed"]).vec_unit(r["tokens"] * r["heads"] * r["head_dim"])
+    pos = (np.arange(r["tokens"], dtype=np.int32) * 3).astype(np.int32)
+    return src, pos
+
+
+def host_powf(x, y):
+    """The host C library's powf (what the runtime and the reference's host use for theta_scale;
+    numpy's float32 power can differ from it in the last bit)."""
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.powf.restype = ctypes.c_float
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    return float(libm.powf(float(np.float32(x)), float(np.float32(y))))
+
+
+def rope_complex(src, pos, n_tokens, n_heads, head_dim, n_dims, freq_base, scaling=None, neox=True):
+    """An independent formulation: each rotated pair is a complex number z = x_lo + i x_hi (pairs
+    taken by slicing -- the two halves for NeoX, even/odd channels otherwise) multiplied by
+    mscale * e^(i theta) in complex128. theta_p = pos * theta_scale^p with theta_scale rounded to
+    f32 (the host's powf); YaRN mixes the interpolated and extrapolated angles by the ramp."""
+    x = np.asarray(src, np.float64).reshape(n_tokens, n_heads, head_dim).copy()
+    half = n_dims // 2
+    ts = host_powf(freq_base, -2.0 / n_dims)
+    p = np.arange(half, dtype=np.float64)
+    ext = np.asarray(pos, np.float64)[:, None] * ts ** p[None, :]  # [tokens][half]
+    fs, ef, af, lo, hi = (1.0, 0.0, 1.0, 0.0, 0.0) if scaling is None else scaling
+    theta, msc = fs * ext, af
+    if ef != 0.0:
+        y = (p - lo) / max(0.001, hi - lo)
+        mix = (1.0 - np.clip(y, 0.0, 1.0)) * ef
+        theta = theta * (1.0 - mix)[None, :] + ext * mix[None, :]
+        msc = af * (1.0 + 0.1 * np.log(1.0 / fs))
+    rot = msc * np.exp(1j * theta)[:, None, :]  # broadcast over heads
+    if neox:
+        z = x[..., :half] + 1j * x[..., half:n_dims]
+        z = z * rot
+        x[..., :half], x[..., half:n_dims] = z.real, z.imag
+    else:
+        z = x[..., 0:n_dims:2] + 1j * x[..., 1:n_dims:2]
+        z = z * rot
+        x[..., 0:n_dims:2], x[..., 1:n_dims:2] = z.real, z.imag
+    return x.reshape(-1)

@@ -12,7 +12,11 @@ The script refuses to write a fixture whose two answers differ by more than 1e-1
 The reference-test fixtures reproduce crates/moearc-kernels/tests/forward_pass_gpu.rs's inputs
 bit-exactly (SplitMix64 and the fill order of fill_cache, :383-428).
 
-Run: python tests/golden/gen_golden.py
+The RoPE fixture (kernels_gpu.rs:292-351's inputs) stores reference::rope's outputs, checked against
+an independent complex128 formulation to 1e-5.
+
+Run: python tests/golden/gen_golden.py            (every fixture)
+     python tests/golden/gen_golden.py rope       (the RoPE fixture only)
 """
 from __future__ import annotations
 
@@ -69,6 +73,27 @@ def prefill_fixture(name, case, n_swa):
     print(f"{name}: oracle vs brute force {err:.2e}")
 
 
+def rope_fixture():
+    # kernels_gpu.rs:292-351's inputs; expected = reference::rope (iterated angle table, f32) for
+    # both conventions; the complex128 closed form must agree to 1e-5 (the iterated table drifts
+    # by a few ulp of the angle).
+    r = fx.ROPE_REF
+    src, pos = fx.rope_reference_inputs()
+    out = {}
+    for name, neox in (("neox", True), ("normal", False)):
+        want = oracle.rope(src, pos, r["tokens"], r["heads"], r["head_dim"], r["n_dims"],
+                           r["freq_base"], neox)
+        ind = fx.rope_complex(src, pos, r["tokens"], r["heads"], r["head_dim"], r["n_dims"],
+                              r["freq_base"], neox=neox)
+        err = float(np.max(np.abs(want.astype(np.float64) - ind)))
+        if not err <= 1e-5:
+            raise SystemExit(f"rope {name}: oracle and complex form differ by {err:.3e}")
+        out["expected_" + name] = want
+    import hashlib
+    np.savez(os.path.join(HERE, "ref_rope.npz"), digest=hashlib.sha256(src.tobytes()).hexdigest(),
+             pos=pos, **out)
+
+
 def main():
     for name in fx.REFERENCE_CASES:
         c = fx.reference_case(name)
@@ -83,7 +108,10 @@ def main():
     pc = fx.prefill_case(0x9F11, n_q=48, pos0=80)
     prefill_fixture("ns_prefill_full", pc, 0)
     prefill_fixture("ns_prefill_swa16", pc, 16)
+    rope_fixture()
 
 
-if __name__ == "__main__":
+if __name__ == "__main__" and sys.argv[1:] == ["rope"]:
+    rope_fixture()
+elif __name__ == "__main__":
     main()
