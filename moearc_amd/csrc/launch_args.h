@@ -95,6 +95,9 @@ struct PrefillArgs {
 
 // RoPE parameters (moearc_rope, moearc_rope_kv_append_chunk): theta_scale = freq_base^(-2/n_dims),
 // computed on the host; neox selects the (p, p + n_dims/2) pairing, else (2p, 2p + 1).
+// Heads per thread of the RoPE kernels (grid y runs over groups of this many heads).
+constexpr uint32_t ROPE_HEADS = 4;
+
 struct RopeParams {
     uint32_t n_dims;
     uint32_t neox;

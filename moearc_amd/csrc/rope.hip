@@ -13,8 +13,9 @@
 // independent), as the reference's kernel computes it; cos and sin are the accurate library
 // functions (full range reduction), since positions reach 10^5 radians.
 //
-// One thread per (token, head, pair): it computes the angle once and writes both channels of the
-// pair -- for the fused append, of K (rotated) and V (copied), as f16 with the reference's rounding.
+// One thread per (token, pair, group of heads): it computes the angle once and writes both channels
+// of the pair in each of its heads -- for the fused append, of K (rotated) and V (copied), as f16
+// with the reference's rounding.
 #include "common.h"
 
 // f32_to_f16_bits: kernels_misc.hip (same translation unit).
@@ -48,33 +49,53 @@ __device__ __forceinline__ void pair_channels(const RopeParams &r, uint32_t j, u
     }
 }
 
-// moearc_rope: src/dst f32 [n_tokens][n_heads][head_dim].
+// A thread handles ROPE_HEADS heads (launch_args.h). The angle depends on (position, pair) only,
+// so a thread computes cos/sin once and applies them to ROPE_HEADS rows: the transcendental work
+// shrinks by that factor, and the thread's 2*ROPE_HEADS independent loads (4*ROPE_HEADS when V
+// rides along) are all issued before the first store.
+
+// moearc_rope: src/dst f32 [n_tokens][n_heads][head_dim]; dst may equal src.
+// Grid: x over (token, pair slot), y over groups of ROPE_HEADS heads.
 extern "C" __global__ void moearc_rope_k(float *dst, const float *src, const int *pos,
                                          uint64_t n_tokens, uint32_t n_heads, uint32_t head_dim,
                                          RopeParams r) {
     const uint32_t slots = (head_dim + 1u) >> 1;  // pair slots per head (head_dim may be odd)
     const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n_tokens * n_heads * slots) return;
+    if (g >= n_tokens * slots) return;
     const uint32_t j = (uint32_t) (g % slots);
-    const uint64_t th = g / slots;  // token * n_heads + head
-    const uint64_t t = th / n_heads;
-    const float *s = src + th * head_dim;
-    float *o = dst + th * head_dim;
+    const uint64_t t = g / slots;
+    const uint32_t h0 = blockIdx.y * ROPE_HEADS;
     uint32_t lo, hi;
     pair_channels(r, j, lo, hi);
-    if (j < (r.n_dims >> 1)) {
-        const float2_t cs = rope_factors(r, pos[t], j);
-        const float x0 = s[lo], x1 = s[hi];
-        o[lo] = x0 * cs[0] - x1 * cs[1];
-        o[hi] = x0 * cs[1] + x1 * cs[0];
-    } else {
-        o[lo] = s[lo];
-        if (hi < head_dim) o[hi] = s[hi];
+    const bool rot = j < (r.n_dims >> 1), has_hi = hi < head_dim;
+    float x0[ROPE_HEADS] = {}, x1[ROPE_HEADS] = {};
+#pragma unroll
+    for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
+        if (h0 + i < n_heads) {
+            const float *s = src + (t * n_heads + h0 + i) * head_dim;
+            x0[i] = s[lo];
+            x1[i] = has_hi ? s[hi] : 0.0f;
+        }
+    }
+    float2_t cs = {1.0f, 0.0f};
+    if (rot) cs = rope_factors(r, pos[t], j);
+#pragma unroll
+    for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
+        if (h0 + i < n_heads) {
+            float *o = dst + (t * n_heads + h0 + i) * head_dim;
+            if (rot) {
+                o[lo] = x0[i] * cs[0] - x1[i] * cs[1];
+                o[hi] = x0[i] * cs[1] + x1[i] * cs[0];
+            } else {
+                o[lo] = x0[i];
+                if (has_hi) o[hi] = x1[i];
+            }
+        }
     }
 }
 
 // A prefill chunk's K (rotated) and V to (page_ids[t], slots[t]); k, v f32 [n_tok][n_kv_heads][head_dim].
-// A slot outside the page is skipped, as in moearc_kv_append_chunk.
+// A slot outside the page is skipped, as in moearc_kv_append_chunk. Grid as moearc_rope_k's.
 extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_pages, const float *k,
                                                          const float *v, const int *pos,
                                                          const uint32_t *page_ids, const uint32_t *slots,
@@ -83,42 +104,61 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
                                                          uint32_t kv_type, RopeParams r) {
     const uint32_t nslot = (head_dim + 1u) >> 1;
     const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n_tok * n_kv_heads * nslot) return;
+    if (g >= n_tok * nslot) return;
     const uint32_t j = (uint32_t) (g % nslot);
-    const uint64_t th = g / nslot;
-    const uint64_t t = th / n_kv_heads;
-    const uint32_t h = (uint32_t) (th - t * n_kv_heads);
-    const uint32_t slot = slots[t];
-    if (slot >= page_tokens) return;
-    const float *ks = k + th * head_dim;
-    const float *vs = v + th * head_dim;
-    const uint64_t dst = (((uint64_t) page_ids[t] * page_tokens + slot) * n_kv_heads + h) * head_dim;
+    const uint64_t t = g / nslot;
+    const uint32_t h0 = blockIdx.y * ROPE_HEADS;
     uint32_t lo, hi;
     pair_channels(r, j, lo, hi);
-    float k0 = ks[lo], k1 = 0.f;
-    const bool has_hi = hi < head_dim;
-    if (has_hi) k1 = ks[hi];
-    if (j < (r.n_dims >> 1)) {
-        const float2_t cs = rope_factors(r, pos[t], j);
-        const float x0 = k0, x1 = k1;
-        k0 = x0 * cs[0] - x1 * cs[1];
-        k1 = x0 * cs[1] + x1 * cs[0];
-    }
-    if (kv_type == MOEARC_KV_F16) {
-        uint16_t *kp = (uint16_t *) k_pages + dst, *vp = (uint16_t *) v_pages + dst;
-        kp[lo] = f32_to_f16_bits(k0);
-        vp[lo] = f32_to_f16_bits(vs[lo]);
-        if (has_hi) {
-            kp[hi] = f32_to_f16_bits(k1);
-            vp[hi] = f32_to_f16_bits(vs[hi]);
+    const bool rot = j < (r.n_dims >> 1), has_hi = hi < head_dim;
+    // Every load (rows, slot, page, position) is issued before the first use of any of them: one
+    // memory latency instead of a chain of three.
+    float k0[ROPE_HEADS] = {}, k1[ROPE_HEADS] = {}, v0[ROPE_HEADS] = {}, v1[ROPE_HEADS] = {};
+#pragma unroll
+    for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
+        if (h0 + i < n_kv_heads) {
+            const uint64_t row = (t * n_kv_heads + h0 + i) * head_dim;
+            k0[i] = k[row + lo];
+            v0[i] = v[row + lo];
+            k1[i] = has_hi ? k[row + hi] : 0.0f;
+            v1[i] = has_hi ? v[row + hi] : 0.0f;
         }
-    } else {
-        float *kp = (float *) k_pages + dst, *vp = (float *) v_pages + dst;
-        kp[lo] = k0;
-        vp[lo] = vs[lo];
-        if (has_hi) {
-            kp[hi] = k1;
-            vp[hi] = vs[hi];
+    }
+    const uint32_t slot = slots[t], page = page_ids[t];
+    const int p = pos[t];
+    asm volatile("" ::"v"(page), "v"(p));  // keeps the two loads above the branch
+    if (slot >= page_tokens) return;
+    if (rot) {
+        const float2_t cs = rope_factors(r, p, j);
+#pragma unroll
+        for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
+            const float x0 = k0[i], x1 = k1[i];
+            k0[i] = x0 * cs[0] - x1 * cs[1];
+            k1[i] = x0 * cs[1] + x1 * cs[0];
+        }
+    }
+    const uint64_t base = ((uint64_t) page * page_tokens + slot) * n_kv_heads;
+#pragma unroll
+    for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
+        if (h0 + i < n_kv_heads) {
+            const uint64_t dst = (base + h0 + i) * head_dim;
+            if (kv_type == MOEARC_KV_F16) {
+                uint16_t *kp = (uint16_t *) k_pages + dst, *vp = (uint16_t *) v_pages + dst;
+                kp[lo] = f32_to_f16_bits(k0[i]);
+                vp[lo] = f32_to_f16_bits(v0[i]);
+                if (has_hi) {
+                    kp[hi] = f32_to_f16_bits(k1[i]);
+                    vp[hi] = f32_to_f16_bits(v1[i]);
+                }
+            } else {
+                float *kp = (float *) k_pages + dst, *vp = (float *) v_pages + dst;
+                kp[lo] = k0[i];
+                vp[lo] = v0[i];
+                if (has_hi) {
+                    kp[hi] = k1[i];
+                    vp[hi] = v1[i];
+                }
+            }
         }
     }
 }

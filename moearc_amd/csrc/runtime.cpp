@@ -135,8 +135,8 @@ void record_bracket(moearc_ctx *c, hipEvent_t start, const char *what, unsigned 
 // Launch `f` with one by-value argument block. With profiling on, a HIP event pair brackets the
 // launch under the key "<what> r<r> m<m>" (the reference's key format, kernels.cpp:1905-1916).
 template <typename Args>
-int launch(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned block, const Args &args,
-           const char *what, unsigned long r, unsigned long m) {
+int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, unsigned block,
+             const Args &args, const char *what, unsigned long r, unsigned long m) {
     if (!f) return ERR;
     hipEvent_t e0 = nullptr;
     if (c->profiling && (e0 = take_event(c))) hipEventRecord(e0, c->stream);
@@ -144,9 +144,15 @@ int launch(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned block, const 
     void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *) &args, HIP_LAUNCH_PARAM_BUFFER_SIZE,
                       &size, HIP_LAUNCH_PARAM_END};
     const hipError_t err =
-        hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, c->stream, nullptr, config);
+        hipModuleLaunchKernel(f, grid, grid_y, 1, block, 1, 1, 0, c->stream, nullptr, config);
     if (e0) record_bracket(c, e0, what, r, m);
     return err == hipSuccess ? OK : ERR;
+}
+
+template <typename Args>
+int launch(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned block, const Args &args,
+           const char *what, unsigned long r, unsigned long m) {
+    return launch2d(c, f, grid, 1, block, args, what, r, m);
 }
 
 int ensure_workspace(moearc_ctx *c, size_t floats) {
@@ -470,8 +476,10 @@ int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
     if (n_dims == 0 || n_dims % 2 != 0 || n_dims > head_dim) return ERR_ARG;
     if (n_tokens == 0 || n_heads == 0) return OK;
     if (head_dim > 0xFFFFFFFFul || n_heads > 0xFFFFFFFFul) return ERR_ARG;
-    const uint64_t threads = (uint64_t) n_tokens * n_heads * ((head_dim + 1) / 2);
-    if (threads / 256 >= 0xFFFFFFFFull) return ERR_ARG;
+    // threads over (token, pair slot); grid y over groups of ROPE_HEADS heads
+    const uint64_t threads = (uint64_t) n_tokens * ((head_dim + 1) / 2);
+    const uint64_t groups = (n_heads + ROPE_HEADS - 1) / ROPE_HEADS;
+    if (threads / 256 >= 0xFFFFFFFFull || groups > 65535) return ERR_ARG;
     struct {
         float *dst;
         const float *src;
@@ -481,7 +489,8 @@ int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
         RopeParams r;
     } a{dst, src, pos, n_tokens, (uint32_t) n_heads, (uint32_t) head_dim,
         rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
-    return launch(c, c->f_rope, (unsigned) ((threads + 255) / 256), 256, a, "rope", n_heads, head_dim);
+    return launch2d(c, c->f_rope, (unsigned) ((threads + 255) / 256), (unsigned) groups, 256, a,
+                    "rope", n_heads, head_dim);
 }
 
 int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
@@ -497,8 +506,9 @@ int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, con
     if (page_tokens == 0 || n_kv_heads == 0 || head_dim == 0) return ERR_ARG;
     if (n_tok == 0) return OK;
     if (head_dim > 0xFFFFFFFFul || n_kv_heads > 0xFFFFFFFFul) return ERR_ARG;
-    const uint64_t threads = (uint64_t) n_tok * n_kv_heads * ((head_dim + 1) / 2);
-    if (threads / 256 >= 0xFFFFFFFFull) return ERR_ARG;
+    const uint64_t threads = (uint64_t) n_tok * ((head_dim + 1) / 2);
+    const uint64_t groups = (n_kv_heads + ROPE_HEADS - 1) / ROPE_HEADS;
+    if (threads / 256 >= 0xFFFFFFFFull || groups > 65535) return ERR_ARG;
     struct {
         void *kp, *vp;
         const float *k, *v;
@@ -512,8 +522,8 @@ int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, con
     } a{k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, (uint32_t) n_kv_heads,
         (uint32_t) head_dim, page_tokens, kv_type,
         rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
-    return launch(c, c->f_rope_append_chunk, (unsigned) ((threads + 255) / 256), 256, a,
-                  "rope_kv_append_chunk", n_kv_heads, head_dim);
+    return launch2d(c, c->f_rope_append_chunk, (unsigned) ((threads + 255) / 256), (unsigned) groups,
+                    256, a, "rope_kv_append_chunk", n_kv_heads, head_dim);
 }
 
 void *moearc_ctx_stream(moearc_ctx *c) { return c ? (void *) c->stream : nullptr; }
