@@ -145,8 +145,8 @@ int moearc_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const fl
  * theta = pos * freq_base^(-2p/n_dims) with YaRN interpolation (freq_scale, ext_factor, corr_lo,
  * corr_hi) and magnitude scale attn_factor (times 1 + 0.1 ln(1/freq_scale) when ext_factor != 0);
  * channels >= n_dims pass through. freq_scale 1, ext_factor 0, attn_factor 1 is plain RoPE.
- * Returns -1 on a null pointer; -2 when n_dims is 0, odd or larger than head_dim; 0 (nothing
- * enqueued) for zero tokens or heads. */
+ * Returns -1 on a null pointer; -2 when n_dims is 0, odd or larger than head_dim, or when
+ * n_heads exceeds 262140 (the launch grid's limit); 0 (nothing enqueued) for zero tokens or heads. */
 int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
                 unsigned long n_tokens, unsigned long n_heads, unsigned long head_dim,
                 unsigned long n_dims, float freq_base, float freq_scale, float ext_factor,
