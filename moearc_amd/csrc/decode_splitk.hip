@@ -385,8 +385,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
 // makes the records visible, with no device-scope cache maintenance inside either kernel
 // (merging inside one launch needs a device-scope release -- an L2 write-back -- in every
 // work-group, measured to cost more than this second launch).
+#ifndef MERGE_WAVES
 #define MERGE_WAVES 4
+#endif
+#ifndef MERGE_BATCH
 #define MERGE_BATCH 32
+#endif
 extern "C" __global__ __launch_bounds__(64 * MERGE_WAVES) void moearc_attn_decode_merge(
     const DecodeArgs a) {
     __shared__ float red_m[MERGE_WAVES], red_l[MERGE_WAVES];

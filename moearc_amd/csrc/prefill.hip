@@ -48,9 +48,10 @@
 // before every read.
 //
 // Softmax. p = 2^(s*c + 7 - m) in the log2 domain (c = scale * log2 e) against a per-row reference
-// m that moves only when some score of the row exceeds it by more than 8: each lane checks its own
-// 16 scores, and the cross-lane row maximum and the rescale of O and the sums run only then (in
-// practice at a row's first chunk). So p <= 2^15 fits f16. P enters the MFMA as one f16 operand with
+// m that moves only when some weight of the row overflows f16 (a score more than ~9 above m): the
+// weights are computed first, an infinite row sum flags the overflow, and only then are the
+// cross-lane row maximum, the rescale of O and the sums and the recomputation run (in practice at
+// a row's first chunk). So p < 2^16 fits f16, and the common chunk computes no maximum. P enters the MFMA as one f16 operand with
 // f32 accumulation: the weights carry f16's 11 bits, an output error of at most 2^-12 max|V|
 // (measured ~2.5e-4 on N(0,1) data); the row sums are dot products of the same f16 weights with
 // ones (v_dot2_f32_f16), so numerator and denominator see the same rounding. The _precise_
@@ -59,7 +60,6 @@
 #include "common.h"
 
 #define PF_LOG2_PSCALE 7.0f
-#define PF_RESCALE_SLACK 8.0f
 #define PF_M_INIT -1.0e30f  // finite "no key yet": keeps exp2(m_old - m_new) defined for rows
                             // whose keys all lie in later chunks
 #define PF_KT 32            // keys per LDS tile (one chunk)
@@ -121,6 +121,12 @@ __device__ __forceinline__ void pf_read_vt(u32x2_t (&r)[4], uint32_t base) {
         : "memory");
 }
 
+// LDS DMA of 16 bytes per lane from a wave-uniform global base plus a per-lane 32-bit offset to
+// LDS address lds + 16 * lane (the scalar-base form: no 64-bit address arithmetic per lane).
+__device__ __forceinline__ void pf_copy16(const void *sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
+
 template <int GROUP, bool SPLIT_P>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     constexpr uint32_t ROWS = MOEARC_PREFILL_ROWS;  // 128 rows per work-group
@@ -168,16 +174,33 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint32_t w_bmin = a.n_swa ? (w_pmin + 1u > a.n_swa ? w_pmin + 1u - a.n_swa : 0u) : 0u;
     const uint32_t w_bmax = a.n_swa ? (w_pmax + 1u > a.n_swa ? w_pmax + 1u - a.n_swa : 0u) : 0u;
 
-    // s*c with c < 0 equals (-s)*(-c): negate the f16 Q operand (exact) so that c > 0 and the
-    // row maximum of s*c is c times the maximum of s
     float c = a.scale_log2e;
-    if (c < 0.f) {
-        c = -c;
+    if constexpr (SPLIT_P) {
+        // s*c with c < 0 equals (-s)*(-c): negate the f16 Q operand (exact) so that c > 0 and the
+        // row maximum of s*c is c times the maximum of s
+        if (c < 0.f) {
+            c = -c;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) qop[t] = -qop[t];
+            for (int t = 0; t < 4; ++t) qop[t] = -qop[t];
+        }
+    } else {
+        // Q is pre-scaled by c (one more f16 rounding of each q element, the same relative size as
+        // the rounding of the weights; the host uses the _precise_ kernels when |c| > 1, where q*c
+        // could leave f16's range), so the MFMA yields scores in the log2 domain directly.
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qop[t][i] = (_Float16) ((float) qop[t][i] * c);
     }
     float m_run = PF_M_INIT;
     float l_run = 0.f;  // this lane's share of the row sum (its 16 keys of every chunk)
+    // Single-f16 kernels: the QK^T accumulator starts from PF_LOG2_PSCALE - m_run in every register,
+    // so the MFMA returns the exponent of each weight and the common chunk needs no VALU before the
+    // exp (a VALU op issued beside MFMAs costs several times its nominal rate on gfx950; the
+    // transcendental unit does not compete with them).
+    float16_t biasv;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) biasv[i] = PF_LOG2_PSCALE - m_run;
     float16_t O[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -202,8 +225,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint32_t ld_key = 8u * wave + (lane >> 3);
     const uint32_t ld_chunk = (lane & 7u) ^ k_swz(ld_key), ld_chunk_v = (lane & 7u) ^ v_swz(ld_key);
     const uint64_t row_bytes = (uint64_t) G * 128u;
-    const uint8_t *k_src = (const uint8_t *) a.k_pages + kvh * 128u + ld_chunk * 16u;
-    const uint8_t *v_src = (const uint8_t *) a.v_pages + kvh * 128u + ld_chunk_v * 16u;
+    const uint32_t lane_ck = kvh * 128u + ld_chunk * 16u, lane_cv = kvh * 128u + ld_chunk_v * 16u;
     // Block-table entry of this lane's key of tile kt (keys past p_last are clamped to it, so no copy
     // reads a slot the cache has not written), issued through asm: the pipeline below waits for it
     // explicitly, and the compiler's own tracking would add conservative waits in the loop.
@@ -214,23 +236,36 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
         asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
         return v;
     };
+    // A tile that lies wholly below p_last in pages of 32 keys or more sits in one page: its base
+    // row is wave-uniform and computed on the scalar unit, and each lane adds a fixed 32-bit offset
+    // (VALU issue is the scarce resource beside the MFMAs). Other tiles address per lane.
+    const bool uni_pages = sh >= 5u;
+    const uint32_t lane_k = ld_key * (uint32_t) row_bytes + lane_ck;
+    const uint32_t lane_v = ld_key * (uint32_t) row_bytes + lane_cv;
     auto copy_tile = [&](uint32_t kt, uint32_t pid, int buf) {
         uint8_t *dst = tiles + buf * BUF_BYTES + 8u * wave * 128u;
-        const uint64_t off = (uint64_t) ((pid << sh) | (key_of(kt) & pmask)) * row_bytes;
-        __builtin_amdgcn_global_load_lds(k_src + off, dst, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(v_src + off, dst + TILE_BYTES, 16, 0, 0);
+        if (uni_pages && kt * PF_KT + (PF_KT - 1u) <= p_last) {
+            const uint32_t pid0 = __builtin_amdgcn_readfirstlane(pid);
+            const uint64_t base = (((uint64_t) pid0 << sh) | ((kt * PF_KT) & pmask)) * row_bytes;
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(
+                (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) dst);
+            pf_copy16((const uint8_t *) a.k_pages + base, lane_k, lds);
+            pf_copy16((const uint8_t *) a.v_pages + base, lane_v, lds + TILE_BYTES);
+        } else {
+            const uint64_t off = (uint64_t) ((pid << sh) | (key_of(kt) & pmask)) * row_bytes;
+            __builtin_amdgcn_global_load_lds((const uint8_t *) a.k_pages + off + lane_ck, dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const uint8_t *) a.v_pages + off + lane_cv, dst + TILE_BYTES, 16, 0, 0);
+        }
     };
 
     // ---- chunk stages ----------------------------------------------------------------------------
     const half2_t ones2 = {1, 1};
     // QK^T of chunk kc of the tile in buffer offset BOFF: S reg 4j + i = key j0 + 8j + 4h + i of row n
-    auto qk = [&](auto boff_c, auto kc_c) -> float16_t {
+    auto qk = [&](auto boff_c, auto kc_c, const float16_t &init) -> float16_t {
         constexpr int BOFF = decltype(boff_c)::value, kc = decltype(kc_c)::value;
         u32x4_t kr[4];
         pf_read_k<BOFF + 4096 * kc>(kr, k_base);
-        float16_t S;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) S[i] = 0.f;
+        float16_t S = init;
 #pragma unroll
         for (int t = 0; t < 4; ++t) S = pf_mfma(__builtin_bit_cast(half8_t, kr[t]), qop[t], S);
         return S;
@@ -243,36 +278,76 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
         for (int i = 0; i < 16; ++i)
             if (off + (uint32_t) (8 * (i >> 2) + (i & 3)) > span) S[i] = -INFINITY;
     };
-    // softmax weights; P^T operand of step s = S regs 8s..8s+7 in order
-    auto softmax = [&](const float16_t &S, half8_t (&phi)[2], half8_t (&plo)[2]) {
-        float lmax = fmaxf(S[0], S[1]);
+    // softmax weights; P^T operand of step s = S regs 8s..8s+7 in order. Returns l0 plus this
+    // lane's share of the chunk's row sum: f16 weights summed with ones (v_dot2_f32_f16), so the
+    // denominator sees the same rounding as the numerator. Weights are non-negative, so the sum
+    // is finite unless some weight overflowed f16 (became +inf).
+    auto weights = [&](const float16_t &S, float bias, float l0, half8_t (&phi)[2], half8_t (&plo)[2]) {
 #pragma unroll
-        for (int i = 2; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(S[i], S[i + 1]));
-        lmax *= c;
-        if (__builtin_amdgcn_ballot_w64(lmax > m_run + PF_RESCALE_SLACK) != 0) {
+        for (int i = 0; i < 16; i += 2) {
+            const float x0 = SPLIT_P ? fmaf(S[i], c, bias) : S[i];
+            const float x1 = SPLIT_P ? fmaf(S[i + 1], c, bias) : S[i + 1];
+            const float p0 = __builtin_amdgcn_exp2f(x0);
+            const float p1 = __builtin_amdgcn_exp2f(x1);
+            const half2_t hv = {(_Float16) p0, (_Float16) p1};
+            phi[i >> 3][i & 7] = hv[0];
+            phi[i >> 3][(i & 7) + 1] = hv[1];
+            l0 = __builtin_amdgcn_fdot2(hv, ones2, l0, false);
+            if constexpr (SPLIT_P) {
+                const half2_t lv = {(_Float16) (p0 - (float) hv[0]), (_Float16) (p1 - (float) hv[1])};
+                plo[i >> 3][i & 7] = lv[0];
+                plo[i >> 3][(i & 7) + 1] = lv[1];
+            }
+        }
+        return l0;
+    };
+    auto lo_sum = [&](const half8_t (&plo)[2], float l0) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < 8; i += 2)
+                l0 = __builtin_amdgcn_fdot2((half2_t){plo[s2][i], plo[s2][i + 1]}, ones2, l0, false);
+        return l0;
+    };
+    // The reference m_run is not compared with the chunk's maximum up front. The weights are
+    // computed against it directly; a score more than ~9 above it (or any visible key of a row
+    // that has seen none) yields a weight >= 2^16, which overflows f16 and makes the lane's sum
+    // infinite. Only then is the row maximum taken, the reference moved (O and l rescaled) and
+    // the weights recomputed, so weights stay below 2^16 and the common chunk pays no max.
+    // raw(): the chunk's scores s*c without the reference (single-f16 kernels: recomputed from a
+    // zero accumulator, since a row's first bias, PF_LOG2_PSCALE - PF_M_INIT, dwarfs them).
+    auto softmax = [&](float16_t &S, auto raw, half8_t (&phi)[2], half8_t (&plo)[2]) {
+        float l_new = weights(S, PF_LOG2_PSCALE - m_run, l_run, phi, plo);
+        if (__builtin_amdgcn_ballot_w64(l_new == INFINITY) != 0) {
+            float16_t R;
+            if constexpr (SPLIT_P) {
+                R = S * c;
+            } else {
+                R = raw();
+            }
+            float lmax = fmaxf(R[0], R[1]);
+#pragma unroll
+            for (int i = 2; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(R[i], R[i + 1]));
             const float m_new = fmaxf(m_run, fmaxf(lmax, __shfl_xor(lmax, 32)));
             const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
             l_run *= corr;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) O[mb] *= corr;
-        }
-        const float bias = PF_LOG2_PSCALE - m_run;
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(S[i], c, bias));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(S[i + 1], c, bias));
-            const half2_t hv = {(_Float16) p0, (_Float16) p1};
-            phi[i >> 3][i & 7] = hv[0];
-            phi[i >> 3][(i & 7) + 1] = hv[1];
-            l_run = __builtin_amdgcn_fdot2(hv, ones2, l_run, false);
+            const float bias = PF_LOG2_PSCALE - m_run;
             if constexpr (SPLIT_P) {
-                const half2_t lv = {(_Float16) (p0 - (float) hv[0]), (_Float16) (p1 - (float) hv[1])};
-                plo[i >> 3][i & 7] = lv[0];
-                plo[i >> 3][(i & 7) + 1] = lv[1];
-                l_run = __builtin_amdgcn_fdot2(lv, ones2, l_run, false);
+                l_new = weights(S, bias, l_run, phi, plo);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    biasv[i] = bias;
+                    S[i] = R[i] + bias;
+                }
+                l_new = weights(S, bias, l_run, phi, plo);
             }
         }
+        if constexpr (SPLIT_P) l_new = lo_sum(plo, l_new);
+        l_run = l_new;
     };
     // P.V per channel block: operands of steps 0, 1 from four transposing reads
     auto pv = [&](auto boff_c, auto kc_c, const half8_t (&phi)[2], const half8_t (&plo)[2]) {
@@ -297,10 +372,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
         const uint32_t jc = kt * PF_KT;
         if (jc > w_pmax || jc + 31u < w_bmin) return;
         using K0 = std::integral_constant<int, 0>;
-        float16_t S = qk(boff_c, K0{});
-        if (jc + 31u > w_pmin || (a.n_swa && jc < w_bmax)) mask(S, jc);
+        float16_t zero;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) zero[i] = 0.f;
+        const bool masked = jc + 31u > w_pmin || (a.n_swa && jc < w_bmax);
+        float16_t S = qk(boff_c, K0{}, SPLIT_P ? zero : biasv);
+        if (masked) mask(S, jc);
+        auto raw = [&]() {
+            float16_t R = qk(boff_c, K0{}, zero);
+            if (masked) mask(R, jc);
+            return R;
+        };
         half8_t phi[2], plo[2];
-        softmax(S, phi, plo);
+        softmax(S, raw, phi, plo);
         pv(boff_c, K0{}, phi, plo);
     };
 
@@ -372,8 +456,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     }
 }
 
+// Four waves per SIMD (128 VGPRs): the single-f16 kernels are held to it.
+#define PF_OCC __attribute__((amdgpu_waves_per_eu(4, 4)))
 #define PREFILL_KERNEL(GRP)                                                                      \
-    extern "C" __global__ __launch_bounds__(MOEARC_PREFILL_THREADS) void moearc_attn_prefill_g##GRP( \
+    extern "C" __global__ __launch_bounds__(MOEARC_PREFILL_THREADS) PF_OCC void moearc_attn_prefill_g##GRP( \
         const PrefillArgs a) {                                                                   \
         prefill_body<GRP, false>(a);                                                             \
     }                                                                                            \

@@ -71,7 +71,9 @@ struct moearc_ctx {
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[5] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2
     hipFunction_t f_dec_merge = nullptr;
+    unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
+    hipFunction_t f_prefill_precise[4] = {};  // the same with p split into f16 hi + lo
     bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
     bool profiling = false;
     std::vector<Pending> pending;
@@ -351,7 +353,7 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
                               64u * kb * wpk, a, "attn_decode.split", n_heads, head_dim);
         if (rc) return rc;
         if (any_split && !fused) {
-            const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads), 256, a,
+            const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads), c->merge_threads, a,
                                   "attn_decode.merge", n_heads, head_dim);
             if (rm) return rm;
         }
@@ -414,12 +416,23 @@ moearc_ctx *moearc_ctx_create(void) {
             return nullptr;
         }
     }
+    int merge_threads = 0;
+    if (hipFuncGetAttribute(&merge_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_dec_merge) !=
+            hipSuccess || merge_threads < 64 || merge_threads > 1024) {
+        std::fprintf(stderr, "moearc: cannot read the merge kernel's work-group size\n");
+        hipModuleUnload(c->module);
+        hipStreamDestroy(c->stream);
+        delete c;
+        return nullptr;
+    }
+    c->merge_threads = (unsigned) merge_threads;
     if (const char *pp = std::getenv("MOEARC_PREFILL_PRECISE")) c->prefill_precise = pp[0] == '1';
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
+        const bool precise = i >= 4;
         char name[64];
-        std::snprintf(name, sizeof(name), "moearc_attn_prefill_%sg%d", c->prefill_precise ? "precise_" : "",
-                      1 << i);
-        if (hipModuleGetFunction(&c->f_prefill[i], c->module, name) != hipSuccess) {
+        std::snprintf(name, sizeof(name), "moearc_attn_prefill_%sg%d", precise ? "precise_" : "", 1 << (i & 3));
+        hipFunction_t *slot = precise ? &c->f_prefill_precise[i & 3] : &c->f_prefill[i & 3];
+        if (hipModuleGetFunction(slot, c->module, name) != hipSuccess) {
             std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), name);
             hipModuleUnload(c->module);
             hipStreamDestroy(c->stream);
@@ -728,7 +741,12 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     if (group != 1 && group != 2 && group != 4 && group != 8) return ERR_ARG;
     if (pos0 + n_q > 0xFFFFFFFFul) return ERR_ARG;
     const int gi = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : 3;
-    if (!c->f_prefill[gi]) return ERR;
+    // The single-f16 kernels pre-scale Q by scale*log2(e) in f16, which stays in range for
+    // |scale*log2(e)| <= 1 (every softmax scale up to 0.69); larger scales take the precise kernels.
+    const float scale_log2e = scale * 1.4426950408889634f;
+    const bool precise = c->prefill_precise || !(std::fabs(scale_log2e) <= 1.0f);
+    hipFunction_t f = precise ? c->f_prefill_precise[gi] : c->f_prefill[gi];
+    if (!f) return ERR;
     PrefillArgs a{};
     a.q = (const uint16_t *) q;
     a.k_pages = (const uint16_t *) k_pages;
@@ -744,7 +762,7 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     a.group = (uint32_t) group;
     a.pt_shift = log2u(page_tokens);
     a.out_f16 = out_type;
-    a.scale_log2e = scale * 1.4426950408889634f;
+    a.scale_log2e = scale_log2e;
     // Each work-group stages the block-table entries of its key span in LDS (PF_PT_CAP = 2048).
     {
         const unsigned long tok = MOEARC_PREFILL_ROWS / group;
@@ -757,7 +775,7 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     a.n_qtiles = (uint32_t) ((rows + rows_per_tile - 1) / rows_per_tile);
     const uint64_t wgs = (uint64_t) a.n_qtiles * n_kv_heads;
     if (wgs > 0x7FFFFFFFull) return ERR_ARG;
-    return launch(c, c->f_prefill[gi], (unsigned) wgs, MOEARC_PREFILL_THREADS, a, "attn_prefill",
+    return launch(c, f, (unsigned) wgs, MOEARC_PREFILL_THREADS, a, "attn_prefill",
                   n_heads, head_dim);
 }
 
