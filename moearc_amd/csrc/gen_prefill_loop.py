@@ -1,0 +1,392 @@
+"""Generates prefill_loop.inc: the key loop of the default prefill kernels (prefill_fast.hip) as one
+gfx950 inline-asm statement.
+
+Why asm: the loop keeps ~210 VGPRs of state (four 16-register O accumulators, two score tuples,
+two bias tuples, Q, K and V^T operands). Written in C++, the compiler's allocator copies whole
+accumulator tuples at every join and spills; and register constraints on separate asm statements
+do not pin a value between them. One asm statement over a fixed register map does.
+
+Run `python gen_prefill_loop.py` after editing; the output is committed (the build does not run
+this script).
+
+Register map (VGPRs):
+  v0-v15 v16-v31     O of block A, channel blocks 0 and 1      v128-v143  Q of block A (4 x half8)
+  v32-v47 v48-v63    O of block B                              v144-v159  Q of block B
+  v64-v79 v80-v95    S of blocks A and B (exponents, weights)  v160-v175  K operands of a chunk
+  v96-v111 v112-v127 bias of blocks A and B (the QK^T init)    v176-v191  V^T operands of a chunk
+  v192-v199          P operands (one block at a time)          v200-v207  temporaries
+  v208 v209          reference m of A, B                       v210 v211  row sums l of A, B
+  v212-v215          LDS addresses of the K operand reads (buffer 0, chunk 0)
+  v216-v217          LDS addresses of the V^T operand reads
+  v218 v219 v220 v221  mask parameters c_A, span_A, c_B, span_B (key offset of chunk 0 relative to
+                     the row's window start; row position minus window start)
+  v222-v229          block-table entries of four tiles (two per tile: this lane's two copy keys)
+  v230-v233          copy offsets within a tile, uniform path (K copy 0, 1, V copy 0, 1)
+  v234-v241          per-lane 64-bit copy bases (K copy 0, 1, V copy 0, 1): pages base + chunk
+  v242               this lane's first copy key within a tile (16 * wave + lane / 8)
+  v243               ds_bpermute address of lane ^ 32
+  v244-v247          temporaries                               v248-v249  block-table base (64-bit)
+  v250-v255          unused
+SGPRs s64-s81 are the loop's own (listed as clobbers).
+"""
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+NBUF = 4          # LDS tile buffers
+BUF = 16384       # bytes per buffer: K tile (8 KiB) + V tile (8 KiB)
+TILE = 8192
+
+out = []
+
+
+def ins(s):
+    out.append(s)
+
+
+def mfma(d, a, b, c):
+    ins(f"v_mfma_f32_32x32x16_f16 v[{d}], v[{a}], v[{b}], {c}")
+
+
+K_OPS = ["160:163", "164:167", "168:171", "172:175"]
+
+
+def qk_exp(sd, q0, bias, e):
+    """S_D = K . Q^T + bias (4 chained MFMAs) beside the exponentials and row-sum tree of the
+    weights in v[e..e+15] (in place); the sum lands in v206."""
+    E = list(range(e, e + 16))
+    qs = [f"{q0 + 4 * t}:{q0 + 4 * t + 3}" for t in range(4)]
+    sd_rng = f"v[{sd}]"
+    exps = lambda idx: [ins(f"v_exp_f32 v{E[i]}, v{E[i]}") for i in idx]
+    add = lambda d, a, b: ins(f"v_add_f32 v{d}, v{a}, v{b}")
+    mfma(sd, K_OPS[0], qs[0], f"v[{bias}]")
+    exps(range(0, 4))
+    mfma(sd, K_OPS[1], qs[1], sd_rng)
+    exps(range(4, 8))
+    add(200, E[0], E[1]); add(201, E[2], E[3])
+    mfma(sd, K_OPS[2], qs[2], sd_rng)
+    exps(range(8, 12))
+    add(202, E[4], E[5]); add(203, E[6], E[7]); add(200, 200, 201)
+    mfma(sd, K_OPS[3], qs[3], sd_rng)
+    exps(range(12, 16))
+    add(204, E[8], E[9]); add(205, E[10], E[11]); add(202, 202, 203)
+    add(206, E[12], E[13]); add(207, E[14], E[15]); add(204, 204, 205)
+    add(206, 206, 207); add(200, 200, 202); add(204, 204, 206)
+    add(206, 200, 204)
+
+
+def pv(o0, o1, e):
+    """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7]."""
+    cvt = lambda d, a, b: ins(f"v_cvt_pk_f16_f32 v{d}, v{e + a}, v{e + b}")
+    cvt(192, 0, 1); cvt(193, 2, 3); cvt(194, 4, 5); cvt(195, 6, 7)
+    ins("s_nop 2")  # VALU write -> MFMA read
+    mfma(o0, "176:179", "192:195", f"v[{o0}]")
+    cvt(196, 8, 9); cvt(197, 10, 11)
+    mfma(o1, "184:187", "192:195", f"v[{o1}]")
+    cvt(198, 12, 13); cvt(199, 14, 15)
+    ins("s_nop 2")
+    mfma(o0, "180:183", "196:199", f"v[{o0}]")
+    mfma(o1, "188:191", "196:199", f"v[{o1}]")
+
+
+def read_k(off, dst="160"):
+    d = int(dst)
+    for t in range(4):
+        ins(f"ds_read_b128 v[{d + 4 * t}:{d + 4 * t + 3}], v{212 + t} offset:{off}")
+
+
+def read_v(off):
+    # operand (mb, s) at v[176 + 8mb + 4s]: low half keys 16s + 4h.., high half 16s + 8 + 4h..
+    for mb in range(2):
+        for e in range(4):
+            r = 176 + 8 * mb + 2 * e
+            ins(f"ds_read_b64_tr_b16 v[{r}:{r + 1}], v{216 + mb} offset:{off + 1024 * e}")
+
+
+def pid_load(slot, tile_sgpr, label):
+    """Block-table entries of tile s[tile_sgpr] (clamped to the last tile) for this lane's two copy
+    keys (clamped to the last query position) into v[222 + 2 slot], v[223 + 2 slot]."""
+    ins(f"s_min_u32 s79, s{tile_sgpr}, %[ntm1]")
+    ins("s_lshl_b32 s79, s79, 6")
+    ins("s_add_u32 s79, s79, %[kb0]")
+    for i in range(2):
+        ins(f"v_add3_u32 v244, s79, v242, {8 * i}")
+        ins("v_min_u32 v244, %[plast], v244")
+        ins("v_lshrrev_b32 v244, %[sh], v244")
+        ins("v_lshlrev_b32 v244, 2, v244")
+        ins("v_add_co_u32 v246, vcc, v248, v244")
+        ins("v_addc_co_u32 v247, vcc, 0, v249, vcc")
+        ins(f"global_load_dword v{222 + 2 * slot + i}, v[246:247], off")
+
+
+def copy_tile(slot, tile_sgpr, buf, label):
+    """LDS-DMA copy of tile s[tile_sgpr] (clamped) into buffer `buf` with the entries in `slot`:
+    wave-uniform scalar-base form when the tile lies in one page (pages >= 64 keys) wholly below
+    the last query position, per-lane addresses otherwise. Four memory operations either way."""
+    ins(f"s_min_u32 s71, s{tile_sgpr}, %[ntm1]")
+    ins("s_lshl_b32 s70, s71, 6")
+    ins("s_add_u32 s70, s70, %[kb0]")          # first key of the tile
+    ins("s_cmp_lt_u32 %[sh], 6")
+    ins(f"s_cbranch_scc1 {label}_lane")
+    ins("s_add_u32 s73, s70, 63")
+    ins("s_cmp_gt_u32 s73, %[plast]")
+    ins(f"s_cbranch_scc1 {label}_lane")
+    ins(f"v_readfirstlane_b32 s72, v{222 + 2 * slot}")
+    ins("s_lshl_b32 s72, s72, %[sh]")
+    ins("s_and_b32 s73, s70, %[pmask]")
+    ins("s_or_b32 s72, s72, s73")               # row of the tile's first key
+    ins("s_mul_i32 s74, s72, %[rowb]")
+    ins("s_mul_hi_u32 s75, s72, %[rowb]")       # byte offset of the row (64-bit)
+    for kind, base, voff in (("k", "kp", (230, 231)), ("v", "vp", (232, 233))):
+        ins(f"s_add_u32 s68, s74, %[{base}lo]")
+        ins(f"s_addc_u32 s69, s75, %[{base}hi]")
+        for i in range(2):
+            lds_off = buf * BUF + (TILE if kind == "v" else 0) + 1024 * i
+            ins(f"s_add_u32 m0, %[ldsw], {lds_off}")
+            ins("s_nop 0")
+            ins(f"global_load_lds_dwordx4 v{voff[i]}, s[68:69]")
+    ins(f"s_branch {label}_done")
+    ins(f"{label}_lane:")
+    for i in range(2):
+        ins(f"v_add3_u32 v244, s70, v242, {8 * i}")
+        ins("v_min_u32 v244, %[plast], v244")
+        ins("v_and_b32 v244, %[pmask], v244")
+        ins(f"v_lshlrev_b32 v245, %[sh], v{222 + 2 * slot + i}")
+        ins("v_or_b32 v244, v244, v245")         # row of this lane's key
+        for kind, pair in (("k", 234 + 2 * i), ("v", 238 + 2 * i)):
+            ins(f"v_mad_u64_u32 v[246:247], vcc, v244, %[rowb], v[{pair}:{pair + 1}]")
+            lds_off = buf * BUF + (TILE if kind == "v" else 0) + 1024 * i
+            ins(f"s_add_u32 m0, %[ldsw], {lds_off}")
+            ins("s_nop 0")
+            ins("global_load_lds_dwordx4 v[246:247], off")
+    ins(f"{label}_done:")
+
+
+def tile_step(si, label):
+    """Tile step t = s65: wait for this wave's copies of tile t and the entries of tile t + 2,
+    meet the other waves, copy tile t + 2 into buffer (t + 2) % 4, load the entries of tile t + 4.
+    Six memory operations per step, so the wait is vmcnt(6)."""
+    sc = (si + 2) % NBUF
+    ins("s_waitcnt vmcnt(6)")
+    ins("s_barrier")
+    ins("s_add_u32 s80, s65, 2")
+    copy_tile(sc, 80, sc, f"{label}_c")
+    ins("s_add_u32 s80, s65, 4")
+    pid_load(si, 80, f"{label}_p")
+
+
+def chunk(bi, ci, label):
+    bn = (bi + 1) % NBUF if ci else bi
+    off = bi * BUF + 4096 * ci
+    offn = bn * BUF + 4096 * (ci ^ 1)
+    if ci == 1:
+        # chunk j + 1 opens tile t = (j + 1) / 2
+        ins("s_add_u32 s65, s64, 1")
+        ins("s_lshr_b32 s65, s65, 1")
+        ins("s_cmp_ge_u32 s65, %[ntiles]")
+        ins(f"s_cbranch_scc1 {label}_nostep")
+        tile_step(bn, f"{label}_t")
+        ins(f"{label}_nostep:")
+    # R1: S_B(j) | weights of A(j)
+    qk_exp("80:95", 144, "112:127", 64)
+    ins("v_cmp_ngt_f32 vcc, 0x477fe000, v206")  # some lane's weights sum to >= 65504 (or NaN)
+    ins(f"s_cbranch_vccz {label}_a_ok")
+    ins("s_mov_b32 s78, s64")
+    ins("s_call_b64 s[66:67], pff_rescale_a")
+    ins(f"{label}_a_ok:")
+    ins("v_add_f32 v210, v210, v206")
+    read_k(offn)
+    # R2: O_A += V(j)^T . P_A(j)
+    ins("s_waitcnt lgkmcnt(4)")
+    pv("0:15", "16:31", 64)
+    # mask of S_B(j)
+    ins("s_mov_b32 s78, s64")
+    ins("s_cmp_lt_u32 s64, %[jlob]")
+    ins(f"s_cbranch_scc1 {label}_mb")
+    ins("s_cmp_gt_u32 s64, %[jhib]")
+    ins(f"s_cbranch_scc0 {label}_mb_ok")
+    ins(f"{label}_mb:")
+    ins("s_call_b64 s[66:67], pff_mask_b")
+    ins(f"{label}_mb_ok:")
+    # R3: S_A(j + 1) | weights of B(j)
+    ins("s_waitcnt lgkmcnt(0)")
+    qk_exp("64:79", 128, "96:111", 80)
+    ins("v_cmp_ngt_f32 vcc, 0x477fe000, v206")
+    ins(f"s_cbranch_vccz {label}_b_ok")
+    ins(f"s_mov_b32 s76, {off}")
+    ins(f"s_mov_b32 s77, {offn}")
+    ins("s_call_b64 s[66:67], pff_rescale_b")
+    ins(f"{label}_b_ok:")
+    ins("v_add_f32 v211, v211, v206")
+    # R4: O_B += V(j)^T . P_B(j)
+    pv("32:47", "48:63", 80)
+    read_v(offn)
+    # mask of S_A(j + 1)
+    ins("s_add_u32 s78, s64, 1")
+    ins("s_cmp_lt_u32 s78, %[jloa]")
+    ins(f"s_cbranch_scc1 {label}_ma")
+    ins("s_cmp_gt_u32 s78, %[jhia]")
+    ins(f"s_cbranch_scc0 {label}_ma_ok")
+    ins(f"{label}_ma:")
+    ins("s_call_b64 s[66:67], pff_mask_a")
+    ins(f"{label}_ma_ok:")
+    ins("s_add_u32 s64, s64, 1")
+
+
+def mask_body(e, c_reg, span_reg):
+    """Keys of chunk s78 outside each row's span -> -inf in v[e..e+15]: key offset of register i
+    is 8 (i >> 2) + (i & 3); outside iff c + 32 j + k > span (unsigned)."""
+    ins("s_lshl_b32 s79, s78, 5")
+    ins(f"v_add_u32 v244, s79, v{c_reg}")
+    ins("v_mov_b32 v245, 0xff800000")
+    for i in range(16):
+        k = 8 * (i >> 2) + (i & 3)
+        ins(f"v_add_u32 v246, {k}, v244")
+        ins(f"v_cmp_gt_u32 vcc, v246, v{span_reg}")
+        ins(f"v_cndmask_b32 v{e + i}, v{e + i}, v245, vcc")
+
+
+def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jhi, label):
+    """Raw scores of the chunk (K in v160-v175) -> v[e..], masked if the chunk needs it, the row
+    maximum across lanes n and n + 32, m moved to it, O, l and the bias rescaled, the weights
+    redone; the chunk's row-sum share lands in v206."""
+    E = list(range(e, e + 16))
+    qs = [f"{q0 + 4 * t}:{q0 + 4 * t + 3}" for t in range(4)]
+    mfma(sd, K_OPS[0], qs[0], "0")
+    for t in (1, 2, 3):
+        mfma(sd, K_OPS[t], qs[t], f"v[{sd}]")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_nop 7")  # MFMA results -> VALU
+    ins(f"s_cmp_lt_u32 s78, {jlo}")
+    ins(f"s_cbranch_scc1 {label}_m")
+    ins(f"s_cmp_gt_u32 s78, {jhi}")
+    ins(f"s_cbranch_scc0 {label}_nm")
+    ins(f"{label}_m:")
+    mask_body(e, c_reg, span_reg)
+    ins(f"{label}_nm:")
+    ins(f"v_max3_f32 v200, v{E[0]}, v{E[1]}, v{E[2]}")
+    for i in range(3, 15, 2):
+        ins(f"v_max3_f32 v200, v200, v{E[i]}, v{E[i + 1]}")
+    ins(f"v_max_f32 v200, v200, v{E[15]}")
+    ins("ds_bpermute_b32 v202, v243, v200")
+    ins("s_waitcnt lgkmcnt(0)")
+    ins(f"v_max3_f32 v202, v202, v200, v{m}")      # m_new
+    ins(f"v_sub_f32 v203, v{m}, v202")
+    ins("v_exp_f32 v203, v203")                      # corr = 2^(m_old - m_new)
+    ins(f"v_mov_b32 v{m}, v202")
+    ins("v_sub_f32 v204, 0x40e00000, v202")          # bias = 7 - m_new
+    ins(f"v_mul_f32 v{l}, v{l}, v203")
+    for i in range(32):
+        ins(f"v_mul_f32 v{o_base + i}, v{o_base + i}, v203")
+    for i in range(16):
+        ins(f"v_mov_b32 v{bias_base + i}, v204")
+    for i in range(16):
+        ins(f"v_add_f32 v{E[i]}, v{E[i]}, v204")
+    for i in range(16):
+        ins(f"v_exp_f32 v{E[i]}, v{E[i]}")
+    for k in range(8):
+        ins(f"v_add_f32 v{200 + k}, v{E[2 * k]}, v{E[2 * k + 1]}")
+    for d, a, b in ((200, 200, 201), (202, 202, 203), (204, 204, 205), (206, 206, 207),
+                    (200, 200, 202), (204, 204, 206), (206, 200, 204)):
+        ins(f"v_add_f32 v{d}, v{a}, v{b}")
+
+
+def generate():
+    # ---- prologue: entries of tiles 0 and 1, their copies, entries of tiles 2 and 3, step 0 ----
+    ins("s_mov_b32 s80, 0")
+    pid_load(0, 80, "pro_p0")
+    ins("s_mov_b32 s80, 1")
+    pid_load(1, 80, "pro_p1")
+    ins("s_waitcnt vmcnt(0)")
+    ins("s_mov_b32 s80, 0")
+    copy_tile(0, 80, 0, "pro_c0")
+    ins("s_mov_b32 s80, 2")
+    pid_load(2, 80, "pro_p2")
+    ins("s_mov_b32 s80, 1")
+    copy_tile(1, 80, 1, "pro_c1")
+    ins("s_mov_b32 s80, 3")
+    pid_load(3, 80, "pro_p3")
+    ins("s_mov_b32 s65, 0")
+    tile_step(0, "pro_t0")
+    # chunk 0's K and V^T operands, S_A(0), its mask
+    read_k(0)
+    read_v(0)
+    ins("s_waitcnt lgkmcnt(8)")
+    mfma("64:79", K_OPS[0], "128:131", "v[96:111]")
+    for t in (1, 2, 3):
+        mfma("64:79", K_OPS[t], f"{128 + 4 * t}:{131 + 4 * t}", "v[64:79]")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_mov_b32 s64, 0")
+    ins("s_mov_b32 s78, 0")
+    ins("s_cmp_lt_u32 s78, %[jloa]")
+    ins("s_cbranch_scc1 pro_ma")
+    ins("s_cmp_gt_u32 s78, %[jhia]")
+    ins("s_cbranch_scc0 pro_ma_ok")
+    ins("pro_ma:")
+    ins("s_call_b64 s[66:67], pff_mask_a")
+    ins("pro_ma_ok:")
+    # ---- main loop: four tiles (eight chunks) per pass; buffers and entry slots fixed ----
+    ins("pff_loop:")
+    for k in range(NBUF):
+        for ci in range(2):
+            chunk(k, ci, f"c{k}{ci}")
+        ins("s_cmp_ge_u32 s64, %[nc]")
+        ins("s_cbranch_scc1 pff_end")
+    ins("s_branch pff_loop")
+    # ---- rare paths (called with s_call_b64 s[66:67], return with s_setpc_b64) ----
+    ins("pff_mask_a:")
+    mask_body(64, 218, 219)
+    ins("s_setpc_b64 s[66:67]")
+    ins("pff_mask_b:")
+    mask_body(80, 220, 221)
+    ins("s_setpc_b64 s[66:67]")
+    ins("pff_rescale_a:")  # K(j) is in v160-v175
+    rescale_body("64:79", 64, 128, 0, 96, 208, 210, 218, 219, "%[jloa]", "%[jhia]", "ra")
+    ins("s_setpc_b64 s[66:67]")
+    ins("pff_rescale_b:")  # K(j + 1) is in v160-v175: read K(j) (LDS offset s76), then K(j + 1) (s77)
+    for t in range(4):
+        ins(f"v_add_u32 v{244 + t}, s76, v{212 + t}")
+    ins("s_waitcnt lgkmcnt(0)")
+    for t in range(4):
+        ins(f"ds_read_b128 v[{160 + 4 * t}:{163 + 4 * t}], v{244 + t}")
+    ins("s_waitcnt lgkmcnt(0)")
+    rescale_body("80:95", 80, 144, 32, 112, 209, 211, 220, 221, "%[jlob]", "%[jhib]", "rb")
+    for t in range(4):
+        ins(f"v_add_u32 v{244 + t}, s77, v{212 + t}")
+    for t in range(4):
+        ins(f"ds_read_b128 v[{160 + 4 * t}:{163 + 4 * t}], v{244 + t}")
+    ins("s_waitcnt lgkmcnt(0)")
+    ins("s_setpc_b64 s[66:67]")
+    # ---- end: every copy and read has landed; the last MFMA results are readable ----
+    ins("pff_end:")
+    ins("s_waitcnt vmcnt(0) lgkmcnt(0)")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_nop 7")
+
+
+def emit():
+    import re
+    generate()
+    # labels get the asm statement's unique number (%=) so that several kernels can inline it
+    label_defs = sorted({l[:-1] for l in out if l.endswith(":")}, key=len, reverse=True)
+
+    def fix(line):
+        for lab in label_defs:
+            line = re.sub(r"\b" + re.escape(lab) + r"\b", lab + "_%=", line)
+        return line
+
+    lines = [fix(l) for l in out]
+    path = os.path.join(HERE, "prefill_loop.inc")
+    with open(path, "w") as f:
+        f.write("// Generated by gen_prefill_loop.py: the key loop of the default prefill kernels as one\n")
+        f.write("// gfx950 asm statement (register map and semantics in that script and prefill_fast.hip).\n")
+        for l in lines:
+            f.write('"' + l + '\\n\\t"\n')
+    print(f"wrote {path}: {len(lines)} instructions and labels")
+
+
+if __name__ == "__main__":
+    emit()

@@ -70,7 +70,8 @@ struct DecodeGeneralArgs {
 
 // Chunked prefill: query rows ((token, head) pairs of one KV head's group) per work-group and the
 // work-group size.
-#define MOEARC_PREFILL_ROWS 128
+#define MOEARC_PREFILL_ROWS 128        // precise (hi/lo weights) kernels
+#define MOEARC_PREFILL_FAST_ROWS 256   // default kernels: 64 rows per wave
 #define MOEARC_PREFILL_THREADS 256
 
 // Chunked prefill over f16 paged KV, head_dim 64.

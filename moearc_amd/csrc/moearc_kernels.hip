@@ -4,4 +4,5 @@
 #include "decode_general.hip"
 #include "decode_splitk.hip"
 #include "prefill.hip"
+#include "prefill_fast.hip"
 #include "rope.hip"

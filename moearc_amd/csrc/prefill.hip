@@ -124,7 +124,8 @@ __device__ __forceinline__ void pf_read_vt(u32x2_t (&r)[4], uint32_t base) {
 // LDS DMA of 16 bytes per lane from a wave-uniform global base plus a per-lane 32-bit offset to
 // LDS address lds + 16 * lane (the scalar-base form: no 64-bit address arithmetic per lane).
 __device__ __forceinline__ void pf_copy16(const void *sbase, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+    // M0 is read by the DMA one wait state after it is written
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
 
 template <int GROUP, bool SPLIT_P>
@@ -424,8 +425,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
             compute_tile(tile(r + k), std::integral_constant<int, k * (int) BUF_BYTES>{});
         });
     }
-    // the clamped copies past the last tile may still be in flight: they must land before this
-    // work-group's LDS is released
+    // The clamped copies past the last tile may still be in flight: they must land before this
+    // work-group's LDS is released. The block-table loads of the last steps are in flight too;
+    // the wait names their registers so that none is given to another value before they land
+    // (an asm load's destination is written whenever the data arrives).
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(pid[0]), "+v"(pid[1]), "+v"(pid[2]), "+v"(pid[3])
+                 :
+                 : "memory");
     __builtin_amdgcn_s_waitcnt(0);
 
     // ---- finalise: row sum over the lane pair, the sink, the normalisation, the store ---------
@@ -456,13 +463,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     }
 }
 
-// Four waves per SIMD (128 VGPRs): the single-f16 kernels are held to it.
-#define PF_OCC __attribute__((amdgpu_waves_per_eu(4, 4)))
+// The precise kernels (p split into f16 hi + lo); the default single-f16 kernels are in
+// prefill_fast.hip.
 #define PREFILL_KERNEL(GRP)                                                                      \
-    extern "C" __global__ __launch_bounds__(MOEARC_PREFILL_THREADS) PF_OCC void moearc_attn_prefill_g##GRP( \
-        const PrefillArgs a) {                                                                   \
-        prefill_body<GRP, false>(a);                                                             \
-    }                                                                                            \
     extern "C" __global__ __launch_bounds__(MOEARC_PREFILL_THREADS) void                        \
         moearc_attn_prefill_precise_g##GRP(const PrefillArgs a) {                                \
         prefill_body<GRP, true>(a);                                                              \

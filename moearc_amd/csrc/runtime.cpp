@@ -770,7 +770,8 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
         const unsigned long win = n_swa ? (tok + n_swa + 64) / page_tokens + 2 : full;
         if (std::min(full, win) > 2048ul) return ERR_ARG;
     }
-    const uint32_t rows_per_tile = MOEARC_PREFILL_ROWS;  // query rows (token x head) per work-group
+    // query rows (token x head) per work-group
+    const uint32_t rows_per_tile = precise ? MOEARC_PREFILL_ROWS : MOEARC_PREFILL_FAST_ROWS;
     const uint64_t rows = (uint64_t) n_q * group;
     a.n_qtiles = (uint32_t) ((rows + rows_per_tile - 1) / rows_per_tile);
     const uint64_t wgs = (uint64_t) a.n_qtiles * n_kv_heads;
