@@ -377,77 +377,85 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
     if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Split merge: one work-group of MERGE_WAVES waves per (sequence, query head) of every sequence
-// whose span was split (records are [item][kv head]). Splits are dealt to the waves, MERGE_BATCH
-// per wave per round; each lane owns one channel and issues every load of a round (its channel,
-// and the split's max and denominator) before using any, so up to MERGE_WAVES * MERGE_BATCH
-// splits cost one memory round trip. Runs as the next launch on the stream: the kernel boundary
-// makes the records visible, with no device-scope cache maintenance inside either kernel
-// (merging inside one launch needs a device-scope release -- an L2 write-back -- in every
-// work-group, measured to cost more than this second launch).
-#ifndef MERGE_WAVES
-#define MERGE_WAVES 4
-#endif
+// Split merge: for every sequence whose span was split (records are [item][kv head]), one
+// MOEARC_MERGE_THREADS (256) work-group per (sequence, query head, quarter of the 64 channels), so a launch has
+// four work-groups per head. Lane (sg, c) owns channel c of the quarter for the splits
+// sg, sg + 16, ...; it issues every load of a round (its channel, and each split's max and
+// denominator) before using any, so up to 16 * MERGE_BATCH splits cost one memory round trip.
+// The 16 split groups then combine by shuffles within a wave and through LDS across the four
+// waves. Runs as the next launch on the stream: the kernel boundary makes the records visible,
+// with no device-scope cache maintenance inside either kernel (merging inside one launch needs a
+// device-scope release -- an L2 write-back -- in every work-group, measured to cost more than
+// this second launch).
 #ifndef MERGE_BATCH
-#define MERGE_BATCH 32
+#define MERGE_BATCH 16
 #endif
-extern "C" __global__ __launch_bounds__(64 * MERGE_WAVES) void moearc_attn_decode_merge(
-    const DecodeArgs a) {
-    __shared__ float red_m[MERGE_WAVES], red_l[MERGE_WAVES];
-    __shared__ float red_o[MERGE_WAVES][64];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t b = blockIdx.x / a.n_heads;
-    const uint32_t hh = blockIdx.x - b * a.n_heads;
+
+// (m, l, o) of two partial softmax sums over disjoint key sets, combined in the frame of the
+// larger max; a side that saw no keys has m = -inf and drops out.
+__device__ __forceinline__ void merge_partial(float &m, float &l, float &o, float m2, float l2, float o2) {
+    const float M = fmaxf(m, m2);
+    const float f1 = m == -INFINITY ? 0.f : exp2_fast(m - M);
+    const float f2 = m2 == -INFINITY ? 0.f : exp2_fast(m2 - M);
+    m = M;
+    l = l * f1 + l2 * f2;
+    o = o * f1 + o2 * f2;
+}
+
+extern "C" __global__ __launch_bounds__(MOEARC_MERGE_THREADS) void moearc_attn_decode_merge(const DecodeArgs a) {
+    __shared__ float red[4][3][16];  // [wave][m, l, o][channel]
+    const uint32_t tid = threadIdx.x, c = tid & 15u, sg = tid >> 4, wave = tid >> 6;
+    const uint32_t per_seq = a.n_heads * MOEARC_MERGE_PARTS;
+    const uint32_t b = blockIdx.x / per_seq;
+    const uint32_t rem = blockIdx.x - b * per_seq;
+    const uint32_t hh = rem / MOEARC_MERGE_PARTS, part = rem - hh * MOEARC_MERGE_PARTS;
     const uint32_t nsplit = a.item_begin[b + 1] - a.item_begin[b];
     if (nsplit <= 1u) return;  // finished by the split kernel itself
     const uint32_t G = a.n_kv_heads;
     const uint32_t kvh = hh / a.group, hn = hh - kvh * a.group;
+    const uint32_t d = 16u * part + c;
     const float *rec0 = a.ws + ((uint64_t) a.item_begin[b] * G + kvh) * MOEARC_PARTIAL_FLOATS;
     const uint64_t rstride = (uint64_t) G * MOEARC_PARTIAL_FLOATS;
-    // Each wave keeps an online (max, denominator, output) over its splits, rescaling per round.
-    float m_w = -INFINITY, l_w = 0.f, o_w = 0.f;
-    for (uint32_t s0 = wave; s0 < nsplit; s0 += MERGE_WAVES * MERGE_BATCH) {
+    float m_t = -INFINITY, l_t = 0.f, o_t = 0.f;
+    for (uint32_t s0 = sg; s0 < nsplit; s0 += 16u * MERGE_BATCH) {
         float v[MERGE_BATCH], ms[MERGE_BATCH], ls[MERGE_BATCH];
 #pragma unroll
         for (int k = 0; k < MERGE_BATCH; ++k) {
-            const uint32_t s = min(s0 + (uint32_t) k * MERGE_WAVES, nsplit - 1u);
+            const uint32_t s = min(s0 + 16u * (uint32_t) k, nsplit - 1u);
             const float *r = rec0 + s * rstride;
-            v[k] = r[32u + hn * 64u + lane];
+            v[k] = r[32u + hn * 64u + d];
             ms[k] = r[hn];
             ls[k] = r[16u + hn];
         }
-        float mr = m_w;
+        float mr = m_t;
 #pragma unroll
         for (int k = 0; k < MERGE_BATCH; ++k) mr = fmaxf(mr, ms[k]);  // duplicates are harmless
-        const float corr = exp2_fast(m_w - mr);
-        l_w *= corr;
-        o_w *= corr;
+        const float corr = exp2_fast(m_t - mr);  // first round: exp2(-inf) = 0
+        l_t *= corr;
+        o_t *= corr;
 #pragma unroll
         for (int k = 0; k < MERGE_BATCH; ++k) {
-            const bool live = s0 + (uint32_t) k * MERGE_WAVES < nsplit;
+            const bool live = s0 + 16u * (uint32_t) k < nsplit;
             const float f = live ? exp2_fast(ms[k] - mr) : 0.f;
-            l_w = fmaf(ls[k], f, l_w);
-            o_w = fmaf(v[k], f, o_w);
+            l_t = fmaf(ls[k], f, l_t);
+            o_t = fmaf(v[k], f, o_t);
         }
-        m_w = mr;
+        m_t = mr;
     }
-    if (lane == 0) red_m[wave] = m_w;
-    __syncthreads();
-    float M = red_m[0];
+    // the four split groups of this wave (lanes c, c + 16, c + 32, c + 48)
 #pragma unroll
-    for (int w = 1; w < MERGE_WAVES; ++w) M = fmaxf(M, red_m[w]);
-    const float f = exp2_fast(m_w - M);  // a wave without splits has m_w = -inf: f = 0
-    red_o[wave][lane] = o_w * f;
-    if (lane == 0) red_l[wave] = l_w * f;
+    for (int x = 16; x <= 32; x <<= 1)
+        merge_partial(m_t, l_t, o_t, __shfl_xor(m_t, x), __shfl_xor(l_t, x), __shfl_xor(o_t, x));
+    if ((tid & 63u) < 16u) {
+        red[wave][0][c] = m_t;
+        red[wave][1][c] = l_t;
+        red[wave][2][c] = o_t;
+    }
     __syncthreads();
-    if (wave == 0) {
-        float tot = 0.f, L = 0.f;
+    if (tid < 16u) {
 #pragma unroll
-        for (int w = 0; w < MERGE_WAVES; ++w) {
-            tot += red_o[w][lane];
-            L += red_l[w];
-        }
-        write_output(a, b, hh, lane, M, L, tot);
+        for (int w = 1; w < 4; ++w) merge_partial(m_t, l_t, o_t, red[w][0][c], red[w][1][c], red[w][2][c]);
+        write_output(a, b, hh, d, m_t, l_t, o_t);
     }
 }
 

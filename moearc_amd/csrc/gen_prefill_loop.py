@@ -27,7 +27,8 @@ Register map (VGPRs):
   v243               ds_bpermute address of lane ^ 32
   v244-v247          temporaries                               v248-v249  block-table base (64-bit)
   v250-v255          unused
-SGPRs s64-s81 are the loop's own (listed as clobbers).
+SGPRs s64-s85 are the loop's own (listed as clobbers); s[82:83] and s[84:85] hold the rescale tests
+of blocks A and B (lanes whose chunk exponents reach the threshold %[thr]).
 """
 import os
 
@@ -37,10 +38,17 @@ BUF = 16384       # bytes per buffer: K tile (8 KiB) + V tile (8 KiB)
 TILE = 8192
 
 out = []
+ool = []  # out-of-line blocks (rare paths), emitted after the main loop
 
 
 def ins(s):
     out.append(s)
+
+
+def ool_block(label, body, back):
+    """A rare path placed after the loop: `label`, its instructions, a branch back to `back`. The
+    common path reaches it by a conditional branch that is normally not taken (falls through)."""
+    ool.extend([f"{label}:", *body, f"s_branch {back}"])
 
 
 def mfma(d, a, b, c):
@@ -51,41 +59,64 @@ K_OPS = ["160:163", "164:167", "168:171", "172:175"]
 
 
 def qk_exp(sd, q0, bias, e):
-    """S_D = K . Q^T + bias (4 chained MFMAs) beside the exponentials and row-sum tree of the
-    weights in v[e..e+15] (in place); the sum lands in v206."""
-    E = list(range(e, e + 16))
+    """S_D = K . Q^T + bias (4 chained MFMAs) beside the 16 exponentials of the weights in
+    v[e..e+15] (in place), four after each MFMA."""
     qs = [f"{q0 + 4 * t}:{q0 + 4 * t + 3}" for t in range(4)]
-    sd_rng = f"v[{sd}]"
-    exps = lambda idx: [ins(f"v_exp_f32 v{E[i]}, v{E[i]}") for i in idx]
-    add = lambda d, a, b: ins(f"v_add_f32 v{d}, v{a}, v{b}")
-    mfma(sd, K_OPS[0], qs[0], f"v[{bias}]")
-    exps(range(0, 4))
-    mfma(sd, K_OPS[1], qs[1], sd_rng)
-    exps(range(4, 8))
-    add(200, E[0], E[1]); add(201, E[2], E[3])
-    mfma(sd, K_OPS[2], qs[2], sd_rng)
-    exps(range(8, 12))
-    add(202, E[4], E[5]); add(203, E[6], E[7]); add(200, 200, 201)
-    mfma(sd, K_OPS[3], qs[3], sd_rng)
-    exps(range(12, 16))
-    add(204, E[8], E[9]); add(205, E[10], E[11]); add(202, 202, 203)
-    add(206, E[12], E[13]); add(207, E[14], E[15]); add(204, 204, 205)
-    add(206, 206, 207); add(200, 200, 202); add(204, 204, 206)
-    add(206, 200, 204)
+    for t in range(4):
+        mfma(sd, K_OPS[t], qs[t], f"v[{bias}]" if t == 0 else f"v[{sd}]")
+        for i in range(4 * t, 4 * t + 4):
+            ins(f"v_exp_f32 v{e + i}, v{e + i}")
 
 
-def pv(o0, o1, e):
-    """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7]."""
+def sum_ops(e, l):
+    """Row-sum tree of the weights v[e..e+15] into l (temporaries v200-v207), in an order that
+    keeps dependent adds apart."""
+    E = list(range(e, e + 16))
+    a = lambda d, x, y: f"v_add_f32 v{d}, v{x}, v{y}"
+    return [a(200, E[0], E[1]), a(201, E[2], E[3]), a(202, E[4], E[5]), a(203, E[6], E[7]),
+            a(200, 200, 201), a(204, E[8], E[9]), a(205, E[10], E[11]), a(202, 202, 203),
+            a(206, E[12], E[13]), a(207, E[14], E[15]), a(204, 204, 205), a(206, 206, 207),
+            a(200, 200, 202), a(204, 204, 206), a(200, 200, 204), a(l, l, 200)]
+
+
+def max_ops(e, flag):
+    """Largest exponent input of v[e..e+15] (two chains in v244, v245: free outside tile steps and
+    the mask and rescale paths) compared with the rescale threshold: s[flag:flag+1] = lanes whose
+    weights could leave f16's range."""
+    E = list(range(e, e + 16))
+    m3 = lambda d, x, y, z: f"v_max3_f32 v{d}, v{x}, v{y}, v{z}"
+    return [m3(244, E[0], E[1], E[2]), m3(245, E[3], E[4], E[5]), m3(244, 244, E[6], E[7]),
+            m3(245, 245, E[8], E[9]), m3(244, 244, E[10], E[11]), m3(245, 245, E[12], E[13]),
+            m3(244, 244, 245, E[14]), f"v_max_f32 v244, v244, v{E[15]}",
+            f"v_cmp_le_f32_e64 s[{flag}:{flag + 1}], %[thr], v244"]
+
+
+def pv(o0, o1, e, extra):
+    """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7], with
+    the VALU instructions `extra` (independent of P and of the V^T operands) spread between the
+    MFMAs: 4 before the first (they cover the VALU-write -> MFMA-read wait), then 6, 6, 6, rest.
+    The chunk places its rescale test (a max3 tree and a compare) from the fifth on: after the
+    first MFMA, far enough from the MFMAs that wrote the scores, and two MFMAs before the branch
+    that reads the compare."""
     cvt = lambda d, a, b: ins(f"v_cvt_pk_f16_f32 v{d}, v{e + a}, v{e + b}")
+    extra = list(extra)
+    take = lambda n: [ins(extra.pop(0)) for _ in range(min(n, len(extra)))]
     cvt(192, 0, 1); cvt(193, 2, 3); cvt(194, 4, 5); cvt(195, 6, 7)
-    ins("s_nop 2")  # VALU write -> MFMA read
+    if len(extra) < 2:
+        ins("s_nop 2")  # VALU write -> MFMA read
+    take(4)
     mfma(o0, "176:179", "192:195", f"v[{o0}]")
     cvt(196, 8, 9); cvt(197, 10, 11)
+    take(6)
     mfma(o1, "184:187", "192:195", f"v[{o1}]")
     cvt(198, 12, 13); cvt(199, 14, 15)
-    ins("s_nop 2")
+    if len(extra) < 2:
+        ins("s_nop 2")
+    take(6)
     mfma(o0, "180:183", "196:199", f"v[{o0}]")
+    take(6)
     mfma(o1, "188:191", "196:199", f"v[{o1}]")
+    take(len(extra))
 
 
 def read_k(off, dst="160"):
@@ -121,7 +152,8 @@ def pid_load(slot, tile_sgpr, label):
 def copy_tile(slot, tile_sgpr, buf, label):
     """LDS-DMA copy of tile s[tile_sgpr] (clamped) into buffer `buf` with the entries in `slot`:
     wave-uniform scalar-base form when the tile lies in one page (pages >= 64 keys) wholly below
-    the last query position, per-lane addresses otherwise. Four memory operations either way."""
+    the last query position, per-lane addresses otherwise (out of line). Four memory operations
+    either way."""
     ins(f"s_min_u32 s71, s{tile_sgpr}, %[ntm1]")
     ins("s_lshl_b32 s70, s71, 6")
     ins("s_add_u32 s70, s70, %[kb0]")          # first key of the tile
@@ -144,21 +176,21 @@ def copy_tile(slot, tile_sgpr, buf, label):
             ins(f"s_add_u32 m0, %[ldsw], {lds_off}")
             ins("s_nop 0")
             ins(f"global_load_lds_dwordx4 v{voff[i]}, s[68:69]")
-    ins(f"s_branch {label}_done")
-    ins(f"{label}_lane:")
-    for i in range(2):
-        ins(f"v_add3_u32 v244, s70, v242, {8 * i}")
-        ins("v_min_u32 v244, %[plast], v244")
-        ins("v_and_b32 v244, %[pmask], v244")
-        ins(f"v_lshlrev_b32 v245, %[sh], v{222 + 2 * slot + i}")
-        ins("v_or_b32 v244, v244, v245")         # row of this lane's key
-        for kind, pair in (("k", 234 + 2 * i), ("v", 238 + 2 * i)):
-            ins(f"v_mad_u64_u32 v[246:247], vcc, v244, %[rowb], v[{pair}:{pair + 1}]")
-            lds_off = buf * BUF + (TILE if kind == "v" else 0) + 1024 * i
-            ins(f"s_add_u32 m0, %[ldsw], {lds_off}")
-            ins("s_nop 0")
-            ins("global_load_lds_dwordx4 v[246:247], off")
     ins(f"{label}_done:")
+    lane = []
+    for i in range(2):
+        lane.append(f"v_add3_u32 v244, s70, v242, {8 * i}")
+        lane.append("v_min_u32 v244, %[plast], v244")
+        lane.append("v_and_b32 v244, %[pmask], v244")
+        lane.append(f"v_lshlrev_b32 v245, %[sh], v{222 + 2 * slot + i}")
+        lane.append("v_or_b32 v244, v244, v245")         # row of this lane's key
+        for kind, pair in (("k", 234 + 2 * i), ("v", 238 + 2 * i)):
+            lane.append(f"v_mad_u64_u32 v[246:247], vcc, v244, %[rowb], v[{pair}:{pair + 1}]")
+            lds_off = buf * BUF + (TILE if kind == "v" else 0) + 1024 * i
+            lane.append(f"s_add_u32 m0, %[ldsw], {lds_off}")
+            lane.append("s_nop 0")
+            lane.append("global_load_lds_dwordx4 v[246:247], off")
+    ool_block(f"{label}_lane", lane, f"{label}_done")
 
 
 def tile_step(si, label):
@@ -175,6 +207,10 @@ def tile_step(si, label):
 
 
 def chunk(bi, ci, label):
+    """Chunk j = s64 (32 keys): R1 S_B(j) MFMAs | exponentials of A(j); R2 O_A += V(j)^T P_A(j) |
+    row sum of A(j), rescale test of S_B(j); R3 S_A(j + 1) | exponentials of B(j); R4 O_B +=
+    V(j)^T P_B(j) | row sum of B(j), rescale test of S_A(j + 1). Each rescale test is taken at
+    the start of the next region that exponentiates the block, long after its compare."""
     bn = (bi + 1) % NBUF if ci else bi
     off = bi * BUF + 4096 * ci
     offn = bn * BUF + 4096 * (ci ^ 1)
@@ -187,48 +223,36 @@ def chunk(bi, ci, label):
         tile_step(bn, f"{label}_t")
         ins(f"{label}_nostep:")
     # R1: S_B(j) | weights of A(j)
-    qk_exp("80:95", 144, "112:127", 64)
-    ins("v_cmp_ngt_f32 vcc, 0x477fe000, v206")  # some lane's weights sum to >= 65504 (or NaN)
-    ins(f"s_cbranch_vccz {label}_a_ok")
-    ins("s_mov_b32 s78, s64")
-    ins("s_call_b64 s[66:67], pff_rescale_a")
+    ins("s_cmp_lg_u64 s[82:83], 0")
+    ins(f"s_cbranch_scc1 {label}_ra")
     ins(f"{label}_a_ok:")
-    ins("v_add_f32 v210, v210, v206")
+    ool_block(f"{label}_ra", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_rescale_a"], f"{label}_a_ok")
+    qk_exp("80:95", 144, "112:127", 64)
     read_k(offn)
-    # R2: O_A += V(j)^T . P_A(j)
+    # R2: mask of S_B(j); O_A += V(j)^T . P_A(j) | row sum of A(j), rescale test of S_B(j)
     ins("s_waitcnt lgkmcnt(4)")
-    pv("0:15", "16:31", 64)
-    # mask of S_B(j)
-    ins("s_mov_b32 s78, s64")
-    ins("s_cmp_lt_u32 s64, %[jlob]")
+    ins("s_sub_u32 s79, s64, %[jlob]")
+    ins("s_cmp_ge_u32 s79, %[jnb]")
     ins(f"s_cbranch_scc1 {label}_mb")
-    ins("s_cmp_gt_u32 s64, %[jhib]")
-    ins(f"s_cbranch_scc0 {label}_mb_ok")
-    ins(f"{label}_mb:")
-    ins("s_call_b64 s[66:67], pff_mask_b")
     ins(f"{label}_mb_ok:")
+    ool_block(f"{label}_mb", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_mask_b"], f"{label}_mb_ok")
+    pv("0:15", "16:31", 64, sum_ops(64, 210)[:5] + max_ops(80, 84) + sum_ops(64, 210)[5:])
     # R3: S_A(j + 1) | weights of B(j)
+    ins("s_cmp_lg_u64 s[84:85], 0")
+    ins(f"s_cbranch_scc1 {label}_rb")
+    ins(f"{label}_b_ok:")
+    ool_block(f"{label}_rb", ["s_mov_b32 s78, s64", f"s_mov_b32 s76, {off}", f"s_mov_b32 s77, {offn}",
+                              "s_call_b64 s[66:67], pff_rescale_b"], f"{label}_b_ok")
     ins("s_waitcnt lgkmcnt(0)")
     qk_exp("64:79", 128, "96:111", 80)
-    ins("v_cmp_ngt_f32 vcc, 0x477fe000, v206")
-    ins(f"s_cbranch_vccz {label}_b_ok")
-    ins(f"s_mov_b32 s76, {off}")
-    ins(f"s_mov_b32 s77, {offn}")
-    ins("s_call_b64 s[66:67], pff_rescale_b")
-    ins(f"{label}_b_ok:")
-    ins("v_add_f32 v211, v211, v206")
-    # R4: O_B += V(j)^T . P_B(j)
-    pv("32:47", "48:63", 80)
-    read_v(offn)
-    # mask of S_A(j + 1)
-    ins("s_add_u32 s78, s64, 1")
-    ins("s_cmp_lt_u32 s78, %[jloa]")
+    # R4: mask of S_A(j + 1); O_B += V(j)^T . P_B(j) | row sum of B(j), rescale test of S_A(j + 1)
+    ins("s_sub_u32 s79, s64, %[jloa1]")           # (j + 1) - jlo_A
+    ins("s_cmp_ge_u32 s79, %[jna]")
     ins(f"s_cbranch_scc1 {label}_ma")
-    ins("s_cmp_gt_u32 s78, %[jhia]")
-    ins(f"s_cbranch_scc0 {label}_ma_ok")
-    ins(f"{label}_ma:")
-    ins("s_call_b64 s[66:67], pff_mask_a")
     ins(f"{label}_ma_ok:")
+    ool_block(f"{label}_ma", ["s_add_u32 s78, s64, 1", "s_call_b64 s[66:67], pff_mask_a"], f"{label}_ma_ok")
+    pv("32:47", "48:63", 80, sum_ops(80, 211)[:5] + max_ops(64, 82) + sum_ops(80, 211)[5:])
+    read_v(offn)
     ins("s_add_u32 s64, s64, 1")
 
 
@@ -245,10 +269,10 @@ def mask_body(e, c_reg, span_reg):
         ins(f"v_cndmask_b32 v{e + i}, v{e + i}, v245, vcc")
 
 
-def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jhi, label):
+def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jn, label):
     """Raw scores of the chunk (K in v160-v175) -> v[e..], masked if the chunk needs it, the row
-    maximum across lanes n and n + 32, m moved to it, O, l and the bias rescaled, the weights
-    redone; the chunk's row-sum share lands in v206."""
+    maximum across lanes n and n + 32, m moved to it, O, l and the bias rescaled, and the exponent
+    inputs redone with the new bias (the caller exponentiates them)."""
     E = list(range(e, e + 16))
     qs = [f"{q0 + 4 * t}:{q0 + 4 * t + 3}" for t in range(4)]
     mfma(sd, K_OPS[0], qs[0], "0")
@@ -257,11 +281,9 @@ def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jhi, 
     ins("s_nop 7")
     ins("s_nop 7")
     ins("s_nop 7")  # MFMA results -> VALU
-    ins(f"s_cmp_lt_u32 s78, {jlo}")
-    ins(f"s_cbranch_scc1 {label}_m")
-    ins(f"s_cmp_gt_u32 s78, {jhi}")
-    ins(f"s_cbranch_scc0 {label}_nm")
-    ins(f"{label}_m:")
+    ins(f"s_sub_u32 s79, s78, {jlo}")
+    ins(f"s_cmp_lt_u32 s79, {jn}")
+    ins(f"s_cbranch_scc1 {label}_nm")
     mask_body(e, c_reg, span_reg)
     ins(f"{label}_nm:")
     ins(f"v_max3_f32 v200, v{E[0]}, v{E[1]}, v{E[2]}")
@@ -282,13 +304,6 @@ def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jhi, 
         ins(f"v_mov_b32 v{bias_base + i}, v204")
     for i in range(16):
         ins(f"v_add_f32 v{E[i]}, v{E[i]}, v204")
-    for i in range(16):
-        ins(f"v_exp_f32 v{E[i]}, v{E[i]}")
-    for k in range(8):
-        ins(f"v_add_f32 v{200 + k}, v{E[2 * k]}, v{E[2 * k + 1]}")
-    for d, a, b in ((200, 200, 201), (202, 202, 203), (204, 204, 205), (206, 206, 207),
-                    (200, 200, 202), (204, 204, 206), (206, 200, 204)):
-        ins(f"v_add_f32 v{d}, v{a}, v{b}")
 
 
 def generate():
@@ -320,13 +335,13 @@ def generate():
     ins("s_nop 7")
     ins("s_mov_b32 s64, 0")
     ins("s_mov_b32 s78, 0")
-    ins("s_cmp_lt_u32 s78, %[jloa]")
-    ins("s_cbranch_scc1 pro_ma")
-    ins("s_cmp_gt_u32 s78, %[jhia]")
-    ins("s_cbranch_scc0 pro_ma_ok")
-    ins("pro_ma:")
+    ins("s_sub_u32 s79, 0, %[jloa]")
+    ins("s_cmp_lt_u32 s79, %[jna]")
+    ins("s_cbranch_scc1 pro_ma_ok")
     ins("s_call_b64 s[66:67], pff_mask_a")
     ins("pro_ma_ok:")
+    for x in max_ops(64, 82):
+        ins(x)
     # ---- main loop: four tiles (eight chunks) per pass; buffers and entry slots fixed ----
     ins("pff_loop:")
     for k in range(NBUF):
@@ -335,15 +350,22 @@ def generate():
         ins("s_cmp_ge_u32 s64, %[nc]")
         ins("s_cbranch_scc1 pff_end")
     ins("s_branch pff_loop")
+    out.extend(ool)
     # ---- rare paths (called with s_call_b64 s[66:67], return with s_setpc_b64) ----
-    ins("pff_mask_a:")
+    ins("pff_mask_a:")  # called soon after the MFMAs that wrote S_A
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_nop 7")
     mask_body(64, 218, 219)
     ins("s_setpc_b64 s[66:67]")
     ins("pff_mask_b:")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_nop 7")
     mask_body(80, 220, 221)
     ins("s_setpc_b64 s[66:67]")
     ins("pff_rescale_a:")  # K(j) is in v160-v175
-    rescale_body("64:79", 64, 128, 0, 96, 208, 210, 218, 219, "%[jloa]", "%[jhia]", "ra")
+    rescale_body("64:79", 64, 128, 0, 96, 208, 210, 218, 219, "%[jloa]", "%[jna]", "ra")
     ins("s_setpc_b64 s[66:67]")
     ins("pff_rescale_b:")  # K(j + 1) is in v160-v175: read K(j) (LDS offset s76), then K(j + 1) (s77)
     for t in range(4):
@@ -352,7 +374,7 @@ def generate():
     for t in range(4):
         ins(f"ds_read_b128 v[{160 + 4 * t}:{163 + 4 * t}], v{244 + t}")
     ins("s_waitcnt lgkmcnt(0)")
-    rescale_body("80:95", 80, 144, 32, 112, 209, 211, 220, 221, "%[jlob]", "%[jhib]", "rb")
+    rescale_body("80:95", 80, 144, 32, 112, 209, 211, 220, 221, "%[jlob]", "%[jnb]", "rb")
     for t in range(4):
         ins(f"v_add_u32 v{244 + t}, s77, v{212 + t}")
     for t in range(4):

@@ -19,6 +19,11 @@
 //   [32, 32 + 64*16) un-normalised output, [head][dim]
 #define MOEARC_PARTIAL_FLOATS (32 + 64 * 16)
 
+// Work-groups of the split merge per (sequence, query head): each combines 64 / MOEARC_MERGE_PARTS
+// output channels.
+#define MOEARC_MERGE_PARTS 4
+#define MOEARC_MERGE_THREADS 256
+
 // Kernel arguments of the split-K decode. Passed by value; the per-sequence arrays let one launch
 // serve a ragged batch. Work item `it` (one (sequence, split) pair) covers the work-groups
 // it * n_kv_heads + kvh for every KV head kvh, so consecutive work-groups -- which the dispatcher

@@ -353,7 +353,7 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
                               64u * kb * wpk, a, "attn_decode.split", n_heads, head_dim);
         if (rc) return rc;
         if (any_split && !fused) {
-            const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads), c->merge_threads, a,
+            const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads * MOEARC_MERGE_PARTS), c->merge_threads, a,
                                   "attn_decode.merge", n_heads, head_dim);
             if (rm) return rm;
         }
@@ -418,7 +418,7 @@ moearc_ctx *moearc_ctx_create(void) {
     }
     int merge_threads = 0;
     if (hipFuncGetAttribute(&merge_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_dec_merge) !=
-            hipSuccess || merge_threads < 64 || merge_threads > 1024) {
+            hipSuccess || merge_threads != MOEARC_MERGE_THREADS) {
         std::fprintf(stderr, "moearc: cannot read the merge kernel's work-group size\n");
         hipModuleUnload(c->module);
         hipStreamDestroy(c->stream);

@@ -257,6 +257,19 @@ def test_forced_splits_and_variants(monkeypatch):
                 _report(f"variant={variant} split={split} rep={rep}", got, want, TOL_NS)
 
 
+def test_merge_over_many_rounds(monkeypatch):
+    # 313 splits: each merge lane takes more than one round of records
+    c = fx.north_star_case(0xAC, 20000, pt=64, spike_frac=0.01)
+    want = oracle.attn_decode(c.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, 0, c.n_kv, c.pt,
+                              float(c.scale), kv_type=1, sinks=c.sinks)
+    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "8x2")
+    monkeypatch.setenv("MOEARC_DECODE_SPLIT", "64")
+    with Context() as cx:
+        b = _upload_case(cx, c)
+        got = _decode(cx, c, b, 0)
+        _report("variant=8x2 split=64 n_kv=20000", got, want, TOL_NS)
+
+
 def test_batched_ragged_decode(ctx):
     _batched_ragged(ctx)
 
