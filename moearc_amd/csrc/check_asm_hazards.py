@@ -1,0 +1,208 @@
+"""Checks the compiled prefill kernels for the gfx950 hazards that hand-written asm must respect.
+
+The key loop of the default prefill kernels is one inline-asm statement (prefill_loop.inc), so the
+compiler inserts no wait states or counter waits inside it. This script compiles moearc_kernels.hip
+to assembly with the build's flags and walks the control-flow graph of each kernel (branches and
+calls followed, `s_setpc_b64` returns ending a path), counting wait states (one per instruction,
+N + 1 for `s_nop N`):
+
+  1. an MFMA result (its destination registers) is not read or written by any other instruction
+     within MFMA_WAIT wait states of the MFMA; a later MFMA may accumulate into exactly the same
+     registers (same-size back-to-back accumulation is forwarded) but not read them as A or B;
+  2. a VALU result is not read by an MFMA within VALU_MFMA_WAIT wait states;
+  3. no register that an asm-issued `ds_read*` or block-table `global_load_dword` writes is touched
+     between the load and the `s_waitcnt` that retires it (loads counted in program order).
+
+Usage: python check_asm_hazards.py [kernel-name-prefix ...]   (default: moearc_attn_prefill_g)
+Exit status 1 when a hazard is found.
+"""
+import os
+import re
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+MFMA_WAIT = 20      # 16-pass XDL result -> VALU: 18 on gfx940, 19 on gfx950, one spare
+VALU_MFMA_WAIT = 2  # VALU result -> MFMA source
+FLAGS = ["--offload-arch=gfx950", "--cuda-device-only", "-S", "-O3", "-std=c++17",
+         "-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def compile_asm():
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    hipcc = os.path.join(rocm, "bin", "hipcc")
+    out = os.path.join(tempfile.mkdtemp(prefix="moearc_asm_"), "kernels.s")
+    subprocess.run([hipcc, *FLAGS, "-I", HERE, os.path.join(HERE, "moearc_kernels.hip"), "-o", out],
+                   check=True, stderr=subprocess.DEVNULL)
+    return open(out).read().split("\n")
+
+
+def kernel_body(lines, name):
+    start = next(i for i, l in enumerate(lines) if l.split(";")[0].rstrip() == name + ":")
+    ins, labels = [], {}
+    for l in lines[start + 1:]:
+        t = l.split(";")[0].strip()
+        if t.startswith(".end_amdhsa_kernel") or t.startswith(".Lfunc_end"):
+            break
+        if not t:
+            continue
+        if t.endswith(":"):
+            labels[t[:-1]] = len(ins)
+        elif not t.startswith("."):
+            ins.append(t)
+    return ins, labels
+
+
+def regs(tok):
+    tok = tok.split()[0] if tok else ""
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"v(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def split_ops(t):
+    parts = t.split(None, 1)
+    return parts[0], ([a.strip() for a in parts[1].split(",")] if len(parts) > 1 else [])
+
+
+def writes_reads(t):
+    """VGPRs an instruction writes and reads."""
+    op, args = split_ops(t)
+    rs = [regs(a) for a in args]
+    allr = set().union(*rs) if rs else set()
+    if op.startswith(("v_cmp", "v_readfirstlane", "v_readlane")):
+        return set(), allr
+    if op.startswith(("ds_write", "global_store", "global_load_lds", "scratch_store",
+                      "buffer_store", "global_atomic")):
+        return set(), allr
+    if op.startswith(("v_", "ds_read", "ds_bpermute", "global_load", "buffer_load", "scratch_load")):
+        return (rs[0] if rs else set()), (set().union(*rs[1:]) if len(rs) > 1 else set())
+    return set(), set()
+
+
+def wait_states(t):
+    m = re.match(r"s_nop (\d+)", t)
+    return int(m.group(1)) + 1 if m else 1
+
+
+def successors(ins, labels, j):
+    op, args = split_ops(ins[j])
+    if op == "s_branch":
+        return [labels[args[0]]]
+    if op.startswith("s_cbranch"):
+        return [labels[args[0]], j + 1]
+    if op == "s_call_b64":
+        return [labels[args[1]], j + 1]
+    if op in ("s_setpc_b64", "s_endpgm"):
+        return []
+    return [j + 1]
+
+
+def walk(ins, labels, i, need, check):
+    """Instructions reachable from i with fewer than `need` wait states in between, for which
+    check() reports a problem."""
+    found, best = [], {}
+    stack = [(k, 0) for k in successors(ins, labels, i)]
+    while stack:
+        j, d = stack.pop()
+        if j >= len(ins) or d >= need or best.get(j, 1 << 30) <= d:
+            continue
+        best[j] = d
+        msg = check(ins[j])
+        if msg:
+            found.append(f"[{ins[i]}] -> [{ins[j]}] after {d} wait states: {msg}")
+            continue
+        stack.extend((k, d + wait_states(ins[j])) for k in successors(ins, labels, j))
+    return found
+
+
+def mfma_hazards(ins, labels):
+    out = []
+    for i, t in enumerate(ins):
+        op, args = split_ops(t)
+        if op.startswith("v_mfma"):
+            dst = regs(args[0])
+
+            def chk(u, dst=dst):
+                uop, ua = split_ops(u)
+                if uop.startswith("v_mfma"):
+                    c = regs(ua[3]) if len(ua) > 3 else set()
+                    if dst & (regs(ua[1]) | regs(ua[2])):
+                        return "MFMA reads the result as A or B"
+                    if dst & c and c != dst:
+                        return "MFMA C partly overlaps the result"
+                    return None
+                w, r = writes_reads(u)
+                return "result used" if dst & (w | r) else None
+            out += walk(ins, labels, i, MFMA_WAIT, chk)
+        elif op.startswith("v_"):
+            w, _ = writes_reads(t)
+            if not w:
+                continue
+
+            def chk2(u, w=w):
+                uop, ua = split_ops(u)
+                if uop.startswith("v_mfma") and w & set().union(*[regs(a) for a in ua[1:4]]):
+                    return "MFMA reads a VALU result"
+                return None
+            out += walk(ins, labels, i, VALU_MFMA_WAIT, chk2)
+    return out
+
+
+def load_hazards(ins):
+    """Straight-line check of asm-issued load destinations against their retiring wait."""
+    out = []
+    for i, t in enumerate(ins):
+        if t.startswith("ds_read"):
+            kind = "lgkm"
+        elif re.match(r"global_load_dword v\d+, v\[\d+:\d+\], off$", t):
+            kind = "vm"
+        else:
+            continue
+        dst = regs(t.split(",")[0].split(None, 1)[1])
+        younger = 0
+        for j in range(i + 1, min(len(ins), i + 3000)):
+            u = ins[j]
+            if u.startswith(("s_branch", "s_endpgm", "s_setpc_b64")):
+                break
+            m = re.match(r"s_waitcnt (.*)", u)
+            if m:
+                c = re.search(kind + r"cnt\((\d+)\)", m.group(1))
+                if c and int(c.group(1)) <= younger:
+                    break
+                continue
+            if (kind == "lgkm" and u.startswith(("ds_", "s_load"))) or \
+               (kind == "vm" and u.startswith(("global_", "buffer_"))):
+                younger += 1
+            w, r = writes_reads(u)
+            if dst & (w | r):
+                out.append(f"[{t}] -> [{u}]: destination touched before its wait")
+                break
+    return out
+
+
+def main(prefixes):
+    lines = compile_asm()
+    heads = [l.split(";")[0].rstrip() for l in lines]
+    names = sorted({h[:-1] for h in heads if re.match(r"^[A-Za-z_]\w*:$", h)
+                    and any(h.startswith(p) for p in prefixes)})
+    bad = 0
+    for name in names:
+        ins, labels = kernel_body(lines, name)
+        probs = mfma_hazards(ins, labels) + load_hazards(ins)
+        print(f"{name}: {len(ins)} instructions, {len(probs)} hazards")
+        for p in probs[:10]:
+            print("   ", p)
+        bad += len(probs)
+    if not names:
+        print("no kernel matches", prefixes)
+        return 1
+    return 1 if bad else 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:] or ["moearc_attn_prefill_g"]))

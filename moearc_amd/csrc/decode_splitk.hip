@@ -269,15 +269,39 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
     st.l = 0.f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) st.O[mb] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    if (kvh_ok) {
-        for (uint32_t t = sub; t < ntiles; t += WPK) {
-            const uint32_t j0 = tb + 32u * t;
-            TileRegs r;
-            load_tile(r, a, pt_lds, page0, j0, te, kvh, lane);
-            // All eight loads issue before any compute: left alone, the scheduler sinks the V loads
-            // below the QK^T MFMAs and every tile pays two memory latencies instead of one.
-            __builtin_amdgcn_sched_barrier(0);
-            process_tile(st, r, qhi, qlo, sel, c, j0, te, g);
+    if (kvh_ok && sub < ntiles) {
+        if constexpr (WAVES <= 8) {
+            // Two tiles in flight per wave: the loads of the next tile issue before this one is
+            // computed, over two register sets (ra, rb). The wave walks its tiles in pairs with a
+            // single loop exit, so every wait leaves exactly the younger set's eight loads
+            // outstanding; a pair's second tile past the span (odd tile count) computes nothing
+            // (all its keys are at or beyond te, so every weight is zero) and its loads repeat a
+            // tile of the span (cache hits).
+            const uint32_t nt = (ntiles - sub + WPK - 1u) / WPK;  // this wave's tiles, >= 1
+            const uint32_t last = sub + (nt - 1u) * WPK;
+            auto tile_of = [&](uint32_t i) { return sub + i * WPK; };
+            TileRegs ra, rb;
+            load_tile(ra, a, pt_lds, page0, tb + 32u * sub, te, kvh, lane);
+            for (uint32_t i = 0; i < nt; i += 2) {
+                load_tile(rb, a, pt_lds, page0, tb + 32u * min(tile_of(i + 1u), last), te, kvh, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                process_tile(st, ra, qhi, qlo, sel, c, tb + 32u * tile_of(i), te, g);
+                load_tile(ra, a, pt_lds, page0, tb + 32u * min(tile_of(i + 2u), last), te, kvh, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                process_tile(st, rb, qhi, qlo, sel, c, min(tb + 32u * tile_of(i + 1u), te), te, g);
+            }
+        } else {
+            // 16-wave work-groups (128 VGPRs per wave): one tile in flight per wave, the
+            // residency of four waves per SIMD keeps HBM busy.
+            for (uint32_t t = sub; t < ntiles; t += WPK) {
+                const uint32_t j0 = tb + 32u * t;
+                TileRegs r;
+                load_tile(r, a, pt_lds, page0, j0, te, kvh, lane);
+                // All eight loads issue before any compute: left alone, the scheduler sinks the V
+                // loads below the QK^T MFMAs and every tile pays two memory latencies.
+                __builtin_amdgcn_sched_barrier(0);
+                process_tile(st, r, qhi, qlo, sel, c, j0, te, g);
+            }
         }
     }
 
@@ -470,3 +494,5 @@ DECODE_KERNEL(1, 16)
 DECODE_KERNEL(2, 8)
 DECODE_KERNEL(4, 4)
 DECODE_KERNEL(8, 2)
+DECODE_KERNEL(1, 8)
+DECODE_KERNEL(2, 4)

@@ -95,9 +95,9 @@ def pv(o0, o1, e, extra):
     """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7], with
     the VALU instructions `extra` (independent of P and of the V^T operands) spread between the
     MFMAs: 4 before the first (they cover the VALU-write -> MFMA-read wait), then 6, 6, 6, rest.
-    The chunk places its rescale test (a max3 tree and a compare) from the fifth on: after the
-    first MFMA, far enough from the MFMAs that wrote the scores, and two MFMAs before the branch
-    that reads the compare."""
+    The chunk places its rescale test (a max3 tree and a compare) from the seventh on: after the
+    first MFMA, at least 20 wait states after the MFMAs that wrote the scores, and two MFMAs before
+    the branch that reads the compare."""
     cvt = lambda d, a, b: ins(f"v_cvt_pk_f16_f32 v{d}, v{e + a}, v{e + b}")
     extra = list(extra)
     take = lambda n: [ins(extra.pop(0)) for _ in range(min(n, len(extra)))]
@@ -236,7 +236,7 @@ def chunk(bi, ci, label):
     ins(f"s_cbranch_scc1 {label}_mb")
     ins(f"{label}_mb_ok:")
     ool_block(f"{label}_mb", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_mask_b"], f"{label}_mb_ok")
-    pv("0:15", "16:31", 64, sum_ops(64, 210)[:5] + max_ops(80, 84) + sum_ops(64, 210)[5:])
+    pv("0:15", "16:31", 64, sum_ops(64, 210)[:6] + max_ops(80, 84) + sum_ops(64, 210)[6:])
     # R3: S_A(j + 1) | weights of B(j)
     ins("s_cmp_lg_u64 s[84:85], 0")
     ins(f"s_cbranch_scc1 {label}_rb")
@@ -251,7 +251,7 @@ def chunk(bi, ci, label):
     ins(f"s_cbranch_scc1 {label}_ma")
     ins(f"{label}_ma_ok:")
     ool_block(f"{label}_ma", ["s_add_u32 s78, s64, 1", "s_call_b64 s[66:67], pff_mask_a"], f"{label}_ma_ok")
-    pv("32:47", "48:63", 80, sum_ops(80, 211)[:5] + max_ops(64, 82) + sum_ops(80, 211)[5:])
+    pv("32:47", "48:63", 80, sum_ops(80, 211)[:6] + max_ops(64, 82) + sum_ops(80, 211)[6:])
     read_v(offn)
     ins("s_add_u32 s64, s64, 1")
 

@@ -69,7 +69,7 @@ struct moearc_ctx {
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
     hipFunction_t f_rope = nullptr, f_rope_append_chunk = nullptr;
     hipFunction_t f_dec_general = nullptr;
-    hipFunction_t f_dec_fast[5] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2
+    hipFunction_t f_dec_fast[7] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2, 1x8, 2x4
     hipFunction_t f_dec_merge = nullptr;
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
@@ -194,10 +194,13 @@ struct SeqSpan {
     uint32_t begin, end;
 };
 
+// The split-K kernel masks keys with -inf scores before multiplying by scale*log2(e) and takes
+// its running maximum on raw scores, so it needs a positive, finite scale; any other scale runs on
+// the general kernel.
 bool fast_decode_ok(unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
-                    unsigned long page_tokens, unsigned int kv_type) {
+                    unsigned long page_tokens, unsigned int kv_type, float scale) {
     return kv_type == 1u && head_dim == 64 && n_heads / n_kv_heads <= 16 && is_pow2(page_tokens) &&
-           page_tokens <= (1ul << 30);
+           page_tokens <= (1ul << 30) && scale > 0.f && scale <= 3.0e38f;
 }
 
 // Block-table entries the split-K kernel stages in LDS per work-group (PT_CAP in the kernel).
@@ -213,10 +216,11 @@ struct DecodeVariant {
     unsigned kb, wpk, target_wgs;
     bool fused;
 };
-constexpr int kNumDecodeVariants = 6;
+constexpr int kNumDecodeVariants = 8;
 constexpr DecodeVariant kDecodeVariants[kNumDecodeVariants] = {
     {"1x4", 0, 1, 4, 384, false},  {"1x16", 1, 1, 16, 384, false}, {"2x8", 2, 2, 8, 384, false},
     {"4x4", 3, 4, 4, 384, false},  {"8x2", 4, 8, 2, 384, false},   {"1x4f", 0, 1, 4, 256, true},
+    {"1x8", 5, 1, 8, 384, false},  {"2x4", 6, 2, 4, 384, false},
 };
 
 // Variant and keys per split. A work-group reads kb*128 bytes of each key row (kb KV heads; four
@@ -276,7 +280,7 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
                        const float *sinks, unsigned long n_heads, unsigned long n_kv_heads,
                        unsigned long head_dim, unsigned long page_tokens, float scale,
                        unsigned int kv_type, size_t nseq, size_t per) {
-    const bool fast_shape = fast_decode_ok(n_heads, n_kv_heads, head_dim, page_tokens, kv_type);
+    const bool fast_shape = fast_decode_ok(n_heads, n_kv_heads, head_dim, page_tokens, kv_type, scale);
     for (size_t s0 = 0; s0 < nseq; s0 += per) {
         const size_t cnt = std::min(per, nseq - s0);
         const float *qb = q + s0 * n_heads * head_dim;
@@ -405,6 +409,8 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_dec_fast[2], "moearc_attn_decode_f16d64_k2w8"},
         {&c->f_dec_fast[3], "moearc_attn_decode_f16d64_k4w4"},
         {&c->f_dec_fast[4], "moearc_attn_decode_f16d64_k8w2"},
+        {&c->f_dec_fast[5], "moearc_attn_decode_f16d64_k1w8"},
+        {&c->f_dec_fast[6], "moearc_attn_decode_f16d64_k2w4"},
         {&c->f_dec_merge, "moearc_attn_decode_merge"},
     };
     for (auto &f : fns) {
