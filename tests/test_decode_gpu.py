@@ -270,6 +270,19 @@ def test_merge_over_many_rounds(monkeypatch):
         _report("variant=8x2 split=64 n_kv=20000", got, want, TOL_NS)
 
 
+@pytest.mark.parametrize("scale", [-0.125, 0.0])
+def test_non_positive_scale(ctx, scale):
+    # the split-K kernel needs a positive scale; these run on the general kernel with the same result
+    c = fx.north_star_case(0xAD, 3000, pt=64)
+    want = oracle.attn_decode(c.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, 0, c.n_kv, c.pt,
+                              scale, kv_type=1, sinks=c.sinks)
+    b = _upload_case(ctx, c)
+    ctx.attn_decode_ext(b["out"], b["q"], b["k"], b["v"], b["bt"], b["sinks"], c.H, c.G, c.D, 0,
+                        c.n_kv, c.pt, scale, KvType.F16)
+    got = ctx.download(b["out"], np.float32, c.H * c.D)
+    _report(f"scale={scale}", got, want, TOL_NS)
+
+
 def test_batched_ragged_decode(ctx):
     _batched_ragged(ctx)
 
