@@ -333,6 +333,66 @@ def _batched_ragged(ctx):
                                 lens, ds, H, G, D, pt, 0.125, KvType.F16)
 
 
+def _shared_pool_case(seed, lens, pool_pages, spike=0.0, pt=256):
+    """Full-size batched decode input: one pool of random f16 pages (K rows optionally spiked by
+    8x), each sequence reading its own random permutation of the pool, so B long sequences cost one
+    pool of host memory while the kernel still walks B distinct page tables."""
+    H, G, D = 64, 8, 64
+    row = G * D
+    rng = np.random.default_rng(seed)
+    n_tok = pool_pages * pt
+    kp = np.empty(n_tok * row, np.uint16)
+    vp = np.empty_like(kp)
+    step = 1 << 16
+    for s in range(0, n_tok, step):
+        n = min(step, n_tok - s)
+        k = rng.standard_normal((n, row), dtype=np.float32)
+        if spike:
+            k[rng.random(n) < spike] *= np.float32(8.0)
+        kp[s * row:(s + n) * row] = k.astype(np.float16).view(np.uint16).ravel()
+        vp[s * row:(s + n) * row] = rng.standard_normal(n * row, dtype=np.float32).astype(np.float16).view(np.uint16)
+    pages = [-(-int(n) // pt) for n in lens]
+    assert max(pages) <= pool_pages
+    bts = np.stack([rng.permutation(pool_pages).astype(np.uint32) for _ in lens])
+    q = rng.standard_normal((len(lens), H, D), dtype=np.float32)
+    sinks = rng.standard_normal(H, dtype=np.float32)
+    return H, G, D, pt, kp, vp, bts, q, sinks
+
+
+def _check_batched_full_size(ctx, label, case, lens, windows, out_types):
+    H, G, D, pt, kp, vp, bts, q, sinks = case
+    dk, dv, dq, dbt, ds = (ctx.upload(kp), ctx.upload(vp), ctx.upload(q), ctx.upload(bts),
+                           ctx.upload(sinks))
+    stride = bts.shape[1]
+    for window in windows:
+        kb = np.maximum(lens.astype(np.int64) - window, 0).astype(np.uint32) if window else np.zeros_like(lens)
+        want = oracle.attn_decode_batched(q, kp, vp, bts, kb, lens, H, G, D, pt, 0.125, sinks=sinks,
+                                          n_threads=16)
+        for out_type in out_types:
+            nb = 2 if out_type == OUT_F16 else 4
+            dout = ctx.alloc(len(lens) * H * D * nb)
+            ctx.attn_decode_batched(dout, dq, dk, dv, dbt, stride, kb, lens, ds, H, G, D, pt, 0.125,
+                                    KvType.F16, out_type=out_type)
+            got = ctx.download(dout, np.float16 if out_type == OUT_F16 else np.float32, want.shape)
+            _report(f"{label} window={window} out={'f16' if nb == 2 else 'f32'}", got, want, TOL_NS)
+
+
+def test_config3_full_size(ctx):
+    # BASELINE config 3: B=32 ragged lengths ~U[1024, 32768], 256-token pages through random page
+    # tables, SWA-128 and full
+    lens = np.random.default_rng(33).integers(1024, 32769, size=32).astype(np.uint32)
+    case = _shared_pool_case(0xC3, lens, pool_pages=128)
+    _check_batched_full_size(ctx, "config 3", case, lens, (0, 128), (OUT_F32, OUT_F16))
+
+
+def test_config5_full_size(ctx):
+    # BASELINE config 5: B=8 x 131072 keys, full attention, 256-token pages, 1% of K rows x8 (the
+    # running maximum moves late and often); 2 GiB of K/V read per call
+    lens = np.full(8, 131072, np.uint32)
+    case = _shared_pool_case(0xC5, lens, pool_pages=512, spike=0.01)
+    _check_batched_full_size(ctx, "config 5", case, lens, (0,), (OUT_F32,))
+
+
 def test_large_q_magnitudes(ctx):
     # q beyond f16's range and far below it: the power-of-two normalisation keeps the hi/lo split exact
     c = fx.north_star_case(0x51, 700, pt=64)
