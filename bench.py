@@ -313,6 +313,103 @@ def cpu_baseline(kp, vp, bt, q, sinks):
             "threads": threads}
 
 
+def bench_configs(steps, warmup):
+    """BASELINE configs 1, 3 and 5 (decode), reported one JSON line each; config 2 is the main line.
+    K/V are random finite f16 bit patterns (|x| < 2) -- timing does not depend on their values --
+    in 256-token pages. Each config touches more than the 256 MB Infinity Cache per replay cycle:
+    config 1 rotates 40 contiguous copies, config 3 rotates 40 random block tables over a pool of
+    every sequence's pages, config 5 reads 2 GiB per call. Algorithmic bytes: K/V read
+    (2 KiB per key), q (16 KiB) and f16 out (8 KiB) per sequence, sinks, block-table entries."""
+    from moearc_amd import Context, KvType, OUT_F16
+    hip = Hip()
+    rng = np.random.default_rng(0xD5)
+    row = G * D
+
+    def pages_of(n_pages):
+        bits = rng.integers(0, 1 << 16, size=n_pages * PT * row, dtype=np.uint16)
+        return bits & np.uint16(0xBFFF)  # exponent below 31: finite, |x| < 2
+
+    def timed(ctx, step):
+        for i in range(warmup):
+            step(i)
+        ctx.sync()
+        graph, exe = hip.capture(ctx.stream, lambda: [step(i) for i in range(steps)])
+        hip.launch(exe, ctx.stream)  # one untimed replay
+        ctx.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, ctx.stream)
+        hip.launch(exe, ctx.stream)
+        hip.record(e1, ctx.stream)
+        ctx.sync()
+        us = hip.elapsed_ms(e0, e1) * 1e3 / steps
+        hip.destroy(graph, exe)
+        return us
+
+    def emit(name, us, nbytes, b):
+        gbs = nbytes / us / 1e3
+        print(json.dumps({"config": name, "us_per_layer": round(us, 2), "algorithmic_bytes": nbytes,
+                          "gbs": round(gbs, 1), "pct_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                          "tokens_per_s": round(b * 1e6 / us, 0)}), flush=True)
+
+    seq_bytes = H * D * 4 + H * D * 2  # q f32 in, f16 out
+    with Context() as ctx:
+        q32 = rng.standard_normal((32, H, D), dtype=np.float32)
+        dq, ds = ctx.upload(q32), ctx.upload(rng.standard_normal(H, dtype=np.float32))
+
+        # C1: B=1, 4096 keys, contiguous pages
+        n1 = 4096
+        copies = 40
+        dk1 = [ctx.upload(pages_of(n1 // PT)) for _ in range(copies)]
+        dv1 = [ctx.upload(pages_of(n1 // PT)) for _ in range(copies)]
+        dbt1 = ctx.upload(np.arange(n1 // PT, dtype=np.uint32))
+        out1 = ctx.alloc(H * D * 2)
+        kb1, nk1 = np.zeros(1, np.uint32), np.full(1, n1, np.uint32)
+        us = timed(ctx, lambda i: ctx.attn_decode_batched(out1, dq, dk1[i % copies], dv1[i % copies], dbt1,
+                                                          n1 // PT, kb1, nk1, ds, H, G, D, PT, 0.125,
+                                                          KvType.F16, out_type=OUT_F16))
+        emit("C1 decode B=1, 4096 keys, full, contiguous pages", us,
+             n1 * 2 * row * 2 + seq_bytes + H * 4 + 4 * (n1 // PT), 1)
+        del dk1, dv1
+
+        # C3: B=32, lengths ~U[1024, 32768], random page tables, SWA-128 and full
+        lens = np.random.default_rng(33).integers(1024, 32769, size=32).astype(np.uint32)
+        npg = [-(-int(n) // PT) for n in lens]
+        pool = sum(npg)
+        dk3, dv3 = ctx.upload(pages_of(pool)), ctx.upload(pages_of(pool))
+        stride = max(npg)
+        bts = []
+        for _ in range(copies):
+            perm = rng.permutation(pool).astype(np.uint32)
+            t = np.zeros((32, stride), np.uint32)
+            off = 0
+            for s, p in enumerate(npg):
+                t[s, :p] = perm[off:off + p]
+                off += p
+            bts.append(ctx.upload(t))
+        out3 = ctx.alloc(32 * H * D * 2)
+        for window in (0, 128):
+            kb = np.maximum(lens.astype(np.int64) - window, 0).astype(np.uint32) if window else np.zeros_like(lens)
+            span = (lens.astype(np.int64) - kb.astype(np.int64))
+            first, last = kb.astype(np.int64) // PT, (lens.astype(np.int64) - 1) // PT
+            us = timed(ctx, lambda i: ctx.attn_decode_batched(out3, dq, dk3, dv3, bts[i % copies], stride, kb,
+                                                              lens, ds, H, G, D, PT, 0.125, KvType.F16,
+                                                              out_type=OUT_F16))
+            emit(f"C3 decode B=32 ragged U[1024,32768], {'SWA-128' if window else 'full'}", us,
+                 int(span.sum()) * 2 * row * 2 + 32 * seq_bytes + H * 4 + 4 * int((last - first + 1).sum()), 32)
+        del dk3, dv3, bts
+
+        # C5: B=8 x 131072 keys, full
+        n5, b5 = 131072, 8
+        p5 = n5 // PT
+        dk5, dv5 = ctx.upload(pages_of(b5 * p5)), ctx.upload(pages_of(b5 * p5))
+        dbt5 = ctx.upload(rng.permutation(b5 * p5).astype(np.uint32).reshape(b5, p5))
+        out5 = ctx.alloc(b5 * H * D * 2)
+        kb5, nk5 = np.zeros(b5, np.uint32), np.full(b5, n5, np.uint32)
+        us = timed(ctx, lambda i: ctx.attn_decode_batched(out5, dq, dk5, dv5, dbt5, p5, kb5, nk5, ds, H, G, D,
+                                                          PT, 0.125, KvType.F16, out_type=OUT_F16))
+        emit("C5 decode B=8 x 131072 keys, full", us, b5 * n5 * 2 * row * 2 + b5 * seq_bytes + H * 4 + 4 * b5 * p5, b5)
+
+
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
     decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
@@ -366,6 +463,8 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
+    ap.add_argument("--configs", action="store_true",
+                    help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
@@ -376,6 +475,9 @@ def main():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     if args.only:
         only(args.only, args.steps, args.warmup)
+        return
+    if args.configs:
+        bench_configs(args.steps, args.warmup)
         return
     r = run(args.steps, args.warmup, args.skip_cpu, args.skip_prefill)
 

@@ -225,19 +225,27 @@ constexpr DecodeVariant kDecodeVariants[kNumDecodeVariants] = {
 
 // Variant and keys per split. A work-group reads kb*128 bytes of each key row (kb KV heads; four
 // keep HBM accesses row-local) with wpk waves per head; the split is sized so that the launch has
-// about 384 work-groups of 16 waves (1.5 per CU on 256 CUs), each wave taking at least one 32-key
-// tile. Returns false when a split would span more pages than the kernel stages.
+// about the variant's target work-group count, rounded up to whole 32-key tiles per wave. Returns
+// false when a split would span more pages than the kernel stages.
 bool plan_split(moearc_ctx *c, const std::vector<SeqSpan> &spans, unsigned long G,
                 unsigned long page_tokens, int &variant, std::vector<uint32_t> &split_len) {
     variant = G >= 4 ? 3 : (G == 2 ? 2 : (G == 1 ? 1 : 3));
     if (c->decode_variant_override >= 0) variant = c->decode_variant_override;
-    const unsigned kb = kDecodeVariants[variant].kb, wpk = kDecodeVariants[variant].wpk;
-    const uint64_t nkb = (G + kb - 1) / kb;
+    uint64_t keys = 0;
+    for (auto &s : spans) keys += (uint64_t) (s.end - s.begin);
+    auto base_of = [&](int v) {
+        const uint64_t nkb = (G + kDecodeVariants[v].kb - 1) / kDecodeVariants[v].kb;
+        const uint64_t target_wgs = kDecodeVariants[v].target_wgs;
+        return (keys * nkb + target_wgs - 1) / target_wgs;
+    };
+    // Too few keys to give the 4-head work-groups full splits (short contexts, windowed layers):
+    // one-head work-groups of 4 waves give 4x the work-groups (measured: 4K keys 12.4 -> 10.4 us,
+    // 32 sequences of SWA-128 10.5 -> 7.8 us).
+    if (c->decode_variant_override < 0 && variant == 3 && base_of(3) < 32ull * kDecodeVariants[3].wpk)
+        variant = 0;
+    const unsigned wpk = kDecodeVariants[variant].wpk;
     const uint64_t quantum = 32ull * wpk;  // one tile per wave
-    uint64_t total = 0;
-    for (auto &s : spans) total += (uint64_t) (s.end - s.begin) * nkb;
-    const uint64_t target_wgs = kDecodeVariants[variant].target_wgs;
-    uint64_t base = (total + target_wgs - 1) / target_wgs;
+    uint64_t base = base_of(variant);
     split_len.resize(spans.size());
     for (size_t i = 0; i < spans.size(); ++i) {
         uint64_t len = c->split_override ? c->split_override : base;
