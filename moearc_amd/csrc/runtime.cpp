@@ -777,13 +777,6 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     a.pt_shift = log2u(page_tokens);
     a.out_f16 = out_type;
     a.scale_log2e = scale_log2e;
-    // Each work-group stages the block-table entries of its key span in LDS (PF_PT_CAP = 2048).
-    {
-        const unsigned long tok = MOEARC_PREFILL_ROWS / group;
-        const unsigned long full = (pos0 + n_q - 1) / page_tokens + 1;
-        const unsigned long win = n_swa ? (tok + n_swa + 64) / page_tokens + 2 : full;
-        if (std::min(full, win) > 2048ul) return ERR_ARG;
-    }
     // query rows (token x head) per work-group
     const uint32_t rows_per_tile = precise ? MOEARC_PREFILL_ROWS : MOEARC_PREFILL_FAST_ROWS;
     const uint64_t rows = (uint64_t) n_q * group;

@@ -64,6 +64,20 @@ def test_shapes_against_oracle(ctx, group, n_q, pos0, pt, n_swa):
 
 
 @pytest.mark.parametrize("precise", [False, True])
+def test_long_context_small_pages(monkeypatch, precise):
+    # 40,024 keys in 16-token pages: 2,502 block-table entries per row's span (the kernels read
+    # block-table entries per tile, so no page-count limit applies)
+    from moearc_amd import Context
+    monkeypatch.setenv("MOEARC_PREFILL_PRECISE", "1" if precise else "0")
+    pc = fx.prefill_case(0x5E, n_q=24, pos0=40000, pt=16)
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q, pc.pos0, 0,
+                               pc.H, pc.G, pc.D, pc.pt, float(pc.scale), sinks=pc.sinks, n_threads=16)
+    with Context() as cx:
+        got = _run(cx, pc, 0)
+    _report(f"prefill 40024 keys, 16-token pages, precise={precise}", got, want)
+
+
+@pytest.mark.parametrize("precise", [False, True])
 def test_rows_equal_decode_calls(monkeypatch, precise):
     # the defining property: row i == moearc_attn_decode at n_kv = pos0 + i + 1 (f16 q widened).
     # The precise variant carries p to ~22 bits like decode; the default one p in f16.
