@@ -69,16 +69,17 @@ __device__ __forceinline__ uint32_t key_row(const uint32_t *pt_lds, uint32_t j, 
     return (pt_lds[(j >> sh) - page0] << sh) | (j & ((1u << sh) - 1u));
 }
 
-__device__ __forceinline__ void load_tile(TileRegs &r, const DecodeArgs &a, const uint32_t *pt_lds,
-                                          uint32_t page0, uint32_t j0, uint32_t te, uint32_t kvh,
-                                          uint32_t lane) {
-    const uint32_t sh = a.pt_shift;
+// Loads one 32-key tile; row_of(j) is the physical row of logical key j (through the page table
+// staged in LDS, or straight from the block table).
+template <typename RowOf>
+__device__ __forceinline__ void load_tile_rows(TileRegs &r, const DecodeArgs &a, RowOf row_of,
+                                               uint32_t j0, uint32_t te, uint32_t kvh, uint32_t lane) {
     const uint64_t row_elems = (uint64_t) a.n_kv_heads * 64u;
     const uint32_t g = lane >> 4, m = lane & 15u;
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
         const uint32_t j = min(j0 + 16u * blk + m, te - 1u);
-        const uint64_t off = (uint64_t) key_row(pt_lds, j, page0, sh) * row_elems + (uint64_t) kvh * 64u + 8u * g;
+        const uint64_t off = (uint64_t) row_of(j) * row_elems + (uint64_t) kvh * 64u + 8u * g;
         const uint16_t *ks = a.k_pages + off;
         const uint16_t *vs = a.v_pages + off;
         // Plain loads: the non-temporal hint measured 15% slower for this pattern (each 128-byte
@@ -88,6 +89,22 @@ __device__ __forceinline__ void load_tile(TileRegs &r, const DecodeArgs &a, cons
         r.v[blk][0] = *(const u32x4_t *) vs;
         r.v[blk][1] = *(const u32x4_t *) (vs + 32);
     }
+}
+
+__device__ __forceinline__ void load_tile(TileRegs &r, const DecodeArgs &a, const uint32_t *pt_lds,
+                                          uint32_t page0, uint32_t j0, uint32_t te, uint32_t kvh,
+                                          uint32_t lane) {
+    const uint32_t sh = a.pt_shift;
+    load_tile_rows(r, a, [&](uint32_t j) { return key_row(pt_lds, j, page0, sh); }, j0, te, kvh, lane);
+}
+
+// The same tile with its page ids read from the block table in global memory: a wave's first tile
+// issues its loads one round trip after launch instead of after the LDS staging and its barrier.
+__device__ __forceinline__ void load_tile_bt(TileRegs &r, const DecodeArgs &a, const uint32_t *bt,
+                                             uint32_t j0, uint32_t te, uint32_t kvh, uint32_t lane) {
+    const uint32_t sh = a.pt_shift;
+    load_tile_rows(r, a, [&](uint32_t j) { return (bt[j >> sh] << sh) | (j & ((1u << sh) - 1u)); },
+                   j0, te, kvh, lane);
 }
 
 struct SoftmaxState {
@@ -213,12 +230,23 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
     const bool head_ok = kvh_ok && n < group;
     const uint32_t h = min(kvh, G - 1u) * group + (n < group ? n : 0u);
     const uint32_t *bt = a.block_tables + (uint64_t) b * a.bt_stride;
+    const bool has_tiles = kvh_ok && sub < ntiles;
 
     // ---- stage this split's block-table entries in LDS ------------------------------------------
     const uint32_t sh = a.pt_shift;
     const uint32_t page0 = tb >> sh;
     const uint32_t npages = ((te - 1u) >> sh) - page0 + 1u;  // host guarantees <= PT_CAP
-    for (uint32_t i = threadIdx.x; i < npages; i += 64u * WAVES) pt_lds[i] = bt[page0 + i];
+    // Start-up order: the page-table and q loads issue first, then this wave's first tile (page
+    // ids read straight from the block table), and only then do the page-table stores and the q
+    // arithmetic wait for their loads -- so the first KV loads leave one round trip after launch,
+    // not after the LDS staging and its barrier.
+    constexpr uint32_t PT_PER_THREAD = (PT_CAP + 64u * WAVES - 1u) / (64u * WAVES);
+    uint32_t ptv[PT_PER_THREAD];
+#pragma unroll
+    for (uint32_t k = 0; k < PT_PER_THREAD; ++k) {
+        const uint32_t i = threadIdx.x + k * 64u * WAVES;
+        ptv[k] = i < npages ? bt[page0 + i] : 0u;
+    }
 
     // ---- Q operands (B of QK^T): lane (g, n) holds head n, channels 32*hf + 8g .. +7 ----------
     float qv[16];
@@ -235,6 +263,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
             }
         }
     }
+    // This wave's first tile. Issued unconditionally (a wave without tiles loads an in-span key of
+    // an existing KV head and ignores it): a branch here would make the compiler's wait counts at
+    // the join assume these loads may be missing and drain them before the q arithmetic.
+    TileRegs r0;
+    load_tile_bt(r0, a, bt, tb + 32u * sub, te, min(kvh, G - 1u), lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t k = 0; k < PT_PER_THREAD; ++k) {
+        const uint32_t i = threadIdx.x + k * 64u * WAVES;
+        if (i < npages) pt_lds[i] = ptv[k];
+    }
+
     // Normalise each head's q by a power of two (exact) so that the hi/lo split keeps full relative
     // precision whatever q's magnitude; the inverse power folds into the score multiplier.
     float amax = 0.f;
@@ -269,7 +309,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
     st.l = 0.f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) st.O[mb] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    if (kvh_ok && sub < ntiles) {
+    if (has_tiles) {
         if constexpr (WAVES <= 8) {
             // Two tiles in flight per wave: the loads of the next tile issue before this one is
             // computed, over two register sets (ra, rb). The wave walks its tiles in pairs with a
@@ -280,8 +320,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
             const uint32_t nt = (ntiles - sub + WPK - 1u) / WPK;  // this wave's tiles, >= 1
             const uint32_t last = sub + (nt - 1u) * WPK;
             auto tile_of = [&](uint32_t i) { return sub + i * WPK; };
-            TileRegs ra, rb;
-            load_tile(ra, a, pt_lds, page0, tb + 32u * sub, te, kvh, lane);
+            TileRegs ra = r0, rb;
             for (uint32_t i = 0; i < nt; i += 2) {
                 load_tile(rb, a, pt_lds, page0, tb + 32u * min(tile_of(i + 1u), last), te, kvh, lane);
                 __builtin_amdgcn_sched_barrier(0);
@@ -293,7 +332,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
         } else {
             // 16-wave work-groups (128 VGPRs per wave): one tile in flight per wave, the
             // residency of four waves per SIMD keeps HBM busy.
-            for (uint32_t t = sub; t < ntiles; t += WPK) {
+            process_tile(st, r0, qhi, qlo, sel, c, tb + 32u * sub, te, g);
+            for (uint32_t t = sub + WPK; t < ntiles; t += WPK) {
                 const uint32_t j0 = tb + 32u * t;
                 TileRegs r;
                 load_tile(r, a, pt_lds, page0, j0, te, kvh, lane);
