@@ -212,15 +212,31 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t G = a.n_kv_heads;
-    const uint32_t nkb = (G + KB - 1u) / KB;
+    const uint32_t nkb = a.nkb;
     const uint32_t kbi = blockIdx.x % nkb;
     const uint32_t item = blockIdx.x / nkb;
+    // Sequence 0's span is read unconditionally, with no load depending on another, so a
+    // single-sequence launch resolves it in one round trip; later sequences search on.
+    uint32_t ib = a.item_begin[0], next = a.item_begin[1], kvb = a.kv_begin[0];
+    uint32_t nkv = a.n_kv[0], slen = a.split_len[0];
+    // Pin these (and the fields the first loads address with) in SGPRs here: otherwise the compiler
+    // folds the sequence-0 reads into the general lookup after its branch, a second round trip.
+    asm volatile("" ::"s"(ib), "s"(next), "s"(kvb), "s"(nkv), "s"(slen), "s"(a.pt_shift),
+                 "s"(a.n_kv_heads), "s"(a.bt_stride), "s"(a.block_tables), "s"(a.k_pages),
+                 "s"(a.v_pages));
     uint32_t b = 0;
-    while (item >= a.item_begin[b + 1]) ++b;
-    const uint32_t split = item - a.item_begin[b];
-    const uint32_t nsplit = a.item_begin[b + 1] - a.item_begin[b];
-    const uint32_t tb = a.kv_begin[b] + split * a.split_len[b];
-    const uint32_t te = min(a.n_kv[b], tb + a.split_len[b]);
+    if (item >= next) {
+        do ++b; while (item >= a.item_begin[b + 1]);
+        ib = a.item_begin[b];
+        next = a.item_begin[b + 1];
+        kvb = a.kv_begin[b];
+        nkv = a.n_kv[b];
+        slen = a.split_len[b];
+    }
+    const uint32_t split = item - ib;
+    const uint32_t nsplit = next - ib;
+    const uint32_t tb = kvb + split * slen;
+    const uint32_t te = min(nkv, tb + slen);
     const uint32_t ntiles = (te - tb + 31u) >> 5;
     const uint32_t kl = wave % KB, sub = wave / KB;
     const uint32_t kvh = kbi * KB + kl;
@@ -410,7 +426,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
         const uint32_t kv2 = kbi * KB + k2;
         if (kv2 >= G) break;
         const uint32_t hn = e >> 6, d = e & 63u;
-        const float *rec0 = a.ws + ((uint64_t) a.item_begin[b] * G + kv2) * MOEARC_PARTIAL_FLOATS;
+        const float *rec0 = a.ws + ((uint64_t) ib * G + kv2) * MOEARC_PARTIAL_FLOATS;
         float M = -INFINITY, L = 0.f, acc = 0.f;
         for (uint32_t s0 = 0; s0 < nsplit; s0 += BATCH) {
             float v[BATCH], ms[BATCH], ls[BATCH];
@@ -442,8 +458,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a) {
 }
 
 // Split merge: for every sequence whose span was split (records are [item][kv head]), one
-// MOEARC_MERGE_THREADS (256) work-group per (sequence, query head, quarter of the 64 channels), so a launch has
-// four work-groups per head. Lane (sg, c) owns channel c of the quarter for the splits
+// MOEARC_MERGE_THREADS (256) work-group per (sequence, query head, quarter of the 64 channels), so a
+// launch has four work-groups per head (grid x: head and quarter, y: sequence). Lane (sg, c) owns channel c of the quarter for the splits
 // sg, sg + 16, ...; it issues every load of a round (its channel, and each split's max and
 // denominator) before using any, so up to 16 * MERGE_BATCH splits cost one memory round trip.
 // The 16 split groups then combine by shuffles within a wave and through LDS across the four
@@ -469,16 +485,17 @@ __device__ __forceinline__ void merge_partial(float &m, float &l, float &o, floa
 extern "C" __global__ __launch_bounds__(MOEARC_MERGE_THREADS) void moearc_attn_decode_merge(const DecodeArgs a) {
     __shared__ float red[4][3][16];  // [wave][m, l, o][channel]
     const uint32_t tid = threadIdx.x, c = tid & 15u, sg = tid >> 4, wave = tid >> 6;
-    const uint32_t per_seq = a.n_heads * MOEARC_MERGE_PARTS;
-    const uint32_t b = blockIdx.x / per_seq;
-    const uint32_t rem = blockIdx.x - b * per_seq;
-    const uint32_t hh = rem / MOEARC_MERGE_PARTS, part = rem - hh * MOEARC_MERGE_PARTS;
-    const uint32_t nsplit = a.item_begin[b + 1] - a.item_begin[b];
+    // grid: x = (query head, channel quarter), y = sequence -- the sequence's item range needs no
+    // load before it can be read
+    const uint32_t b = blockIdx.y;
+    const uint32_t ib0 = a.item_begin[b], ib1 = a.item_begin[b + 1];
+    const uint32_t G = a.n_kv_heads, group = a.group;
+    const uint32_t hh = blockIdx.x / MOEARC_MERGE_PARTS, part = blockIdx.x % MOEARC_MERGE_PARTS;
+    const uint32_t nsplit = ib1 - ib0;
     if (nsplit <= 1u) return;  // finished by the split kernel itself
-    const uint32_t G = a.n_kv_heads;
-    const uint32_t kvh = hh / a.group, hn = hh - kvh * a.group;
+    const uint32_t kvh = hh / group, hn = hh - kvh * group;
     const uint32_t d = 16u * part + c;
-    const float *rec0 = a.ws + ((uint64_t) a.item_begin[b] * G + kvh) * MOEARC_PARTIAL_FLOATS;
+    const float *rec0 = a.ws + ((uint64_t) ib0 * G + kvh) * MOEARC_PARTIAL_FLOATS;
     const uint64_t rstride = (uint64_t) G * MOEARC_PARTIAL_FLOATS;
     float m_t = -INFINITY, l_t = 0.f, o_t = 0.f;
     for (uint32_t s0 = sg; s0 < nsplit; s0 += 16u * MERGE_BATCH) {

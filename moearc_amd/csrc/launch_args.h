@@ -26,8 +26,8 @@
 
 // Kernel arguments of the split-K decode. Passed by value; the per-sequence arrays let one launch
 // serve a ragged batch. Work item `it` (one (sequence, split) pair) covers the work-groups
-// it * n_kv_heads + kvh for every KV head kvh, so consecutive work-groups -- which the dispatcher
-// places on consecutive XCDs -- take consecutive KV heads of the same split.
+// it * nkb + kbi for every KV-head block kbi, so consecutive work-groups -- which the dispatcher
+// places on consecutive XCDs -- take consecutive KV-head blocks of the same split.
 struct DecodeArgs {
     const float *q;               // [n_seqs][n_heads][64] f32
     const uint16_t *k_pages;      // f16 bits, [page][slot][kv_head][64]
@@ -46,10 +46,12 @@ struct DecodeArgs {
     uint32_t out_f16;
     float scale_log2e;            // scale * log2(e)
     uint32_t n_seqs;
-    uint32_t item_begin[MOEARC_MAX_SEQS_PER_LAUNCH + 1]; // first work item of each sequence
-    uint32_t kv_begin[MOEARC_MAX_SEQS_PER_LAUNCH];
+    uint32_t nkb;                 // KV-head blocks per work item (KV heads / heads per work-group)
+    uint32_t item_begin[MOEARC_MAX_SEQS_PER_LAUNCH + 1]; // first work item of each sequence; entries
+                                                         // n_seqs .. the end: the work-item count
+    uint32_t kv_begin[MOEARC_MAX_SEQS_PER_LAUNCH];       // key span [kv_begin, n_kv)
     uint32_t n_kv[MOEARC_MAX_SEQS_PER_LAUNCH];
-    uint32_t split_len[MOEARC_MAX_SEQS_PER_LAUNCH];   // keys per split (a multiple of 32)
+    uint32_t split_len[MOEARC_MAX_SEQS_PER_LAUNCH];      // keys per split (a multiple of 32)
 };
 
 // General decode (any head_dim <= 1024, f32 or f16 KV, any page size, any group).

@@ -340,6 +340,9 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
         a.out_f16 = out_f16;
         a.scale_log2e = scale * 1.4426950408889634f;
         a.n_seqs = (uint32_t) cnt;
+        const unsigned kb = kDecodeVariants[variant].kb, wpk = kDecodeVariants[variant].wpk;
+        const size_t nkb = (n_kv_heads + kb - 1) / kb;
+        a.nkb = (uint32_t) nkb;
         uint32_t items = 0;
         for (size_t i = 0; i < cnt; ++i) {
             a.item_begin[i] = items;
@@ -349,8 +352,6 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
             items += (sub[i].end - sub[i].begin + split_len[i] - 1) / split_len[i];
         }
         for (size_t i = cnt; i <= MOEARC_MAX_SEQS_PER_LAUNCH; ++i) a.item_begin[i] = items;
-        const unsigned kb = kDecodeVariants[variant].kb, wpk = kDecodeVariants[variant].wpk;
-        const size_t nkb = (n_kv_heads + kb - 1) / kb;
         const size_t wgs = (size_t) items * nkb;
         if (wgs > 0x7FFFFFFFull) return ERR_ARG;
         if (ensure_workspace(c, (size_t) items * n_kv_heads * MOEARC_PARTIAL_FLOATS)) return ERR;
@@ -365,8 +366,8 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
                               64u * kb * wpk, a, "attn_decode.split", n_heads, head_dim);
         if (rc) return rc;
         if (any_split && !fused) {
-            const int rm = launch(c, c->f_dec_merge, (unsigned) (cnt * n_heads * MOEARC_MERGE_PARTS), c->merge_threads, a,
-                                  "attn_decode.merge", n_heads, head_dim);
+            const int rm = launch2d(c, c->f_dec_merge, (unsigned) (n_heads * MOEARC_MERGE_PARTS), (unsigned) cnt,
+                                    c->merge_threads, a, "attn_decode.merge", n_heads, head_dim);
             if (rm) return rm;
         }
     }
