@@ -4,8 +4,9 @@ Two artefacts, both written next to this file:
 
 * ``moearc_attn_gfx950.co`` -- the device code object (every kernel, one translation unit), built
   by ``hipcc --genco`` for gfx950 only and loaded at context creation with ``hipModuleLoad``;
-* ``libmoearc_attn.so`` -- the host runtime behind the C ABI in ``include/moearc_attn.h``, built by
-  the host compiler against the HIP runtime API (no device code in it).
+* ``libmoearc_attn.so`` -- the host runtime behind the C ABI in ``include/moearc_attn.h`` and the
+  KV page pool of ``include/moearc_kv.h``, built by the host compiler against the HIP runtime API
+  (no device code in it).
 
 Run ``python -m moearc_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -57,7 +58,7 @@ def build(verbose: bool = False) -> None:
     tmp_so = LIBRARY + ".tmp"
     _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", CSRC, "-I", os.path.join(ROCM, "include"),
-          os.path.join(CSRC, "runtime.cpp"), "-o", tmp_so,
+          os.path.join(CSRC, "runtime.cpp"), os.path.join(CSRC, "kv_cache.cpp"), "-o", tmp_so,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl",
           "-Wl,-rpath," + os.path.join(ROCM, "lib")], verbose)
     os.replace(tmp_so, LIBRARY)

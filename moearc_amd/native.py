@@ -1,4 +1,5 @@
-"""ctypes binding of ``libmoearc_attn.so`` (the C ABI in ``include/moearc_attn.h``).
+"""ctypes binding of ``libmoearc_attn.so`` (the C ABI in ``include/moearc_attn.h`` and
+``include/moearc_kv.h``).
 
 The library is loaded from this package's directory only. A missing library is an error, never a
 fallback: there is no CPU implementation behind this package.
@@ -54,6 +55,20 @@ SIGNATURES = {
                                                    _c_ulong, ctypes.c_float, ctypes.c_float,
                                                    ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                                    ctypes.c_float, ctypes.c_int, _u32]),
+    # include/moearc_kv.h
+    "moearc_kv_pool_create": (ctypes.c_int, [_u32, _u32, _u32, ctypes.POINTER(_vp)]),
+    "moearc_kv_pool_destroy": (None, [_vp]),
+    "moearc_kv_pool_last_error": (ctypes.c_int, [_vp, _vp, _vp]),
+    "moearc_kv_pool_begin": (ctypes.c_int, [_vp, ctypes.c_uint64, _u32]),
+    "moearc_kv_pool_append": (ctypes.c_int, [_vp, ctypes.c_uint64, _vp, _vp]),
+    "moearc_kv_pool_append_chunk": (ctypes.c_int, [_vp, ctypes.c_uint64, _u32, _vp, _vp]),
+    "moearc_kv_pool_end": (ctypes.c_int, [_vp, ctypes.c_uint64, _vp]),
+    "moearc_kv_pool_pages": (ctypes.c_int, [_vp, ctypes.c_uint64, _vp, _u32, _vp, _vp]),
+    "moearc_kv_pool_can_admit": (ctypes.c_int, [_vp, _u32]),
+    "moearc_kv_pool_usage": (ctypes.c_int, [_vp, _vp]),
+    "moearc_kv_pool_block_tables": (ctypes.c_int, [_vp, _vp, _u32, _u32, _vp]),
+    "moearc_kv_geometry": (ctypes.c_int, [_u32, _u32, _u32, _u32, _vp, _vp]),
+    "moearc_kv_ring_table": (ctypes.c_int, [_u32, _u32, _vp]),
 }
 
 _lib = None

@@ -1,4 +1,4 @@
-"""The C ABI library loads and exports every symbol include/moearc_attn.h declares (CPU only).
+"""The C ABI library loads and exports every symbol include/*.h declares (CPU only).
 
 No compute call is made: only entry points refused on the host before any device work (a null
 context returns -1, the reference's null-argument code) are called.
@@ -6,6 +6,7 @@ context returns -1, the reference's null-argument code) are called.
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 
@@ -15,15 +16,16 @@ from moearc_amd import native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "moearc_attn.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
-def declared_symbols():
-    text = open(HEADER).read()
+def declared_symbols(headers=None):
+    text = "".join(open(h).read() for h in (headers or HEADERS))
     return sorted(set(re.findall(r"\b(moearc_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_reference_surface():
-    names = declared_symbols()
+    names = declared_symbols([HEADER])
     # the attention + lifecycle subset of crates/moearc-kernels/src/ffi.rs:20-234
     for n in ("moearc_ctx_create", "moearc_ctx_destroy", "moearc_profile_events_enabled",
               "moearc_profile_events_reset", "moearc_profile_events_report", "moearc_sync",
@@ -48,6 +50,13 @@ def test_code_object_holds_every_kernel_the_runtime_loads():
     assert kernels
     for k in kernels:
         assert k.encode() in blob, f"kernel {k} missing from the code object"
+
+
+def test_kv_pool_header_is_bound():
+    names = declared_symbols([os.path.join(ROOT, "include", "moearc_kv.h")])
+    assert "moearc_kv_pool_create" in names and "moearc_kv_ring_table" in names
+    lib = native.load()
+    assert lib.moearc_kv_pool_begin(None, 1, 1) == -1
 
 
 def test_null_context_is_refused_with_minus_one():
