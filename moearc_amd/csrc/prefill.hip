@@ -1,4 +1,8 @@
-// Chunked prefill over a paged f16 KV cache, head_dim 64, on gfx950 MFMA.
+// Chunked prefill over a paged f16 KV cache, head_dim 64, on gfx950 MFMA: the precise kernels
+// (moearc_attn_prefill_precise_g{1,2,4,8}, softmax weights carried as f16 hi + lo), which the host
+// selects when MOEARC_PREFILL_PRECISE=1 or when |scale * log2 e| > 1 (where the default kernels'
+// f16 pre-scaled Q could leave f16's range); and the layout helpers the default kernels
+// (prefill_fast.hip) share.
 //
 // Semantics are the reference engine's prefill -- one decode per prompt token
 // (moe.rs:1856-1862, session.rs:378-381): query row i sits at absolute position p = pos0 + i, its own
@@ -11,14 +15,15 @@
 // all the group's heads. Four waves take 32 rows each. Query tiles are dispatched latest first:
 // under the causal mask the latest tokens have the most keys, and the short tiles fill in behind.
 //
-// Keys stream through LDS in 64-key tiles, double-buffered: at the top of tile kt every wave waits
-// for its copies of tile kt and meets the others at a barrier, issues the copies of tile kt + 1
-// into the other buffer, then computes tile kt. The copies are global_load_lds_dwordx4 (16 bytes
-// per lane, placed at base + 16 * lane), so tiles go from the cache to LDS without passing through
-// registers. Wave w copies keys 16w..16w+15 of each tile; with pages of at least 16 tokens they
-// lie in one page, whose block-table entry is a wave-uniform scalar load, otherwise every lane
-// looks up its own key's page. Keys past the last query position are clamped to it, so no copy
-// reads a slot the cache has not written.
+// Keys stream through LDS in 32-key tiles (one chunk each), four buffers, copies three tiles ahead:
+// at the top of tile kt every wave waits for its copies of tile kt (a constant vmcnt: two copies
+// and one block-table load per step) and meets the others at a barrier, issues the copies of tile
+// kt + 3 into the buffer tile kt - 1 used, then computes tile kt. The copies are
+// global_load_lds_dwordx4 (16 bytes per lane, placed at base + 16 * lane), so tiles go from the
+// cache to LDS without passing through registers. Wave w copies keys 8w..8w+7 of each tile; when
+// the tile lies in one page its block-table entry is wave-uniform and the copy takes one scalar
+// base, otherwise every lane looks up its own key's page. Keys past the last query position are
+// clamped to it, so no copy reads a slot the cache has not written.
 //
 // Matrix layout: v_mfma_f32_32x32x16_f16 throughout (on gfx950 it leaves room for a few VALU
 // instructions beside each MFMA, where 16x16x32 leaves almost none). Per 32-key chunk a wave
@@ -51,12 +56,11 @@
 // m that moves only when some weight of the row overflows f16 (a score more than ~9 above m): the
 // weights are computed first, an infinite row sum flags the overflow, and only then are the
 // cross-lane row maximum, the rescale of O and the sums and the recomputation run (in practice at
-// a row's first chunk). So p < 2^16 fits f16, and the common chunk computes no maximum. P enters the MFMA as one f16 operand with
-// f32 accumulation: the weights carry f16's 11 bits, an output error of at most 2^-12 max|V|
-// (measured ~2.5e-4 on N(0,1) data); the row sums are dot products of the same f16 weights with
-// ones (v_dot2_f32_f16), so numerator and denominator see the same rounding. The _precise_
-// variants split p = p_hi + p_lo into two f16 operands, keeping ~22 bits like the decode kernel.
-// Causal/window masks are applied only in chunks that cross a row's span boundary.
+// a row's first chunk). So p < 2^16 fits f16, and the common chunk computes no maximum. p is split
+// p = p_hi + p_lo into two f16 MFMA operands (~22 bits, like the decode kernel), so prefill rows
+// equal decode calls to ~2e-7; the row sums are dot products of the same f16 parts with ones
+// (v_dot2_f32_f16), so numerator and denominator see the same rounding. Causal/window masks are
+// applied only in chunks that cross a row's span boundary.
 #include "common.h"
 
 #define PF_LOG2_PSCALE 7.0f
@@ -128,7 +132,7 @@ __device__ __forceinline__ void pf_copy16(const void *sbase, uint32_t voff, uint
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
 
-template <int GROUP, bool SPLIT_P>
+template <int GROUP>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     constexpr uint32_t ROWS = MOEARC_PREFILL_ROWS;  // 128 rows per work-group
     constexpr uint32_t TOK = ROWS / GROUP;          // query tokens per work-group
@@ -176,32 +180,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     const uint32_t w_bmax = a.n_swa ? (w_pmax + 1u > a.n_swa ? w_pmax + 1u - a.n_swa : 0u) : 0u;
 
     float c = a.scale_log2e;
-    if constexpr (SPLIT_P) {
-        // s*c with c < 0 equals (-s)*(-c): negate the f16 Q operand (exact) so that c > 0 and the
-        // row maximum of s*c is c times the maximum of s
-        if (c < 0.f) {
-            c = -c;
+    // s*c with c < 0 equals (-s)*(-c): negate the f16 Q operand (exact) so that c > 0 and the row
+    // maximum of s*c is c times the maximum of s
+    if (c < 0.f) {
+        c = -c;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) qop[t] = -qop[t];
-        }
-    } else {
-        // Q is pre-scaled by c (one more f16 rounding of each q element, the same relative size as
-        // the rounding of the weights; the host uses the _precise_ kernels when |c| > 1, where q*c
-        // could leave f16's range), so the MFMA yields scores in the log2 domain directly.
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qop[t][i] = (_Float16) ((float) qop[t][i] * c);
+        for (int t = 0; t < 4; ++t) qop[t] = -qop[t];
     }
     float m_run = PF_M_INIT;
     float l_run = 0.f;  // this lane's share of the row sum (its 16 keys of every chunk)
-    // Single-f16 kernels: the QK^T accumulator starts from PF_LOG2_PSCALE - m_run in every register,
-    // so the MFMA returns the exponent of each weight and the common chunk needs no VALU before the
-    // exp (a VALU op issued beside MFMAs costs several times its nominal rate on gfx950; the
-    // transcendental unit does not compete with them).
-    float16_t biasv;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) biasv[i] = PF_LOG2_PSCALE - m_run;
     float16_t O[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -286,19 +273,17 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     auto weights = [&](const float16_t &S, float bias, float l0, half8_t (&phi)[2], half8_t (&plo)[2]) {
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-            const float x0 = SPLIT_P ? fmaf(S[i], c, bias) : S[i];
-            const float x1 = SPLIT_P ? fmaf(S[i + 1], c, bias) : S[i + 1];
+            const float x0 = fmaf(S[i], c, bias);
+            const float x1 = fmaf(S[i + 1], c, bias);
             const float p0 = __builtin_amdgcn_exp2f(x0);
             const float p1 = __builtin_amdgcn_exp2f(x1);
             const half2_t hv = {(_Float16) p0, (_Float16) p1};
             phi[i >> 3][i & 7] = hv[0];
             phi[i >> 3][(i & 7) + 1] = hv[1];
             l0 = __builtin_amdgcn_fdot2(hv, ones2, l0, false);
-            if constexpr (SPLIT_P) {
-                const half2_t lv = {(_Float16) (p0 - (float) hv[0]), (_Float16) (p1 - (float) hv[1])};
-                plo[i >> 3][i & 7] = lv[0];
-                plo[i >> 3][(i & 7) + 1] = lv[1];
-            }
+            const half2_t lv = {(_Float16) (p0 - (float) hv[0]), (_Float16) (p1 - (float) hv[1])};
+            plo[i >> 3][i & 7] = lv[0];
+            plo[i >> 3][(i & 7) + 1] = lv[1];
         }
         return l0;
     };
@@ -315,17 +300,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     // that has seen none) yields a weight >= 2^16, which overflows f16 and makes the lane's sum
     // infinite. Only then is the row maximum taken, the reference moved (O and l rescaled) and
     // the weights recomputed, so weights stay below 2^16 and the common chunk pays no max.
-    // raw(): the chunk's scores s*c without the reference (single-f16 kernels: recomputed from a
-    // zero accumulator, since a row's first bias, PF_LOG2_PSCALE - PF_M_INIT, dwarfs them).
-    auto softmax = [&](float16_t &S, auto raw, half8_t (&phi)[2], half8_t (&plo)[2]) {
+    auto softmax = [&](float16_t &S, half8_t (&phi)[2], half8_t (&plo)[2]) {
         float l_new = weights(S, PF_LOG2_PSCALE - m_run, l_run, phi, plo);
         if (__builtin_amdgcn_ballot_w64(l_new == INFINITY) != 0) {
-            float16_t R;
-            if constexpr (SPLIT_P) {
-                R = S * c;
-            } else {
-                R = raw();
-            }
+            const float16_t R = S * c;
             float lmax = fmaxf(R[0], R[1]);
 #pragma unroll
             for (int i = 2; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(R[i], R[i + 1]));
@@ -335,19 +313,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
             l_run *= corr;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) O[mb] *= corr;
-            const float bias = PF_LOG2_PSCALE - m_run;
-            if constexpr (SPLIT_P) {
-                l_new = weights(S, bias, l_run, phi, plo);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    biasv[i] = bias;
-                    S[i] = R[i] + bias;
-                }
-                l_new = weights(S, bias, l_run, phi, plo);
-            }
+            l_new = weights(S, PF_LOG2_PSCALE - m_run, l_run, phi, plo);
         }
-        if constexpr (SPLIT_P) l_new = lo_sum(plo, l_new);
+        l_new = lo_sum(plo, l_new);
         l_run = l_new;
     };
     // P.V per channel block: operands of steps 0, 1 from four transposing reads
@@ -362,7 +330,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
                 const half8_t va = __builtin_bit_cast(
                     half8_t, (u32x4_t){vt[2 * s][0], vt[2 * s][1], vt[2 * s + 1][0], vt[2 * s + 1][1]});
                 O[mb] = pf_mfma(va, phi[s], O[mb]);
-                if constexpr (SPLIT_P) O[mb] = pf_mfma(va, plo[s], O[mb]);
+                O[mb] = pf_mfma(va, plo[s], O[mb]);
             }
         });
     };
@@ -377,15 +345,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) zero[i] = 0.f;
         const bool masked = jc + 31u > w_pmin || (a.n_swa && jc < w_bmax);
-        float16_t S = qk(boff_c, K0{}, SPLIT_P ? zero : biasv);
+        float16_t S = qk(boff_c, K0{}, zero);
         if (masked) mask(S, jc);
-        auto raw = [&]() {
-            float16_t R = qk(boff_c, K0{}, zero);
-            if (masked) mask(R, jc);
-            return R;
-        };
         half8_t phi[2], plo[2];
-        softmax(S, raw, phi, plo);
+        softmax(S, phi, plo);
         pv(boff_c, K0{}, phi, plo);
     };
 
@@ -468,7 +431,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
 #define PREFILL_KERNEL(GRP)                                                                      \
     extern "C" __global__ __launch_bounds__(MOEARC_PREFILL_THREADS) void                        \
         moearc_attn_prefill_precise_g##GRP(const PrefillArgs a) {                                \
-        prefill_body<GRP, true>(a);                                                              \
+        prefill_body<GRP>(a);                                                              \
     }
 
 PREFILL_KERNEL(1)
