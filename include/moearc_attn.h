@@ -165,6 +165,46 @@ int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, con
                                 float freq_scale, float ext_factor, float attn_factor,
                                 float corr_lo, float corr_hi, int neox, unsigned int kv_type);
 
+/* ---- attention projections: matrix-vector products and the bias add ---------------------------
+ * Weight formats by GGUF type id: 0 F32, 1 F16, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K, 39 MXFP4, laid
+ * out as ggml writes them (row-major, each row n_cols / block_elems blocks). All pointers are
+ * device pointers; W may sit at any byte alignment. Results match the reference's f64 twin
+ * (reference.rs:305-336) within 2 (n_cols/32 + 5) * 2^-24 * sum|w x| per row. */
+
+/* ffi.rs:68-75, kernels.cpp:1046-1111: out[r] = sum_c W[r][c] x[c] for r < n_rows.
+ * Refusals: null pointer -> -1; unknown type_id, n_cols not a whole number of blocks,
+ * n_rows >= 2^32 or n_cols >= 2^31 -> -2. n_rows == 0 -> 0, nothing enqueued. */
+int moearc_matvec_q(moearc_ctx *c, unsigned int type_id, float *out, const void *w,
+                    const float *x, unsigned long n_rows, unsigned long n_cols);
+
+/* ffi.rs:77-87, kernels.cpp:1146-1206: n_mat matrices of one type and shape in one launch;
+ * matrix m reads x + m * x_stride (x_stride 0: one shared x) and writes out[m * n_rows ..]. w is a
+ * HOST array of n_mat device pointers. Bit-identical to n_mat moearc_matvec_q calls.
+ * Refusals: null c/out/w/x or a null w[m] -> -1; n_mat > 32, and those of moearc_matvec_q -> -2.
+ * n_mat == 0 or n_rows == 0 -> 0. */
+int moearc_matvec_q_batched(moearc_ctx *c, unsigned int type_id, float *out,
+                            const void *const *w, unsigned int n_mat, const float *x,
+                            unsigned long x_stride, unsigned long n_rows, unsigned long n_cols);
+
+/* ffi.rs:97-103, kernels.cpp:1116-1135: moearc_matvec_q over f32 weights (w f32 [n_rows][n_cols]).
+ * Refusals: null pointer -> -1. */
+int moearc_matvec_f32(moearc_ctx *c, float *out, const float *w, const float *x,
+                      unsigned long n_rows, unsigned long n_cols);
+
+/* ffi.rs:167-173, kernels.cpp:1676-1683: out[i] = a[i] + b[i]; out may alias a or b.
+ * Refusals: null pointer -> -1. n == 0 -> 0. */
+int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsigned long n);
+
+/* Extension (no counterpart in the reference, which runs three moearc_matvec_q and up to three
+ * moearc_add calls for attn.qkv, moe.rs:1942-1959): projection i (0 q, 1 k, 2 v) writes
+ * out[i][r] = sum_c W_i[r][c] x[c] + bias[i][r] for r < rows[i] (bias[i] may be null), one launch
+ * per distinct weight type. Bit-identical to the reference's sequence. type_ids, out, w, bias and
+ * rows are HOST arrays of 3. Refusals: null c/x/arrays or a null out[i]/w[i] with rows[i] > 0 ->
+ * -1; those of moearc_matvec_q for each projection -> -2. */
+int moearc_attn_qkv(moearc_ctx *c, const unsigned int *type_ids, float *const *out,
+                    const void *const *w, const float *const *bias, const unsigned long *rows,
+                    const float *x, unsigned long n_cols);
+
 /* The stream the context enqueues on (a hipStream_t), so a caller can order its own work. */
 void *moearc_ctx_stream(moearc_ctx *c);
 

@@ -363,3 +363,103 @@ class Context:
                                            n_swa, n_heads, n_kv_heads, head_dim, page_tokens,
                                            float(scale), int(KvType(kv)))
         self.finish(rc, "chunked prefill attention")
+
+    # ---- attention projections -------------------------------------------------------------
+    def matvec_q(self, ty, out: DeviceBuffer, w: DeviceBuffer, x: DeviceBuffer, n_rows: int,
+                  n_cols: int) -> None:
+        """out[r] = W[r] . x against quantised weights (lib.rs matvec_q, kernels.cpp:1046-1111)."""
+        ty = QuantType(ty)
+        if n_cols % ty.block_elems:
+            raise BadArgument(f"{ty.name}: {n_cols} columns is not a whole number of blocks")
+        w.require("weights", n_rows * ty.row_bytes(n_cols))
+        x.require("activation", n_cols * 4)
+        out.require("output", n_rows * 4)
+        self.finish(self._lib.moearc_matvec_q(self.raw, int(ty), out.ptr, w.ptr, x.ptr, n_rows, n_cols),
+                    f"matvec {ty.name}")
+
+
+    def matvec_q_batched(self, ty, out: DeviceBuffer, ws, x: DeviceBuffer, x_stride: int, n_rows: int,
+                          n_cols: int) -> None:
+        """len(ws) matrices in one launch (lib.rs matvec_q_batched, kernels.cpp:1146-1206)."""
+        ty = QuantType(ty)
+        if n_cols % ty.block_elems:
+            raise BadArgument(f"{ty.name}: {n_cols} columns is not a whole number of blocks")
+        for w in ws:
+            w.require("weights", n_rows * ty.row_bytes(n_cols))
+        x.require("activation", ((len(ws) - 1) * x_stride + n_cols) * 4)
+        out.require("output", len(ws) * n_rows * 4)
+        ptrs = _ptr_array(ws)
+        self.finish(self._lib.moearc_matvec_q_batched(self.raw, int(ty), out.ptr, ptrs, len(ws), x.ptr,
+                                                      x_stride, n_rows, n_cols), f"batched matvec {ty.name}")
+
+
+    def matvec_f32(self, out: DeviceBuffer, w: DeviceBuffer, x: DeviceBuffer, n_rows: int,
+                    n_cols: int) -> None:
+        """out[r] = W[r] . x against f32 weights (kernels.cpp:1116-1135)."""
+        w.require("weights", n_rows * n_cols * 4)
+        x.require("activation", n_cols * 4)
+        out.require("output", n_rows * 4)
+        self.finish(self._lib.moearc_matvec_f32(self.raw, out.ptr, w.ptr, x.ptr, n_rows, n_cols),
+                    "matvec f32")
+
+
+    def add(self, out: DeviceBuffer, a: DeviceBuffer, b: DeviceBuffer, n: int) -> None:
+        """out = a + b, element-wise (kernels.cpp:1676-1683)."""
+        for buf, what in ((out, "output"), (a, "left operand"), (b, "right operand")):
+            buf.require(what, n * 4)
+        self.finish(self._lib.moearc_add(self.raw, out.ptr, a.ptr, b.ptr, n), "add")
+
+
+    def attn_qkv(self, types, outs, ws, biases, rows, x: DeviceBuffer, n_cols: int) -> None:
+        """The q, k, v projections plus their biases in as few launches as the types allow."""
+        types = [QuantType(t) for t in types]
+        for t, o, w, b, r in zip(types, outs, ws, biases, rows):
+            if n_cols % t.block_elems:
+                raise BadArgument(f"{t.name}: {n_cols} columns is not a whole number of blocks")
+            if r:
+                w.require("weights", r * t.row_bytes(n_cols))
+                o.require("output", r * 4)
+                if b is not None:
+                    b.require("bias", r * 4)
+        x.require("activation", n_cols * 4)
+        tarr = (ctypes.c_uint * 3)(*[int(t) for t in types])
+        rarr = (ctypes.c_ulong * 3)(*rows)
+        self.finish(self._lib.moearc_attn_qkv(self.raw, tarr, _ptr_array(outs), _ptr_array(ws),
+                                              _ptr_array(biases), rarr, x.ptr, n_cols), "attn qkv")
+
+
+class QuantType(enum.IntEnum):
+    """GGUF weight formats the matvec kernels expand (lib.rs ``QuantType``, reference.rs:69-121)."""
+    F32 = 0
+    F16 = 1
+    Q8_0 = 8
+    Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
+    MXFP4 = 39
+
+    @property
+    def block_bytes(self) -> int:
+        return {0: 4, 1: 2, 8: 34, 12: 144, 13: 176, 14: 210, 39: 17}[int(self)]
+
+    @property
+    def block_elems(self) -> int:
+        return {0: 1, 1: 1, 8: 32, 12: 256, 13: 256, 14: 256, 39: 32}[int(self)]
+
+    def row_bytes(self, n_cols: int) -> int:
+        return n_cols // self.block_elems * self.block_bytes
+
+
+class DeviceView(DeviceBuffer):
+    """A non-owning window into a DeviceBuffer (e.g. a tensor at an offset inside a weight blob)."""
+
+    def __init__(self, base: DeviceBuffer, offset: int, nbytes: Optional[int] = None):
+        self._base = base
+        super().__init__(base.ctx, base.ptr + offset, base.len - offset if nbytes is None else nbytes)
+
+    def free(self) -> None:
+        self.ptr = 0
+
+
+def _ptr_array(bufs) -> ctypes.Array:
+    return (ctypes.c_void_p * len(bufs))(*[b.ptr if b is not None else None for b in bufs])

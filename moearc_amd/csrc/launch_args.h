@@ -116,3 +116,56 @@ struct RopeParams {
     float corr_lo;
     float corr_hi;
 };
+
+// ---- quantised matrix-vector products (matvec.hip) ----------------------------------------------
+//
+// The weight formats, by GGUF type id: bytes per block (BB), elements per block (BE) and elements
+// per "piece" (PE) -- the share of a row one lane decodes at a time. A lane owns the pieces
+// lane, lane + 64, ... of every row, so the activation values of its pieces stay in registers
+// while it walks the rows; MOEARC_MV_PPL_MAX bounds its pieces per pass (a row with more is
+// walked in several column slabs).
+#define MOEARC_MV_MAX_SEG 32   // matrices (or projections) one launch carries
+#define MOEARC_MV_MAX_WAVES 8
+
+constexpr uint32_t moearc_mv_bb(uint32_t ty) {
+    return ty == 0 ? 4u : ty == 1 ? 2u : ty == 8 ? 34u : ty == 12 ? 144u : ty == 13 ? 176u
+         : ty == 14 ? 210u : ty == 39 ? 17u : 0u;
+}
+constexpr uint32_t moearc_mv_be(uint32_t ty) {
+    return ty == 0 || ty == 1 ? 1u : ty == 8 || ty == 39 ? 32u : ty == 12 || ty == 13 || ty == 14 ? 256u : 0u;
+}
+constexpr uint32_t moearc_mv_pe(uint32_t ty) {
+    return ty == 0 ? 8u : ty == 12 || ty == 13 || ty == 39 ? 32u : 16u;
+}
+// Largest pieces per lane per pass: activation registers (PPL * PE) stay at or under 128 and a
+// slab's staging buffer at or under 10 KiB.
+constexpr uint32_t moearc_mv_ppl_max(uint32_t ty) {
+    return ty == 8 || ty == 14 ? 8u : 4u;
+}
+// 16-byte granules one lane stages per slab (a slab of 64 * PPL pieces, any byte alignment).
+constexpr uint32_t moearc_mv_gmax(uint32_t ty, uint32_t ppl) {
+    return (uint32_t) ((64ull * ppl * moearc_mv_pe(ty) * moearc_mv_bb(ty) / moearc_mv_be(ty) + 30u + 1023u) / 1024u);
+}
+// Bytes of one wave's staging buffer: the granules plus slack for reads that run past a piece.
+constexpr uint32_t moearc_mv_wave_buf(uint32_t ty, uint32_t ppl) {
+    return moearc_mv_gmax(ty, ppl) * 1024u + 64u;
+}
+
+// Segment s covers work-groups [wg_end[s-1], wg_end[s]) and rows [0, rows[s]) of matrix w[s]:
+// out[s][r] = sum_c W_s[r][c] * x[s][c] (+ bias[s][r] when bias[s] is non-null).
+struct MatvecArgs {
+    const uint8_t *w[MOEARC_MV_MAX_SEG];
+    const float *x[MOEARC_MV_MAX_SEG];
+    const float *bias[MOEARC_MV_MAX_SEG];
+    float *out[MOEARC_MV_MAX_SEG];
+    uint32_t rows[MOEARC_MV_MAX_SEG];
+    uint32_t wg_end[MOEARC_MV_MAX_SEG];
+    uint64_t row_bytes;
+    uint32_t n_seg;
+    uint32_t n_cols;
+    uint32_t n_pieces;     // pieces per row, ceil(n_cols / PE)
+    uint32_t n_slabs;      // column slabs per row
+    uint32_t rpw;          // consecutive rows per wave
+    uint32_t x_in_lds;     // 1: the activation is staged once per work-group in LDS
+    uint32_t x_lds_bytes;  // LDS bytes before the waves' staging buffers
+};

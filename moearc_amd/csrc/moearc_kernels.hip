@@ -6,3 +6,4 @@
 #include "prefill.hip"
 #include "prefill_fast.hip"
 #include "rope.hip"
+#include "matvec.hip"

@@ -54,6 +54,17 @@ std::string library_dir() {
 
 bool is_pow2(unsigned long x) { return x && !(x & (x - 1)); }
 
+// Matvec weight formats (GGUF type ids), their kernel-name stems and profiling key names.
+constexpr uint32_t kMvTypes[7] = {0, 1, 8, 12, 13, 14, 39};
+constexpr const char *kMvNames[7] = {"f32", "f16", "q8_0", "q4_k", "q5_k", "q6_k", "mxfp4"};
+constexpr const char *kMvKeys[7] = {"F32", "F16", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "MXFP4"};
+
+int mv_type_index(unsigned ty) {
+    for (int t = 0; t < 7; ++t)
+        if (kMvTypes[t] == ty) return t;
+    return -1;
+}
+
 uint32_t log2u(unsigned long x) {
     uint32_t s = 0;
     while ((1ul << s) < x) ++s;
@@ -72,6 +83,8 @@ struct moearc_ctx {
     hipFunction_t f_dec_fast[7] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2, 1x8, 2x4
     hipFunction_t f_dec_merge = nullptr;
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
+    hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
+    hipFunction_t f_add = nullptr;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
     hipFunction_t f_prefill_precise[4] = {};  // the same with p split into f16 hi + lo
     bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
@@ -138,7 +151,8 @@ void record_bracket(moearc_ctx *c, hipEvent_t start, const char *what, unsigned 
 // launch under the key "<what> r<r> m<m>" (the reference's key format, kernels.cpp:1905-1916).
 template <typename Args>
 int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, unsigned block,
-             const Args &args, const char *what, unsigned long r, unsigned long m) {
+             const Args &args, const char *what, unsigned long r, unsigned long m,
+             unsigned lds_bytes = 0) {
     if (!f) return ERR;
     hipEvent_t e0 = nullptr;
     if (c->profiling && (e0 = take_event(c))) hipEventRecord(e0, c->stream);
@@ -146,7 +160,7 @@ int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, uns
     void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *) &args, HIP_LAUNCH_PARAM_BUFFER_SIZE,
                       &size, HIP_LAUNCH_PARAM_END};
     const hipError_t err =
-        hipModuleLaunchKernel(f, grid, grid_y, 1, block, 1, 1, 0, c->stream, nullptr, config);
+        hipModuleLaunchKernel(f, grid, grid_y, 1, block, 1, 1, lds_bytes, c->stream, nullptr, config);
     if (e0) record_bracket(c, e0, what, r, m);
     return err == hipSuccess ? OK : ERR;
 }
@@ -421,6 +435,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_dec_fast[5], "moearc_attn_decode_f16d64_k1w8"},
         {&c->f_dec_fast[6], "moearc_attn_decode_f16d64_k2w4"},
         {&c->f_dec_merge, "moearc_attn_decode_merge"},
+        {&c->f_add, "moearc_add_k"},
     };
     for (auto &f : fns) {
         if (hipModuleGetFunction(f.slot, c->module, f.name) != hipSuccess) {
@@ -453,6 +468,20 @@ moearc_ctx *moearc_ctx_create(void) {
             hipStreamDestroy(c->stream);
             delete c;
             return nullptr;
+        }
+    }
+    for (int t = 0; t < 7; ++t) {
+        for (int i = 0; i < 4; ++i) {
+            if ((1u << i) > moearc_mv_ppl_max(kMvTypes[t])) continue;
+            char name[64];
+            std::snprintf(name, sizeof(name), "moearc_matvec_%s_p%u", kMvNames[t], 1u << i);
+            if (hipModuleGetFunction(&c->f_mv[t][i], c->module, name) != hipSuccess) {
+                std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), name);
+                hipModuleUnload(c->module);
+                hipStreamDestroy(c->stream);
+                delete c;
+                return nullptr;
+            }
         }
     }
     const char *ev = std::getenv("MOEARC_PROFILE_EVENTS");
@@ -642,6 +671,165 @@ int moearc_copy_d2h(moearc_ctx *c, void *dst, const void *src, unsigned long byt
     if (!dst || !src) return ERR;
     if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return ERR;
     return hipStreamSynchronize(c->stream) == hipSuccess ? OK : ERR;
+}
+
+namespace {
+
+// One matrix of a matvec launch: out[r] = W[r] . x (+ bias[r]) for r < rows.
+struct MvJob {
+    const void *w;
+    const float *x;
+    const float *bias;
+    float *out;
+    unsigned long rows;
+};
+
+constexpr unsigned kMvLdsCap = 64u * 1024u;  // dynamic LDS per work-group the launches stay under
+constexpr unsigned long kMvWavesTarget = 256ul * 16ul;  // waves that fill the chip (16 per CU)
+
+// Shape checks shared by the matvec entry points (kernels.cpp:1053-1057): the type must be known
+// and a row a whole number of blocks.
+int mv_check(unsigned ty, unsigned long n_rows, unsigned long n_cols) {
+    if (mv_type_index(ty) < 0) return ERR_ARG;
+    if (n_cols % moearc_mv_be(ty) != 0) return ERR_ARG;
+    if (n_rows > 0xFFFFFFFFul || n_cols >= 0x80000000ul) return ERR_ARG;
+    return OK;
+}
+
+// Enqueue jobs[0..n) (all of weight type ty, n_cols columns) as one launch; n <= MOEARC_MV_MAX_SEG.
+int mv_launch(moearc_ctx *c, unsigned ty, const MvJob *jobs, unsigned n, unsigned long n_cols,
+              const char *what, unsigned long key_r, unsigned long key_m) {
+    const int t = mv_type_index(ty);
+    if (t < 0 || n == 0 || n > MOEARC_MV_MAX_SEG) return ERR_ARG;
+    const uint32_t pe = moearc_mv_pe(ty);
+    if (n_cols == 0) {  // empty rows: the sum is 0 (then the bias)
+        for (unsigned i = 0; i < n; ++i) {
+            if (!jobs[i].rows) continue;
+            const int rc = jobs[i].bias
+                               ? (hipMemcpyAsync(jobs[i].out, jobs[i].bias, jobs[i].rows * 4ul,
+                                                 hipMemcpyDeviceToDevice, c->stream) == hipSuccess ? OK : ERR)
+                               : moearc_zero(c, jobs[i].out, jobs[i].rows);
+            if (rc) return rc;
+        }
+        return OK;
+    }
+    const uint64_t pieces = (n_cols + pe - 1) / pe;
+    uint32_t li = 0;  // pieces per lane 1 << li
+    while ((64ull << li) < pieces && (2u << li) <= moearc_mv_ppl_max(ty)) ++li;
+    const uint32_t ppl = 1u << li;
+    const uint64_t slabs = (pieces + 64ull * ppl - 1) / (64ull * ppl);
+    const unsigned wave_buf = moearc_mv_wave_buf(ty, ppl);
+    const uint64_t x_lds = (pieces * (pe + 4u) * 4u + 15u) & ~15ull;
+    unsigned waves = MOEARC_MV_MAX_WAVES, x_in_lds = 1;
+    if (x_lds + (uint64_t) waves * wave_buf > kMvLdsCap) {
+        if (x_lds + 4ull * wave_buf <= kMvLdsCap) {
+            waves = 4;
+        } else {
+            x_in_lds = 0;
+            if ((uint64_t) waves * wave_buf > kMvLdsCap) waves = 4;
+        }
+    }
+    const uint64_t x_bytes = x_in_lds ? x_lds : 0;
+    unsigned long total = 0;
+    for (unsigned i = 0; i < n; ++i) total += jobs[i].rows;
+    if (total == 0) return OK;
+    const uint32_t rpw = (uint32_t) std::min<unsigned long>(64, std::max<unsigned long>(
+                                                                     1, (total + kMvWavesTarget - 1) / kMvWavesTarget));
+    MatvecArgs a{};
+    uint64_t wgs = 0;
+    for (unsigned i = 0; i < n; ++i) {
+        a.w[i] = static_cast<const uint8_t *>(jobs[i].w);
+        a.x[i] = jobs[i].x;
+        a.bias[i] = jobs[i].bias;
+        a.out[i] = jobs[i].out;
+        a.rows[i] = (uint32_t) jobs[i].rows;
+        wgs += (jobs[i].rows + (uint64_t) waves * rpw - 1) / ((uint64_t) waves * rpw);
+        if (wgs >= 0x7FFFFFFFull) return ERR_ARG;
+        a.wg_end[i] = (uint32_t) wgs;
+    }
+    a.row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
+    a.n_seg = n;
+    a.n_cols = (uint32_t) n_cols;
+    a.n_pieces = (uint32_t) pieces;
+    a.n_slabs = (uint32_t) slabs;
+    a.rpw = rpw;
+    a.x_in_lds = x_in_lds;
+    a.x_lds_bytes = (uint32_t) x_bytes;
+    char key[48];
+    std::snprintf(key, sizeof(key), "%s %s", what, kMvKeys[t]);
+    return launch2d(c, c->f_mv[t][li], (unsigned) wgs, 1, 64u * waves, a, key, key_r, key_m,
+                    (unsigned) (x_bytes + (uint64_t) waves * wave_buf));
+}
+
+}  // namespace
+
+int moearc_matvec_q(moearc_ctx *c, unsigned int type_id, float *out, const void *w,
+                    const float *x, unsigned long n_rows, unsigned long n_cols) {
+    if (!c || !out || !w || !x) return ERR;
+    if (const int rc = mv_check(type_id, n_rows, n_cols)) return rc;
+    if (n_rows == 0) return OK;
+    const MvJob j{w, x, nullptr, out, n_rows};
+    return mv_launch(c, type_id, &j, 1, n_cols, "mvq", n_rows, 1);
+}
+
+int moearc_matvec_q_batched(moearc_ctx *c, unsigned int type_id, float *out, const void *const *w,
+                            unsigned int n_mat, const float *x, unsigned long x_stride,
+                            unsigned long n_rows, unsigned long n_cols) {
+    if (!c || !out || !w || !x) return ERR;
+    if (n_mat == 0 || n_rows == 0) return OK;
+    if (n_mat > MOEARC_MV_MAX_SEG) return ERR_ARG;
+    if (const int rc = mv_check(type_id, n_rows, n_cols)) return rc;
+    MvJob jobs[MOEARC_MV_MAX_SEG];
+    for (unsigned m = 0; m < n_mat; ++m) {
+        if (!w[m]) return ERR;
+        jobs[m] = MvJob{w[m], x + m * x_stride, nullptr, out + m * n_rows, n_rows};
+    }
+    return mv_launch(c, type_id, jobs, n_mat, n_cols, "mvq_batched", n_rows, n_mat);
+}
+
+int moearc_matvec_f32(moearc_ctx *c, float *out, const float *w, const float *x,
+                      unsigned long n_rows, unsigned long n_cols) {
+    if (!c || !out || !w || !x) return ERR;
+    if (n_rows == 0) return OK;
+    if (const int rc = mv_check(0, n_rows, n_cols)) return rc;
+    const MvJob j{w, x, nullptr, out, n_rows};
+    return mv_launch(c, 0, &j, 1, n_cols, "mvf32", n_rows, 1);
+}
+
+int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsigned long n) {
+    if (!c || !out || !a || !b) return ERR;
+    if (n == 0) return OK;
+    const unsigned grid = (unsigned) std::min<unsigned long>((n + 255) / 256, 65536ul);
+    struct {
+        float *o;
+        const float *a, *b;
+        uint64_t n;
+    } args{out, a, b, n};
+    return launch(c, c->f_add, grid, 256, args, "add", n, 0);
+}
+
+int moearc_attn_qkv(moearc_ctx *c, const unsigned int *type_ids, float *const *out,
+                    const void *const *w, const float *const *bias, const unsigned long *rows,
+                    const float *x, unsigned long n_cols) {
+    if (!c || !type_ids || !out || !w || !bias || !rows || !x) return ERR;
+    for (int i = 0; i < 3; ++i) {
+        if (rows[i] && (!out[i] || !w[i])) return ERR;
+        if (const int rc = mv_check(type_ids[i], rows[i], n_cols)) return rc;
+    }
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; ++i) {  // one launch per distinct weight type, in q, k, v order
+        if (done[i]) continue;
+        MvJob jobs[3];
+        unsigned n = 0;
+        for (int k = i; k < 3; ++k) {
+            if (done[k] || type_ids[k] != type_ids[i]) continue;
+            done[k] = true;
+            if (rows[k]) jobs[n++] = MvJob{w[k], x, bias[k], out[k], rows[k]};
+        }
+        if (n == 0) continue;
+        if (const int rc = mv_launch(c, type_ids[i], jobs, n, n_cols, "attn_qkv", n, 3)) return rc;
+    }
+    return OK;
 }
 
 int moearc_quantize_f16(moearc_ctx *c, void *dst, const float *src, unsigned long n) {

@@ -34,6 +34,12 @@ SIGNATURES = {
     "moearc_copy_h2d_async": (ctypes.c_int, [_vp, _vp, _vp, _c_ulong]),
     "moearc_copy_d2h": (ctypes.c_int, [_vp, _vp, _vp, _c_ulong]),
     "moearc_quantize_f16": (ctypes.c_int, [_vp, _vp, _vp, _c_ulong]),
+    "moearc_matvec_q": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _c_ulong, _c_ulong]),
+    "moearc_matvec_q_batched": (ctypes.c_int, [_vp, _u32, _vp, _vp, _u32, _vp, _c_ulong, _c_ulong,
+                                               _c_ulong]),
+    "moearc_matvec_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong, _c_ulong]),
+    "moearc_add": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong]),
+    "moearc_attn_qkv": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_ulong]),
     "moearc_kv_append": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _c_ulong, _c_ulong,
                                         _c_ulong, _u32]),
     "moearc_kv_append_chunk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_ulong,

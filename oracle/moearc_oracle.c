@@ -33,7 +33,12 @@
  *                                       identity; rotated pairs keep their length times mscale;
  *                                       YaRN's ramp endpoints (pure extrapolation below corr_lo,
  *                                       freq_scale-interpolated above corr_hi); YaRN off equals
- *                                       plain RoPE.
+ *                                       plain RoPE;
+ *   orc_dequant (all seven formats)  -- encoders written from the packing side of each format
+ *                                       round-trip through it (Q4_K/Q5_K/Q6_K bit layouts and
+ *                                       6-bit scale split); Q8_0 with d = 1 is its payload; MXFP4 is
+ *                                       the OCP E2M1 code points times 2^(e-127), every byte value;
+ *   orc_matvec_q                     -- numpy's float64 product of the decoded matrix.
  */
 #include <math.h>
 #include <stddef.h>
@@ -406,4 +411,185 @@ void orc_rope_kv_append_chunk(void *k_pages, void *v_pages, const float *k, cons
             orc_kv_append_raw(k_pages, v_pages, scratch_f, v + t * row, page_ids[t], slots[t],
                               n_kv_heads, head_dim, page_tokens, kv_type);
     }
+}
+
+/* ---- GGUF block formats and the matrix-vector product --------------------------------------
+ * Restating reference.rs:42-336, which itself restates ggml's dequantize_row_* (ggml-quants.c,
+ * a dependency of the reference not vendored in it). Values are expanded in f32 exactly as those
+ * functions compute them (each product and difference rounded to f32, no contraction -- the
+ * Makefile builds with -ffp-contract=off), then the products are accumulated in f64. */
+
+#define ORC_TY_F32 0u
+#define ORC_TY_F16 1u
+#define ORC_TY_Q8_0 8u
+#define ORC_TY_Q4_K 12u
+#define ORC_TY_Q5_K 13u
+#define ORC_TY_Q6_K 14u
+#define ORC_TY_MXFP4 39u
+
+/* Bytes and elements per block (reference.rs:79-104). 0 for an unknown type. */
+size_t orc_block_bytes(uint32_t ty) {
+    switch (ty) {
+        case ORC_TY_F32: return 4;
+        case ORC_TY_F16: return 2;
+        case ORC_TY_Q8_0: return 34;
+        case ORC_TY_Q4_K: return 144;
+        case ORC_TY_Q5_K: return 176;
+        case ORC_TY_Q6_K: return 210;
+        case ORC_TY_MXFP4: return 17;
+        default: return 0;
+    }
+}
+
+size_t orc_block_elems(uint32_t ty) {
+    switch (ty) {
+        case ORC_TY_F32: case ORC_TY_F16: return 1;
+        case ORC_TY_Q8_0: case ORC_TY_MXFP4: return 32;
+        case ORC_TY_Q4_K: case ORC_TY_Q5_K: case ORC_TY_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+static float ld_f16(const uint8_t *p) { return orc_f16_to_f32((uint16_t) (p[0] | (p[1] << 8))); }
+
+/* 2^(x - 128) (reference.rs:66-70): half the E8M0 value, to match the doubled E2M1 table. */
+float orc_e8m0_half(uint8_t x) {
+    const uint32_t bits = x < 2 ? 0x00200000u << x : ((uint32_t) x - 1u) << 23;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* The E2M1 code points doubled (reference.rs:52-55): magnitude codes 0..7 are 0, 0.5, 1, 1.5, 2,
+ * 3, 4, 6 in the OCP MX format; bit 3 is the sign. */
+static int mxfp4_doubled(unsigned code) {
+    static const int mag[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+    return (code & 8u) ? -mag[code & 7u] : mag[code & 7u];
+}
+
+/* Sub-block j's 6-bit scale and min from the 12 packed bytes (reference.rs:150-160). */
+static void scale_min_k4(const uint8_t *q, int j, unsigned *sc, unsigned *m) {
+    if (j < 4) {
+        *sc = q[j] & 63u;
+        *m = q[j + 4] & 63u;
+    } else {
+        *sc = (q[j + 4] & 0xFu) | ((unsigned) (q[j - 4] >> 6) << 4);
+        *m = (unsigned) (q[j + 4] >> 4) | ((unsigned) (q[j] >> 6) << 4);
+    }
+}
+
+static void dq_block(uint32_t ty, const uint8_t *b, float *y) {
+    switch (ty) {
+        case ORC_TY_F32: memcpy(y, b, 4); break;
+        case ORC_TY_F16: y[0] = ld_f16(b); break;
+        case ORC_TY_Q8_0: { /* reference.rs:194-200: y = q * d */
+            const float d = ld_f16(b);
+            for (int j = 0; j < 32; ++j) y[j] = (float) (int8_t) b[2 + j] * d;
+            break;
+        }
+        case ORC_TY_MXFP4: { /* reference.rs:202-217: byte j -> elements j (low), j + 16 (high) */
+            const float d = orc_e8m0_half(b[0]);
+            for (int j = 0; j < 16; ++j) {
+                y[j] = (float) mxfp4_doubled(b[1 + j] & 0xFu) * d;
+                y[j + 16] = (float) mxfp4_doubled(b[1 + j] >> 4) * d;
+            }
+            break;
+        }
+        case ORC_TY_Q4_K: { /* reference.rs:219-244 */
+            const float d = ld_f16(b), dmin = ld_f16(b + 2);
+            const uint8_t *sc = b + 4, *qs = b + 16;
+            for (int g = 0; g < 4; ++g) {  /* 64 elements: low nibbles, then high, of 32 bytes */
+                unsigned s0, m0, s1, m1;
+                scale_min_k4(sc, 2 * g, &s0, &m0);
+                scale_min_k4(sc, 2 * g + 1, &s1, &m1);
+                const float d0 = d * (float) s0, n0 = dmin * (float) m0;
+                const float d1 = d * (float) s1, n1 = dmin * (float) m1;
+                for (int l = 0; l < 32; ++l) {
+                    const float lo = d0 * (float) (qs[32 * g + l] & 0xF);
+                    const float hi = d1 * (float) (qs[32 * g + l] >> 4);
+                    y[64 * g + l] = lo - n0;
+                    y[64 * g + 32 + l] = hi - n1;
+                }
+            }
+            break;
+        }
+        case ORC_TY_Q5_K: { /* reference.rs:246-277: fifth bits in qh, bit 2g (low) / 2g+1 (high) */
+            const float d = ld_f16(b), dmin = ld_f16(b + 2);
+            const uint8_t *sc = b + 4, *qh = b + 16, *qs = b + 48;
+            for (int g = 0; g < 4; ++g) {
+                unsigned s0, m0, s1, m1;
+                scale_min_k4(sc, 2 * g, &s0, &m0);
+                scale_min_k4(sc, 2 * g + 1, &s1, &m1);
+                const float d0 = d * (float) s0, n0 = dmin * (float) m0;
+                const float d1 = d * (float) s1, n1 = dmin * (float) m1;
+                for (int l = 0; l < 32; ++l) {
+                    const unsigned ql = qs[32 * g + l];
+                    const unsigned q0 = (ql & 0xFu) + ((qh[l] >> (2 * g)) & 1u) * 16u;
+                    const unsigned q1 = (ql >> 4) + ((qh[l] >> (2 * g + 1)) & 1u) * 16u;
+                    const float lo = d0 * (float) q0, hi = d1 * (float) q1;
+                    y[64 * g + l] = lo - n0;
+                    y[64 * g + 32 + l] = hi - n1;
+                }
+            }
+            break;
+        }
+        case ORC_TY_Q6_K: { /* reference.rs:279-303 */
+            const float d = ld_f16(b + 208);
+            for (int n = 0; n < 2; ++n) {
+                const uint8_t *ql = b + 64 * n, *qh = b + 128 + 32 * n;
+                const int8_t *sc = (const int8_t *) (b + 192 + 8 * n);
+                for (int l = 0; l < 32; ++l) {
+                    const int is = l / 16;
+                    const int q[4] = {
+                        (int) ((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32,
+                        (int) ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32,
+                        (int) ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32,
+                        (int) ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32};
+                    for (int c = 0; c < 4; ++c) {
+                        const float ds = d * (float) sc[is + 2 * c];
+                        y[128 * n + 32 * c + l] = ds * (float) q[c];
+                    }
+                }
+            }
+            break;
+        }
+    }
+}
+
+/* Expand nblocks blocks (reference.rs:168-192). -2 for an unknown type. */
+int orc_dequant(uint32_t ty, const uint8_t *src, size_t nblocks, float *dst) {
+    const size_t bb = orc_block_bytes(ty), be = orc_block_elems(ty);
+    if (!bb) return -2;
+    for (size_t i = 0; i < nblocks; ++i) dq_block(ty, src + i * bb, dst + i * be);
+    return 0;
+}
+
+/* out[r] = sum_c W[r][c] x[c], W dequantised to f32 then accumulated in f64 (reference.rs:305-336).
+ * absum (nullable) receives sum_c |W[r][c] x[c]| per row, the scale of the reference tests'
+ * tolerance (kernels_gpu.rs:126-137). -2 for an unknown type or a ragged row. */
+int orc_matvec_q(uint32_t ty, const uint8_t *w, const float *x, size_t n_rows, size_t n_cols,
+                 float *out, double *absum, int n_threads) {
+    const size_t bb = orc_block_bytes(ty), be = orc_block_elems(ty);
+    if (!bb || n_cols % be) return -2;
+    const size_t nb = n_cols / be;
+    int rc = 0;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(n_threads > 0 ? n_threads : 1) schedule(static)
+#endif
+    for (size_t r = 0; r < n_rows; ++r) {
+        float row[256];
+        double acc = 0.0, mag = 0.0;
+        for (size_t i = 0; i < nb; ++i) {
+            dq_block(ty, w + (r * nb + i) * bb, row);
+            for (size_t j = 0; j < be; ++j) {
+                const double p = (double) row[j] * (double) x[i * be + j];
+                acc += p;
+                mag += fabs(p);
+            }
+        }
+        out[r] = (float) acc;
+        if (absum) absum[r] = mag;
+    }
+    (void) n_threads;
+    return rc;
 }

@@ -84,6 +84,17 @@ def lib():
         L.orc_rope_kv_append_chunk.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _f32p, _f32p, _i32p,
                                                _u32p, _u32p, _sz, _sz, _sz, _sz, _sz, _f, _f, _f, _f,
                                                _f, _f, ctypes.c_int, ctypes.c_uint32, _f64p, _f32p]
+        L.orc_block_bytes.argtypes = [ctypes.c_uint32]
+        L.orc_block_bytes.restype = _sz
+        L.orc_block_elems.argtypes = [ctypes.c_uint32]
+        L.orc_block_elems.restype = _sz
+        L.orc_e8m0_half.argtypes = [ctypes.c_uint8]
+        L.orc_e8m0_half.restype = ctypes.c_float
+        L.orc_dequant.argtypes = [ctypes.c_uint32, ctypes.c_void_p, _sz, _f32p]
+        L.orc_dequant.restype = ctypes.c_int
+        L.orc_matvec_q.argtypes = [ctypes.c_uint32, ctypes.c_void_p, _f32p, _sz, _sz, _f32p, _f64p,
+                                   ctypes.c_int]
+        L.orc_matvec_q.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -276,3 +287,46 @@ def rope_kv_append_chunk(k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, n_
                                    _p(pos, _i32p), _p(pg, _u32p), _p(sl, _u32p), n_tok, n_kv_heads,
                                    head_dim, page_tokens, n_dims, _f(freq_base), _f(fs), _f(ext), _f(att),
                                    _f(clo), _f(chi), int(bool(neox)), kv_type, _p(sd, _f64p), _p(sf, _f32p))
+
+
+# ---- GGUF block formats and matvec (crates/moearc-kernels/src/reference.rs:42-336) ---------------
+
+def block_bytes(ty: int) -> int:
+    return int(lib().orc_block_bytes(ty))
+
+
+def block_elems(ty: int) -> int:
+    return int(lib().orc_block_elems(ty))
+
+
+def e8m0_half(x: int) -> float:
+    """2^(x - 128) as reference.rs:66-70 builds it (subnormal below x = 2)."""
+    return float(lib().orc_e8m0_half(x))
+
+
+def dequant(ty: int, src, nblocks: int) -> np.ndarray:
+    """Expand nblocks blocks to f32 (reference.rs:168-192)."""
+    src = np.ascontiguousarray(np.frombuffer(bytes(src), np.uint8) if not isinstance(src, np.ndarray)
+                               else src.view(np.uint8).reshape(-1))
+    if src.size < nblocks * block_bytes(ty):
+        raise OracleRefusal(f"{nblocks} blocks need {nblocks * block_bytes(ty)} bytes, got {src.size}")
+    out = np.zeros(nblocks * max(block_elems(ty), 1), np.float32)
+    if lib().orc_dequant(ty, src.ctypes.data, nblocks, _p(out, _f32p)):
+        raise OracleRefusal(f"unknown type {ty}")
+    return out
+
+
+def matvec_q(ty: int, w, x, n_rows: int, n_cols: int, n_threads: int = 8):
+    """(out f32 [n_rows], absum f64 [n_rows]) with out[r] = W[r] . x accumulated in f64 over the
+    f32-dequantised row (reference.rs:305-321) and absum[r] = sum |W[r][c] x[c]|."""
+    w = np.ascontiguousarray(np.asarray(w).view(np.uint8).reshape(-1))
+    x = np.ascontiguousarray(x, np.float32)
+    assert x.size >= n_cols
+    if n_cols % max(block_elems(ty), 1) or not block_bytes(ty):
+        raise OracleRefusal(f"type {ty}: {n_cols} columns")
+    assert w.size >= n_rows * n_cols // block_elems(ty) * block_bytes(ty)
+    out = np.zeros(n_rows, np.float32)
+    absum = np.zeros(n_rows, np.float64)
+    lib().orc_matvec_q(ty, w.ctypes.data, _p(x, _f32p), n_rows, n_cols, _p(out, _f32p),
+                       _p(absum, _f64p), n_threads)
+    return out, absum

@@ -261,3 +261,55 @@ def rope_complex(src, pos, n_tokens, n_heads, head_dim, n_dims, freq_base, scali
         z = z * rot
         x[..., 0:n_dims:2], x[..., 1:n_dims:2] = z.real, z.imag
     return x.reshape(-1)
+
+
+# ---- quantised weights (crates/moearc-kernels/tests/common/mod.rs:45-84) ---------------------
+
+QT_BLOCK = {0: (4, 1), 1: (2, 1), 8: (34, 32), 12: (144, 256), 13: (176, 256), 14: (210, 256),
+            39: (17, 32)}  # type id -> (block bytes, block elements)
+
+
+def synth_blocks(ty: int, nblocks: int, seed: int):
+    """The reference tests' ``synth_blocks(ty, nblocks, &mut Rng::new(seed))`` followed by
+    ``rng.vec_unit`` -- returns (blocks as uint8, draws consumed) so the caller can continue the
+    stream. Random payload bytes (low byte of each draw), then per block the constrained fields:
+    f16 scales 0x1000 + u32 % 0x1800 (Q8_0: d; Q4_K/Q5_K: d, dmin; Q6_K: d at byte 208), an E8M0
+    exponent 100 + u32 % 56 (MXFP4), a unit value (F32) or its f16 (F16)."""
+    bb, _ = QT_BLOCK[ty]
+    n = nblocks * bb
+    v = (synth.splitmix64(seed, n) & np.uint64(0xFF)).astype(np.uint8).reshape(nblocks, bb)
+    per = {8: 1, 12: 2, 13: 2, 14: 1, 39: 1, 0: 1, 1: 1}[ty]
+    draws = synth.splitmix64(seed, nblocks * per, n).reshape(nblocks, per)
+    lo32 = draws & np.uint64(0xFFFFFFFF)
+
+    def scale(col):
+        return (np.uint64(0x1000) + lo32[:, col] % np.uint64(0x1800)).astype(np.uint16)
+
+    if ty in (8, 12, 13):
+        v[:, 0:2] = scale(0).view(np.uint8).reshape(nblocks, 2)
+        if ty != 8:
+            v[:, 2:4] = scale(1).view(np.uint8).reshape(nblocks, 2)
+    elif ty == 14:
+        v[:, 208:210] = scale(0).view(np.uint8).reshape(nblocks, 2)
+    elif ty == 39:
+        v[:, 0] = (np.uint64(100) + lo32[:, 0] % np.uint64(56)).astype(np.uint8)
+    else:
+        u = synth.unit(seed, nblocks, n)
+        if ty == 0:
+            v[:, :] = u.view(np.uint8).reshape(nblocks, 4)
+        else:
+            v[:, :] = synth.f16_bits(u).view(np.uint8).reshape(nblocks, 2)
+    return v.reshape(-1), n + nblocks * per
+
+
+def matvec_case(ty: int, rows: int, cols: int, seed: int):
+    """(w bytes, x f32) drawn as the reference's matvec tests draw them (kernels_gpu.rs:110-116)."""
+    be = QT_BLOCK[ty][1]
+    w, used = synth_blocks(ty, rows * cols // be, seed)
+    x = synth.unit(seed, cols, used)
+    return w, x
+
+
+def matvec_tolerance(cols: int, absum: np.ndarray) -> np.ndarray:
+    """The reference's bound (kernels_gpu.rs:126-137): 2 (cols/32 + 5) u sum|w x| per row."""
+    return 2.0 * (cols / 32.0 + 5.0) * 2.0 ** -24 * absum

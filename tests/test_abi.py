@@ -31,7 +31,8 @@ def test_header_declares_the_reference_surface():
               "moearc_profile_events_reset", "moearc_profile_events_report", "moearc_sync",
               "moearc_zero", "moearc_device_name", "moearc_alloc_device", "moearc_free_device",
               "moearc_copy_h2d", "moearc_copy_h2d_async", "moearc_copy_d2h",
-              "moearc_quantize_f16", "moearc_kv_append", "moearc_attn_decode"):
+              "moearc_quantize_f16", "moearc_kv_append", "moearc_attn_decode", "moearc_matvec_q",
+              "moearc_matvec_q_batched", "moearc_matvec_f32", "moearc_add"):
         assert n in names
 
 
@@ -47,6 +48,8 @@ def test_code_object_holds_every_kernel_the_runtime_loads():
     src = open(os.path.join(ROOT, "moearc_amd", "csrc", "runtime.cpp")).read()
     kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge)"', src))
     kernels |= {f"moearc_attn_prefill_{v}g{g}" for v in ("", "precise_") for g in (1, 2, 4, 8)}
+    kernels |= {f"moearc_matvec_{t}_p{p}" for t in ("f32", "f16", "q4_k", "q5_k", "mxfp4") for p in (1, 2, 4)}
+    kernels |= {f"moearc_matvec_{t}_p{p}" for t in ("q8_0", "q6_k") for p in (1, 2, 4, 8)}
     assert kernels
     for k in kernels:
         assert k.encode() in blob, f"kernel {k} missing from the code object"
@@ -72,6 +75,11 @@ def test_null_context_is_refused_with_minus_one():
     assert lib.moearc_alloc_device(None, 16) is None
     assert lib.moearc_copy_h2d(None, None, None, 0) == -1
     assert lib.moearc_quantize_f16(None, None, None, 4) == -1
+    assert lib.moearc_matvec_q(None, 8, None, None, None, 4, 32) == -1
+    assert lib.moearc_matvec_q_batched(None, 8, None, None, 1, None, 0, 4, 32) == -1
+    assert lib.moearc_matvec_f32(None, None, None, None, 4, 4) == -1
+    assert lib.moearc_add(None, None, None, None, 4) == -1
+    assert lib.moearc_attn_qkv(None, None, None, None, None, None, None, 32) == -1
 
 
 def test_missing_build_fails_loudly(monkeypatch):

@@ -1,0 +1,205 @@
+"""Quantised matvec, batched matvec, the fused q/k/v projections and the bias add on the GPU,
+through the C ABI, against the oracle (reference.rs:305-336 restated, pinned in
+test_matvec_oracle.py).
+
+Bar: the reference's own (kernels_gpu.rs:126-137): per row |gpu - oracle| <= 2 (cols/32 + 5) u
+sum|w x|, u = 2^-24. Batched and fused launches are held to bit-identity with the single calls
+they replace, as the reference holds its batched matvec (kernels_gpu.rs:483-533).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import fixtures as fx
+from moearc_amd import BadArgument, DeviceView, QuantType
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+ALL = [QuantType.F32, QuantType.F16, QuantType.Q8_0, QuantType.Q4_K, QuantType.Q5_K,
+       QuantType.Q6_K, QuantType.MXFP4]
+
+
+def _run(ctx, ty, w, x, rows, cols, w_offset=0):
+    buf = ctx.alloc(w.nbytes + w_offset + 64)
+    wv = DeviceView(buf, w_offset, w.nbytes)
+    ctx.upload_slice(wv, w)
+    dx = ctx.upload(x)
+    out = ctx.alloc(max(rows, 1) * 4)
+    ctx.matvec_q(ty, out, wv, dx, rows, cols)
+    return ctx.download(out, np.float32, rows)
+
+
+def _check(label, got, ty, w, x, rows, cols):
+    want, absum = oracle.matvec_q(int(ty), w, x, rows, cols, n_threads=16)
+    tol = fx.matvec_tolerance(cols, absum)
+    fin = np.isfinite(want)
+    err = np.abs(got.astype(np.float64) - want)
+    worst = float(np.max(np.where(fin, err / np.maximum(tol, 1e-300), 0.0))) if fin.any() else 0.0
+    print(f"{label}: worst |gpu - oracle| / bound = {worst:.3f}", flush=True)
+    assert np.all(err[fin] <= tol[fin]), f"{label}: over the bound"
+    bad = ~fin
+    if bad.any():  # rows the reference overflows: the same infinities / NaNs
+        assert np.array_equal(np.isnan(got[bad]), np.isnan(want[bad]))
+        assert np.array_equal(got[bad & ~np.isnan(want)], want[bad & ~np.isnan(want)])
+    return want
+
+
+@pytest.mark.parametrize("ty", ALL, ids=lambda t: t.name)
+def test_matvec_matches_the_oracle_for_every_type(ctx, ty):
+    # 37 rows x 1024 columns, drawn as kernels_gpu.rs:99-140 draws them
+    rows, cols = 37, 1024
+    w, x = fx.matvec_case(int(ty), rows, cols, 0x5EED ^ int(ty))
+    want = _check(f"matvec {ty.name} {rows}x{cols}", _run(ctx, ty, w, x, rows, cols), ty, w, x, rows, cols)
+    assert np.any(want != 0)
+
+
+def test_f32_matvec_33x700(ctx):
+    # kernels_gpu.rs:143-172: 700 columns, not a multiple of the 8-float piece
+    rows, cols = 33, 700
+    w, x = fx.matvec_case(0, rows, cols, 0x000A11CE)
+    dw, dx, out = ctx.upload(w), ctx.upload(x), ctx.alloc(rows * 4)
+    ctx.matvec_f32(out, dw, dx, rows, cols)
+    _check("matvec_f32 33x700", ctx.download(out, np.float32, rows), QuantType.F32, w, x, rows, cols)
+
+
+@pytest.mark.parametrize("ty,rows,cols", [
+    (QuantType.Q8_0, 4096, 2880), (QuantType.Q8_0, 2880, 4096), (QuantType.F16, 4096, 2880),
+    (QuantType.MXFP4, 4096, 2880), (QuantType.Q4_K, 4096, 2048), (QuantType.Q5_K, 512, 2048),
+    (QuantType.Q6_K, 512, 2048), (QuantType.Q6_K, 2048, 4096)], ids=str)
+def test_projection_shapes(ctx, ty, rows, cols):
+    # gpt-oss attention (64 x 64 query, 8 x 64 KV, 2880 embedding) and Qwen3-30B-A3B (4096 / 2048)
+    w, x = fx.matvec_case(int(ty), rows, cols, 0x7A11 + rows + int(ty))
+    _check(f"matvec {ty.name} {rows}x{cols}", _run(ctx, ty, w, x, rows, cols), ty, w, x, rows, cols)
+
+
+@pytest.mark.parametrize("ty,cols,offset", [
+    (QuantType.Q8_0, 1024, 1), (QuantType.Q8_0, 2880, 2), (QuantType.Q6_K, 1024, 3),
+    (QuantType.Q4_K, 512, 13), (QuantType.MXFP4, 1024, 5), (QuantType.F16, 1001, 7),
+    (QuantType.F32, 7, 9), (QuantType.F16, 3, 1)], ids=str)
+def test_any_weight_alignment_and_ragged_float_rows(ctx, ty, cols, offset):
+    rows = 19
+    w, x = fx.matvec_case(int(ty), rows, cols, 0xA1 + offset)
+    _check(f"matvec {ty.name} cols={cols} +{offset}B", _run(ctx, ty, w, x, rows, cols, offset), ty, w, x,
+           rows, cols)
+
+
+@pytest.mark.parametrize("ty,cols", [(QuantType.Q8_0, 12288), (QuantType.F32, 5000),
+                                     (QuantType.F16, 4100), (QuantType.Q4_K, 16384),
+                                     (QuantType.MXFP4, 9216)], ids=str)
+def test_rows_longer_than_one_slab(ctx, ty, cols):
+    # more pieces than one pass of a wave holds: the row is walked in column slabs (and the widest
+    # read their activation from global memory instead of LDS)
+    rows = 45
+    w, x = fx.matvec_case(int(ty), rows, cols, 0x51AB + cols)
+    _check(f"matvec {ty.name} 45x{cols}", _run(ctx, ty, w, x, rows, cols), ty, w, x, rows, cols)
+
+
+def test_mxfp4_extreme_exponents(ctx):
+    # E8M0 0 and 1 give subnormal scales; from 253 up the reference's per-element products
+    # overflow f32, and the kernel must overflow the same way
+    rows, cols = 8, 256
+    w, x = fx.matvec_case(39, rows, cols, 0xE8E0)
+    blocks = w.reshape(-1, 17)
+    blocks[:, 0] = np.array([0, 1, 2, 252, 253, 254, 255, 127], np.uint8)[np.arange(blocks.shape[0]) % 8]
+    _check("matvec MXFP4 extreme exponents", _run(ctx, QuantType.MXFP4, w, x, rows, cols),
+           QuantType.MXFP4, w, x, rows, cols)
+
+
+@pytest.mark.parametrize("ty", [QuantType.Q8_0, QuantType.Q4_K, QuantType.Q5_K, QuantType.Q6_K],
+                         ids=lambda t: t.name)
+def test_batched_is_bit_identical_to_single_calls(ctx, ty):
+    # kernels_gpu.rs:494-533
+    rows, cols, mats = 37, 1024, 5
+    x = fx.synth.unit(0x0BA7C4ED ^ int(ty), cols)
+    dx = ctx.upload(x)
+    ws, want = [], []
+    for m in range(mats):
+        w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0xB0 + 7 * m + int(ty))
+        dw = ctx.upload(w)
+        one = ctx.alloc(rows * 4)
+        ctx.matvec_q(ty, one, dw, dx, rows, cols)
+        want.append(ctx.download(one, np.float32, rows))
+        ws.append(dw)
+    out = ctx.alloc(mats * rows * 4)
+    ctx.matvec_q_batched(ty, out, ws, dx, 0, rows, cols)
+    got = ctx.download(out, np.float32, mats * rows)
+    assert np.array_equal(got, np.concatenate(want)), "batching changed the answer"
+    assert np.any(got != 0)
+
+
+def test_batched_strided_activation(ctx):
+    # kernels_gpu.rs:536-577: matrix m reads x + m * cols
+    ty, rows, cols, mats = QuantType.Q4_K, 20, 512, 4
+    xs = fx.synth.unit(0x05731DED, mats * cols)
+    dxs = ctx.upload(xs)
+    ws, want = [], []
+    for m in range(mats):
+        w, _ = fx.synth_blocks(int(ty), rows * cols // 256, 0x5700 + m)
+        ws.append(ctx.upload(w))
+        want.append(_run(ctx, ty, w, xs[m * cols:(m + 1) * cols], rows, cols))
+    out = ctx.alloc(mats * rows * 4)
+    ctx.matvec_q_batched(ty, out, ws, dxs, cols, rows, cols)
+    assert np.array_equal(ctx.download(out, np.float32, mats * rows), np.concatenate(want))
+
+
+def test_batched_refusals(ctx):
+    # kernels_gpu.rs:580-593: more matrices than one launch carries is refused, not truncated
+    ty, cols = QuantType.Q4_K, 256
+    dw, dx, out = ctx.alloc(144), ctx.alloc(cols * 4), ctx.alloc(33 * 4)
+    with pytest.raises(BadArgument):
+        ctx.matvec_q_batched(ty, out, [dw] * 33, dx, 0, 1, cols)
+    ctx.matvec_q_batched(ty, out, [], dx, 0, 1, cols)  # nothing to do
+    ctx.sync()
+
+
+@pytest.mark.parametrize("types", [(8, 8, 8), (12, 12, 14), (39, 1, 8)], ids=str)
+def test_attn_qkv_is_bit_identical_to_matvec_then_add(ctx, types):
+    # moe.rs:1942-1959: three matvecs, then the biases added in place
+    cols = 2048
+    rows = (512, 128, 128)
+    x = fx.synth.unit(0x9C5, cols)
+    dx = ctx.upload(x)
+    outs, ws, biases, want = [], [], [], []
+    for i, (t, r) in enumerate(zip(types, rows)):
+        w, _ = fx.synth_blocks(t, r * cols // fx.QT_BLOCK[t][1], 0x9C50 + i)
+        dw = ctx.upload(w)
+        b = ctx.upload(fx.synth.unit(0x9C60 + i, r)) if i != 1 else None  # k without a bias
+        one = ctx.alloc(r * 4)
+        ctx.matvec_q(t, one, dw, dx, r, cols)
+        if b is not None:
+            ctx.add(one, one, b, r)
+        want.append(ctx.download(one, np.float32, r))
+        outs.append(ctx.alloc(r * 4))
+        ws.append(dw)
+        biases.append(b)
+    ctx.attn_qkv(types, outs, ws, biases, rows, dx, cols)
+    for i, r in enumerate(rows):
+        assert np.array_equal(ctx.download(outs[i], np.float32, r), want[i]), f"projection {i}"
+
+
+def test_add_is_exact_and_may_alias(ctx):
+    n = 10000
+    a, b = fx.synth.unit(1, n), fx.synth.unit(2, n)
+    da, db, out = ctx.upload(a), ctx.upload(b), ctx.alloc(n * 4)
+    ctx.add(out, da, db, n)
+    assert np.array_equal(ctx.download(out, np.float32, n), a + b)
+    ctx.add(da, da, db, n)  # out aliasing the left operand, as the engine calls it
+    assert np.array_equal(ctx.download(da, np.float32, n), a + b)
+
+
+def test_matvec_refusals_and_empty_shapes(ctx):
+    dw, dx, out = ctx.alloc(1 << 16), ctx.alloc(4096), ctx.alloc(256)
+    lib = ctx._lib
+    assert lib.moearc_matvec_q(ctx.raw, 12, out.ptr, dw.ptr, dx.ptr, 4, 300) == -2  # ragged Q4_K
+    assert lib.moearc_matvec_q(ctx.raw, 2, out.ptr, dw.ptr, dx.ptr, 4, 256) == -2   # Q4_0: unknown
+    assert lib.moearc_matvec_q(ctx.raw, 8, None, dw.ptr, dx.ptr, 4, 256) == -1
+    assert lib.moearc_matvec_q(ctx.raw, 8, out.ptr, dw.ptr, dx.ptr, 0, 256) == 0   # no rows
+    with pytest.raises(BadArgument):
+        ctx.matvec_q(QuantType.Q4_K, out, dw, dx, 4, 300)
+    # zero columns: every row's sum is empty
+    ctx.upload_slice(out, np.full(8, 7.0, np.float32))
+    ctx.matvec_q(QuantType.Q8_0, out, dw, dx, 8, 0)
+    assert np.array_equal(ctx.download(out, np.float32, 8), np.zeros(8, np.float32))
+    ctx.sync()
