@@ -171,6 +171,8 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
         result["step_us_wall"] = wall_ms * 1e3 / steps
         result["graph_equals_eager"] = bool(np.array_equal(graph_out, eager_out))
         result["out"] = graph_out
+        del dks, dvs
+        result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
 
     # per-kernel event timing (eager, profiling context)
     os.environ["MOEARC_PROFILE_EVENTS"] = "1"
@@ -282,6 +284,79 @@ def bench_rope_append(ctx, steps, warmup):
     gbs = RA_BYTES / us / 1e3
     return {"us": round(us, 2), "bytes": RA_BYTES, "hbm_gbs": round(gbs, 0),
             "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+# The attention projections either side of the path, at gpt-oss-20b's shapes (2880-wide residual,
+# 64 x 64 query, 8 x 64 KV; moe.rs:1942-1959 and 2063-2071) and Qwen3-30B-A3B's q (4096 x 2048):
+# (label, type id, rows of q / k / v or of the single matrix, columns, fused qkv with biases?)
+MV_CASES = [
+    ("attn.qkv Q8_0 gpt-oss (4096+512+512)x2880 +bias", 8, (4096, 512, 512), 2880, True),
+    ("attn.proj Q8_0 gpt-oss 2880x4096", 8, (2880,), 4096, False),
+    ("attn.qkv F16 gpt-oss (4096+512+512)x2880 +bias", 1, (4096, 512, 512), 2880, True),
+    ("attn.qkv MXFP4 gpt-oss (4096+512+512)x2880 +bias", 39, (4096, 512, 512), 2880, True),
+    ("attn_q Q4_K qwen3-30b 4096x2048", 12, (4096,), 2048, False),
+]
+
+
+def mv_inputs(ctx, ty, rows, cols, fused, copies):
+    """Weight copies enough to stream from HBM (each launch reads a different copy, and all of
+    them together exceed the 256 MB Infinity Cache), one activation, biases and outputs."""
+    from moearc_amd import QuantType
+    qt = QuantType(ty)
+    rng = np.random.default_rng(0x3A7 + ty)
+    x = rng.standard_normal(cols).astype(np.float32)
+    mats = []
+    for r in rows:
+        nbytes = r * qt.row_bytes(cols)
+        w = rng.integers(0, 256, nbytes, dtype=np.uint8)
+        if ty in (0, 1):  # finite values, not random bit patterns
+            w = (rng.standard_normal(nbytes // qt.block_bytes).astype(np.float32 if ty == 0 else np.float16)
+                 .view(np.uint8))
+        mats.append(w)
+    per_copy = sum(m.nbytes for m in mats)
+    n = max(2, min(copies, (400 << 20) // per_copy + 1))
+    dws = [[ctx.upload(m) for m in mats] for _ in range(n)]
+    biases = [ctx.upload(rng.standard_normal(r).astype(np.float32)) if fused else None for r in rows]
+    outs = [ctx.alloc(r * 4) for r in rows]
+    return ctx.upload(x), dws, biases, outs, per_copy
+
+
+def mv_launch(ctx, ty, rows, cols, fused, inputs, i):
+    dx, dws, biases, outs, _ = inputs
+    ws = dws[i % len(dws)]
+    if fused:
+        ctx.attn_qkv([ty] * 3, outs, ws, biases, rows, dx, cols)
+    else:
+        ctx.matvec_q(ty, outs[0], ws[0], dx, rows[0], cols)
+
+
+def bench_matvec(ctx, hip, steps):
+    """Each projection case as a captured graph of `steps` launches (each on the next weight copy),
+    replayed once untimed and once between HIP events: the per-launch time excludes host
+    submission, which for kernels this short would otherwise dominate. Achieved bandwidth counts
+    the algorithmic bytes (every weight byte once, the activation, biases and outputs)."""
+    res = {}
+    for label, ty, rows, cols, fused in MV_CASES:
+        inputs = mv_inputs(ctx, ty, rows, cols, fused, 128)
+        mv_launch(ctx, ty, rows, cols, fused, inputs, 0)
+        ctx.sync()
+        graph, exe = hip.capture(ctx.stream, lambda: [mv_launch(ctx, ty, rows, cols, fused, inputs, i)
+                                                      for i in range(steps)])
+        e0, e1 = hip.event(), hip.event()
+        hip.launch(exe, ctx.stream)
+        ctx.sync()
+        hip.record(e0, ctx.stream)
+        hip.launch(exe, ctx.stream)
+        hip.record(e1, ctx.stream)
+        ctx.sync()
+        us = hip.elapsed_ms(e0, e1) * 1e3 / steps
+        hip.destroy(graph, exe)
+        nbytes = inputs[4] + cols * 4 + sum(rows) * 4 * (2 if fused else 1)
+        gbs = nbytes / us / 1e3
+        res[label] = {"us": round(us, 2), "bytes": nbytes, "hbm_gbs": round(gbs, 0),
+                      "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del inputs
+    return res
 
 
 def cpu_baseline(kp, vp, bt, q, sinks):
@@ -413,7 +488,7 @@ def bench_configs(steps, warmup):
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
     decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
-    C4 chunk), or copy (a 256 MiB device-to-device copy, the
+    C4 chunk), matvec (the projection cases of MV_CASES, in order), or copy (a 256 MiB device-to-device copy, the
     reference size for scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
     from moearc_amd import Context, KvType, OUT_F16
     with Context() as ctx:
@@ -441,6 +516,13 @@ def only(what, steps, warmup):
             sets, meta = rope_append_inputs(ctx, 24)
             for i in range(warmup + steps):
                 rope_append_launch(ctx, sets, meta, i)
+        elif what == "matvec":
+            for label, ty, rows, cols, fused in MV_CASES:
+                inputs = mv_inputs(ctx, ty, rows, cols, fused, 128)
+                for i in range(warmup + steps):
+                    mv_launch(ctx, ty, rows, cols, fused, inputs, i)
+                ctx.sync()
+                del inputs
         elif what == "copy":
             hip = Hip()
             n = 256 << 20
@@ -461,7 +543,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "copy"],
+    ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "matvec", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
@@ -529,6 +611,8 @@ def main():
     }
     if "prefill" in r:
         line["prefill"] = r["prefill"]
+    if "projections" in r:
+        line["projections"] = r["projections"]
     if "cpu" in r:
         c = r["cpu"]
         line["cpu_baseline"] = {

@@ -137,22 +137,24 @@ constexpr uint32_t moearc_mv_be(uint32_t ty) {
 constexpr uint32_t moearc_mv_pe(uint32_t ty) {
     return ty == 0 ? 8u : ty == 12 || ty == 13 || ty == 39 ? 32u : 16u;
 }
-// Largest pieces per lane per pass: activation registers (PPL * PE) stay at or under 128 and a
-// slab's staging buffer at or under 10 KiB.
-constexpr uint32_t moearc_mv_ppl_max(uint32_t ty) {
-    return ty == 8 || ty == 14 ? 8u : 4u;
+// Largest pieces per lane per pass: activation registers (PPL * PE) stay at or under 128, so a
+// wave keeps at least three waves per SIMD of occupancy.
+constexpr uint32_t moearc_mv_ppl_max(uint32_t) {
+    return 4u;
 }
 // 16-byte granules one lane stages per slab (a slab of 64 * PPL pieces, any byte alignment).
 constexpr uint32_t moearc_mv_gmax(uint32_t ty, uint32_t ppl) {
     return (uint32_t) ((64ull * ppl * moearc_mv_pe(ty) * moearc_mv_bb(ty) / moearc_mv_be(ty) + 30u + 1023u) / 1024u);
 }
-// Bytes of one wave's staging buffer: the granules plus slack for reads that run past a piece.
-constexpr uint32_t moearc_mv_wave_buf(uint32_t ty, uint32_t ppl) {
-    return moearc_mv_gmax(ty, ppl) * 1024u + 64u;
+// Bytes of one wave's staging buffer for slabs of `slab_bytes`: the granules a slab at any
+// alignment spans, plus slack for reads that run past a piece.
+constexpr uint32_t moearc_mv_wave_buf(uint64_t slab_bytes) {
+    return (uint32_t) (((slab_bytes + 30u + 15u) / 16u) * 16u + 64u);
 }
 
 // Segment s covers work-groups [wg_end[s-1], wg_end[s]) and rows [0, rows[s]) of matrix w[s]:
-// out[s][r] = sum_c W_s[r][c] * x[s][c] (+ bias[s][r] when bias[s] is non-null).
+// out[s][r] = sum_c W_s[r][c] * x[s][c] (+ bias[s][r] when bit s of bias_mask is set; bias[s]
+// then points at the bias, else at any readable rows[s] floats).
 struct MatvecArgs {
     const uint8_t *w[MOEARC_MV_MAX_SEG];
     const float *x[MOEARC_MV_MAX_SEG];
@@ -168,4 +170,6 @@ struct MatvecArgs {
     uint32_t rpw;          // consecutive rows per wave
     uint32_t x_in_lds;     // 1: the activation is staged once per work-group in LDS
     uint32_t x_lds_bytes;  // LDS bytes before the waves' staging buffers
+    uint32_t wave_buf;     // LDS bytes of one wave's staging buffer
+    uint32_t bias_mask;
 };

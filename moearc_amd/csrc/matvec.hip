@@ -258,6 +258,25 @@ template <> struct Fmt<39> {
 
 constexpr bool needs_xsum(uint32_t ty) { return ty == 12 || ty == 13 || ty == 14; }
 
+// v + the DPP-moved v (lanes the row mask leaves out add 0).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false);
+    return v + __int_as_float(moved);
+}
+
+// Sum over the 64 lanes, complete in lane 63: quad swaps, half-row and row mirrors (each lane of a
+// 16-lane row then holds the row's sum), then row 0 -> 1 and 2 -> 3 (row_bcast:15) and row 1 ->
+// 2, 3 (row_bcast:31).
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v = dpp_add<0xB1>(v);         // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E>(v);         // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);        // row_half_mirror
+    v = dpp_add<0x140>(v);        // row_mirror
+    v = dpp_add<0x142, 0xA>(v);   // row_bcast:15
+    return dpp_add<0x143, 0xC>(v);  // row_bcast:31
+}
+
 }  // namespace
 
 extern __shared__ __attribute__((aligned(16))) uint8_t mv_smem[];
@@ -279,43 +298,65 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
     const float *x = a.x[seg];
     const uint8_t *W = a.w[seg];
 
-    if (a.x_in_lds) {  // activation -> LDS, piece p's values at floats [p * XPAD, p * XPAD + PE)
-        float *xl = (float *) mv_smem;
-        for (uint32_t c = threadIdx.x; c < P * PE; c += blockDim.x)
-            xl[(c / PE) * XPAD + c % PE] = c < n_cols ? x[c] : 0.f;
-        __syncthreads();
-    }
     const uint32_t r0 = (wg * waves + wave) * a.rpw;
-    if (r0 >= rows) return;
+    const bool has_rows = r0 < rows;  // uniform per wave
     const uint32_t r1 = min(r0 + a.rpw, rows);
-    const uint32_t units = (r1 - r0) * n_slabs;
-    uint8_t *wb = mv_smem + a.x_lds_bytes + wave * moearc_mv_wave_buf(TY, PPL);
-    const uint32_t wb_off = a.x_lds_bytes + wave * moearc_mv_wave_buf(TY, PPL);
+    const uint32_t units = has_rows ? (r1 - r0) * n_slabs : 0u;
+    const uint32_t wb_off = a.x_lds_bytes + wave * a.wave_buf;
+    uint8_t *wb = mv_smem + wb_off;
 
     // Byte offset of piece p's block (or of the piece itself, for F32/F16) within its row.
     auto piece_byte = [&](uint32_t p) -> uint64_t {
         return BE == 1u ? (uint64_t) p * (PE * BB) : (uint64_t) (p / PPB) * BB;
     };
 
-    u32x4_t g[GMAX];
-    uint32_t next_delta = 0, next_ng = 0;
-    auto issue = [&](uint32_t u) {  // granules of unit u (row r0 + u / n_slabs, slab u % n_slabs)
+    // Unit u = (row r0 + u / n_slabs, slab u % n_slabs). Two units' granules are in flight at
+    // once, in registers ga / gb (a unit's LDS copy is written just before it is decoded).
+    u32x4_t ga[GMAX], gb[GMAX];
+    uint32_t da = 0, na = 0, db = 0, nb = 0;  // LDS offset of the first byte, granule count
+    auto issue = [&](uint32_t u, u32x4_t (&g)[GMAX], uint32_t &delta, uint32_t &ng) {
         const uint32_t r = r0 + u / n_slabs, sl = u % n_slabs;
         const uint64_t b0 = piece_byte(sl * SP);
         const uint64_t b1 = min((uint64_t) a.row_bytes, piece_byte(min((sl + 1u) * SP, P) - 1u) +
                                                             (BE == 1u ? PE * BB : BB));
         const uintptr_t src = (uintptr_t) (W + (uint64_t) r * a.row_bytes + b0);
         const uintptr_t base = src & ~(uintptr_t) 15;
-        next_delta = (uint32_t) (src - base);
-        next_ng = P ? (uint32_t) ((next_delta + (b1 - b0) + 15u) >> 4) : 0u;
+        delta = (uint32_t) (src - base);
+        ng = (uint32_t) ((delta + (b1 - b0) + 15u) >> 4);  // >= 1: the host never launches P == 0
+        // Every lane issues all GMAX loads (indices past the unit clamp to its last granule), so
+        // the number of loads in flight is fixed and each LDS copy waits for its own only.
 #pragma unroll
         for (uint32_t k = 0; k < GMAX; ++k) {
-            if (k * 64u < next_ng) {
-                const uint32_t gi = min(lane + 64u * k, next_ng - 1u);
-                g[k] = gload16(base + 16u * (uintptr_t) gi);
-            }
+            const uint32_t gi = min(lane + 64u * k, ng - 1u);
+            g[k] = gload16(base + 16u * (uintptr_t) gi);
         }
     };
+
+    // The first row's weights are in flight before anything waits on the activation.
+    if (has_rows) {
+        issue(0, ga, da, na);
+        issue(min(1u, units - 1u), gb, db, nb);  // always two units in flight (re-reads past the end)
+    }
+    if (a.x_in_lds) {  // activation -> LDS, piece p's values at floats [p * XPAD, p * XPAD + PE)
+        constexpr uint32_t XB = 8;  // loads in flight per thread before their stores
+        float *xl = (float *) mv_smem;
+        const uint32_t total = P * PE;
+        for (uint32_t c0 = threadIdx.x; c0 < total; c0 += XB * blockDim.x) {
+            float v[XB];
+#pragma unroll
+            for (uint32_t k = 0; k < XB; ++k) {
+                const uint32_t c = c0 + k * blockDim.x;
+                v[k] = c < n_cols ? x[c] : 0.f;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < XB; ++k) {
+                const uint32_t c = c0 + k * blockDim.x;
+                if (c < total) xl[(c / PE) * XPAD + c % PE] = v[k];
+            }
+        }
+        __syncthreads();
+    }
+    if (!has_rows) return;
 
     float xr[PPL][PE];
     float xs[PPL];
@@ -339,6 +380,9 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
                     const uint64_t c = (uint64_t) min(p, P - 1u) * PE + j;
                     xr[i][j] = c < n_cols ? x[c] : 0.f;
                 }
+                // Drain here (vmcnt(0)): otherwise the compiler cannot tell these loads from the
+                // weight granules in flight and waits for everything wherever xr is read.
+                __builtin_amdgcn_s_waitcnt(0x0F70);
             }
             if constexpr (needs_xsum(TY)) {
                 float t = 0.f;
@@ -351,17 +395,19 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
         }
     };
 
-    issue(0);
     float acc = 0.f;
-    for (uint32_t u = 0; u < units; ++u) {
+    auto step = [&](uint32_t u, u32x4_t (&g)[GMAX], uint32_t &delta_ref, uint32_t &ng_ref) {
         const uint32_t sl = u % n_slabs, r = r0 + u / n_slabs;
-        const uint32_t delta = next_delta, ng = next_ng;
+        const uint32_t delta = delta_ref, ng = ng_ref;
 #pragma unroll
         for (uint32_t k = 0; k < GMAX; ++k) {
             const uint32_t gi = lane + 64u * k;
-            if (k * 64u < ng && gi < ng) *(u32x4_t *) (wb + 16u * gi) = g[k];
+            if (gi < ng) *(u32x4_t *) (wb + 16u * gi) = g[k];
         }
-        if (u + 1u < units) issue(u + 1u);
+        // The row's bias (a.bias[seg] points at readable memory even without one) is requested
+        // before the next loads so that waiting for it never waits for them.
+        const float bv = a.bias[seg][r];
+        issue(min(u + 2u, units - 1u), g, delta_ref, ng_ref);
         __builtin_amdgcn_wave_barrier();
         if (u == 0 || n_slabs > 1u) load_x(sl);
         const uint64_t slab_b0 = piece_byte(sl * SP);
@@ -376,16 +422,15 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
         }
         __builtin_amdgcn_wave_barrier();
         if (sl + 1u == n_slabs) {
-#pragma unroll
-            for (uint32_t off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, (int) off);
-            if (lane == 0) {
-                const float *bias = a.bias[seg];
-                a.out[seg][r] = bias ? acc + bias[r] : acc;
-            }
+            acc = wave_sum_to_lane63(acc);
+            if (lane == 63u) a.out[seg][r] = (a.bias_mask >> seg) & 1u ? acc + bv : acc;
             acc = 0.f;
         }
+    };
+    for (uint32_t u = 0; u < units; u += 2u) {
+        step(u, ga, da, na);
+        if (u + 1u < units) step(u + 1u, gb, db, nb);
     }
-    (void) wb;
 }
 
 #define MATVEC_KERNEL(NAME, TY, PPL)                                                              \
@@ -403,7 +448,6 @@ MATVEC_KERNEL(f16, 1, 4)
 MATVEC_KERNEL(q8_0, 8, 1)
 MATVEC_KERNEL(q8_0, 8, 2)
 MATVEC_KERNEL(q8_0, 8, 4)
-MATVEC_KERNEL(q8_0, 8, 8)
 MATVEC_KERNEL(q4_k, 12, 1)
 MATVEC_KERNEL(q4_k, 12, 2)
 MATVEC_KERNEL(q4_k, 12, 4)
@@ -413,7 +457,6 @@ MATVEC_KERNEL(q5_k, 13, 4)
 MATVEC_KERNEL(q6_k, 14, 1)
 MATVEC_KERNEL(q6_k, 14, 2)
 MATVEC_KERNEL(q6_k, 14, 4)
-MATVEC_KERNEL(q6_k, 14, 8)
 MATVEC_KERNEL(mxfp4, 39, 1)
 MATVEC_KERNEL(mxfp4, 39, 2)
 MATVEC_KERNEL(mxfp4, 39, 4)

@@ -99,6 +99,8 @@ struct moearc_ctx {
     size_t counters_n = 0;
     int decode_variant_override = -1;  // MOEARC_DECODE_VARIANT, e.g. "4x4"
     unsigned long split_override = 0;  // MOEARC_DECODE_SPLIT (keys per split)
+    unsigned long mv_rpw_override = 0;  // MOEARC_MATVEC_RPW: rows per wave of the matvec launches
+    unsigned mv_waves_override = 0;     // MOEARC_MATVEC_WAVES: 4 or 8 waves per work-group
 };
 
 namespace {
@@ -484,6 +486,11 @@ moearc_ctx *moearc_ctx_create(void) {
             }
         }
     }
+    if (const char *r = std::getenv("MOEARC_MATVEC_RPW")) c->mv_rpw_override = std::strtoul(r, nullptr, 10);
+    if (const char *w = std::getenv("MOEARC_MATVEC_WAVES")) {
+        const unsigned long v = std::strtoul(w, nullptr, 10);
+        if (v == 4 || v == 8) c->mv_waves_override = (unsigned) v;
+    }
     const char *ev = std::getenv("MOEARC_PROFILE_EVENTS");
     c->profiling = ev && ev[0] == '1';
     if (const char *w = std::getenv("MOEARC_DECODE_VARIANT")) {
@@ -685,7 +692,10 @@ struct MvJob {
 };
 
 constexpr unsigned kMvLdsCap = 64u * 1024u;  // dynamic LDS per work-group the launches stay under
-constexpr unsigned long kMvWavesTarget = 256ul * 16ul;  // waves that fill the chip (16 per CU)
+// Rows per wave: enough that the launch is about one work-group per CU (256 on MI355X). Fewer,
+// longer-lived waves measured faster than more, shorter ones at the projection shapes: each
+// work-group stages the activation once, and a wave keeps two rows in flight.
+constexpr unsigned long kMvCUs = 256ul;
 
 // Shape checks shared by the matvec entry points (kernels.cpp:1053-1057): the type must be known
 // and a row a whole number of blocks.
@@ -718,7 +728,10 @@ int mv_launch(moearc_ctx *c, unsigned ty, const MvJob *jobs, unsigned n, unsigne
     while ((64ull << li) < pieces && (2u << li) <= moearc_mv_ppl_max(ty)) ++li;
     const uint32_t ppl = 1u << li;
     const uint64_t slabs = (pieces + 64ull * ppl - 1) / (64ull * ppl);
-    const unsigned wave_buf = moearc_mv_wave_buf(ty, ppl);
+    const uint64_t row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
+    const uint64_t slab_bytes =
+        slabs == 1 ? row_bytes : 64ull * ppl * pe * moearc_mv_bb(ty) / moearc_mv_be(ty);
+    const unsigned wave_buf = moearc_mv_wave_buf(slab_bytes);
     const uint64_t x_lds = (pieces * (pe + 4u) * 4u + 15u) & ~15ull;
     unsigned waves = MOEARC_MV_MAX_WAVES, x_in_lds = 1;
     if (x_lds + (uint64_t) waves * wave_buf > kMvLdsCap) {
@@ -733,21 +746,26 @@ int mv_launch(moearc_ctx *c, unsigned ty, const MvJob *jobs, unsigned n, unsigne
     unsigned long total = 0;
     for (unsigned i = 0; i < n; ++i) total += jobs[i].rows;
     if (total == 0) return OK;
-    const uint32_t rpw = (uint32_t) std::min<unsigned long>(64, std::max<unsigned long>(
-                                                                     1, (total + kMvWavesTarget - 1) / kMvWavesTarget));
+    if (c->mv_waves_override && x_lds * (x_in_lds ? 1 : 0) + (uint64_t) c->mv_waves_override * wave_buf <= kMvLdsCap)
+        waves = c->mv_waves_override;
+    const uint32_t rpw = (uint32_t) std::min<unsigned long>(
+        64, c->mv_rpw_override ? c->mv_rpw_override
+                               : std::max<unsigned long>(1, (total + kMvCUs * waves - 1) / (kMvCUs * waves)));
     MatvecArgs a{};
     uint64_t wgs = 0;
     for (unsigned i = 0; i < n; ++i) {
         a.w[i] = static_cast<const uint8_t *>(jobs[i].w);
         a.x[i] = jobs[i].x;
-        a.bias[i] = jobs[i].bias;
+        a.bias[i] = jobs[i].bias ? jobs[i].bias : jobs[i].out;
+        a.bias_mask |= jobs[i].bias ? 1u << i : 0u;
         a.out[i] = jobs[i].out;
         a.rows[i] = (uint32_t) jobs[i].rows;
         wgs += (jobs[i].rows + (uint64_t) waves * rpw - 1) / ((uint64_t) waves * rpw);
         if (wgs >= 0x7FFFFFFFull) return ERR_ARG;
         a.wg_end[i] = (uint32_t) wgs;
     }
-    a.row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
+    a.row_bytes = row_bytes;
+    a.wave_buf = wave_buf;
     a.n_seg = n;
     a.n_cols = (uint32_t) n_cols;
     a.n_pieces = (uint32_t) pieces;
