@@ -205,6 +205,42 @@ int moearc_attn_qkv(moearc_ctx *c, const unsigned int *type_ids, float *const *o
                     const void *const *w, const float *const *bias, const unsigned long *rows,
                     const float *x, unsigned long n_cols);
 
+/* ---- the attention block over a prompt chunk ---------------------------------------------------
+ * Extension (no counterpart in the reference, whose prefill runs the whole model one token at a
+ * time, session.rs:378-381 and moe.rs:1856-1862): the attention half of one block for n_tok
+ * consecutive tokens in one call, the sequence of moe.rs:1942-2071 after attn.norm --
+ *   q, k, v = W_{q,k,v} x (+ biases)        (moearc_attn_qkv, per token)
+ *   q, k    = NeoX RoPE at pos[t]           (moearc_rope; K fused with the append below)
+ *   K, V    -> pages[page_ids[t]], slot slots[t], f16   (moearc_rope_kv_append_chunk)
+ *   attn    = chunked prefill over keys [pos0 + t + 1 - n_swa | 0, pos0 + t + 1)   (moearc_attn_prefill)
+ *   h      += W_o attn (+ bias_o)           (moearc_matvec_q per token, moearc_add)
+ * with every earlier token's K/V already in the pages. n_tok = 1 is one decode step. All pointers
+ * are device memory except `b` itself. The projections of a chunk are run token by token through
+ * the batched matvec (up to 32 matrix-vector products per launch). */
+typedef struct moearc_attn_block {
+    unsigned int w_type[4];      /* GGUF type ids of W_q, W_k, W_v, W_o */
+    const void *w[4];            /* W_q [n_head*head_dim][n_embd], W_k / W_v [n_head_kv*head_dim][n_embd],
+                                    W_o [n_embd][n_head*head_dim] */
+    const float *bias[4];        /* the matching biases, each may be NULL */
+    const float *sinks;          /* [n_head] or NULL */
+    void *k_pages, *v_pages;     /* f16 paged cache of this block */
+    const unsigned int *block_table; /* the sequence's pages (a windowed block: its ring table) */
+    unsigned long n_embd, n_head, n_head_kv, head_dim, page_tokens;
+    unsigned long n_swa;         /* 0: full attention */
+    float scale;                 /* attention scale, 1/sqrt(head_dim) */
+    unsigned long n_rot;         /* rotated dimensions */
+    float freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi;  /* as moearc_rope */
+} moearc_attn_block;
+
+/* h f32 [n_tok][n_embd] (updated in place), x f32 [n_tok][n_embd] (attn.norm's output), pos i32,
+ * page_ids / slots u32 [n_tok] (the tokens' cache places, as moearc_kv_pool_append_chunk returns
+ * them), tokens at positions pos0 .. pos0 + n_tok - 1. Working memory is the context's (grown on
+ * demand, kept). Refusals: null c, b, h, x, pos, page_ids or slots -> -1; then those of the calls
+ * above, in that order (nothing is enqueued for a refusal found before the first launch). */
+int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h, const float *x,
+                            unsigned long n_tok, unsigned long pos0, const int *pos,
+                            const unsigned int *page_ids, const unsigned int *slots);
+
 /* The stream the context enqueues on (a hipStream_t), so a caller can order its own work. */
 void *moearc_ctx_stream(moearc_ctx *c);
 

@@ -5,5 +5,5 @@ mirror of the reference wrapper (context.py), the ctypes binding (native.py), th
 (build.py) and the seeded synthetic-input generator (synth.py).
 """
 from .context import (BadArgument, BufferTooSmall, Context, DeviceBuffer, Failed, KernelError,  # noqa: F401
-                      DeviceView, KvType, NoDevice, OutOfMemory, OUT_F16, OUT_F32, QuantType,
+                      AttnBlockDesc, DeviceView, KvType, NoDevice, OutOfMemory, OUT_F16, OUT_F32, QuantType,
                       RopeKind, RopeScaling)

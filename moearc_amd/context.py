@@ -410,6 +410,16 @@ class Context:
         self.finish(self._lib.moearc_add(self.raw, out.ptr, a.ptr, b.ptr, n), "add")
 
 
+    def attn_block_chunk(self, desc: "AttnBlockDesc", h: DeviceBuffer, x: DeviceBuffer, n_tok: int,
+                         pos0: int, pos: DeviceBuffer, page_ids: DeviceBuffer, slots: DeviceBuffer) -> None:
+        """The attention half of one block over n_tok prompt tokens (moe.rs:1942-2071, chunked)."""
+        h.require("residual", n_tok * desc.n_embd * 4)
+        x.require("normed input", n_tok * desc.n_embd * 4)
+        for buf, what in ((pos, "positions"), (page_ids, "page ids"), (slots, "slots")):
+            buf.require(what, n_tok * 4)
+        self.finish(self._lib.moearc_attn_block_chunk(self.raw, ctypes.byref(desc), h.ptr, x.ptr, n_tok, pos0,
+                                                      pos.ptr, page_ids.ptr, slots.ptr), "attention block chunk")
+
     def attn_qkv(self, types, outs, ws, biases, rows, x: DeviceBuffer, n_cols: int) -> None:
         """The q, k, v projections plus their biases in as few launches as the types allow."""
         types = [QuantType(t) for t in types]
@@ -427,6 +437,35 @@ class Context:
         self.finish(self._lib.moearc_attn_qkv(self.raw, tarr, _ptr_array(outs), _ptr_array(ws),
                                               _ptr_array(biases), rarr, x.ptr, n_cols), "attn qkv")
 
+
+class AttnBlockDesc(ctypes.Structure):
+    """``moearc_attn_block`` (include/moearc_attn.h): one block's attention weights, cache and RoPE."""
+    _fields_ = [("w_type", ctypes.c_uint * 4), ("w", ctypes.c_void_p * 4), ("bias", ctypes.c_void_p * 4),
+                ("sinks", ctypes.c_void_p), ("k_pages", ctypes.c_void_p), ("v_pages", ctypes.c_void_p),
+                ("block_table", ctypes.c_void_p), ("n_embd", ctypes.c_ulong), ("n_head", ctypes.c_ulong),
+                ("n_head_kv", ctypes.c_ulong), ("head_dim", ctypes.c_ulong), ("page_tokens", ctypes.c_ulong),
+                ("n_swa", ctypes.c_ulong), ("scale", ctypes.c_float), ("n_rot", ctypes.c_ulong),
+                ("freq_base", ctypes.c_float), ("freq_scale", ctypes.c_float), ("ext_factor", ctypes.c_float),
+                ("attn_factor", ctypes.c_float), ("corr_lo", ctypes.c_float), ("corr_hi", ctypes.c_float)]
+
+    @staticmethod
+    def make(types, ws, biases, sinks, k_pages, v_pages, block_table, n_embd, n_head, n_head_kv,
+             head_dim, page_tokens, n_swa, scale, n_rot, freq_base, scaling: "RopeScaling | None" = None):
+        s = scaling or RopeScaling()
+        d = AttnBlockDesc()
+        for i in range(4):
+            d.w_type[i] = int(types[i])
+            d.w[i] = ws[i].ptr
+            d.bias[i] = biases[i].ptr if biases[i] is not None else None
+        d.sinks = sinks.ptr if sinks is not None else None
+        d.k_pages, d.v_pages, d.block_table = k_pages.ptr, v_pages.ptr, block_table.ptr
+        d.n_embd, d.n_head, d.n_head_kv, d.head_dim = n_embd, n_head, n_head_kv, head_dim
+        d.page_tokens, d.n_swa, d.scale, d.n_rot, d.freq_base = page_tokens, n_swa, scale, n_rot, freq_base
+        d.freq_scale, d.ext_factor, d.attn_factor = s.freq_scale, s.ext_factor, s.attn_factor
+        d.corr_lo, d.corr_hi = s.corr_lo, s.corr_hi
+        # the descriptor holds raw device pointers: keep their buffers alive as long as it lives
+        d._buffers = [b for b in (*ws, *biases, sinks, k_pages, v_pages, block_table) if b is not None]
+        return d
 
 class QuantType(enum.IntEnum):
     """GGUF weight formats the matvec kernels expand (lib.rs ``QuantType``, reference.rs:69-121)."""

@@ -99,6 +99,8 @@ struct moearc_ctx {
     size_t counters_n = 0;
     int decode_variant_override = -1;  // MOEARC_DECODE_VARIANT, e.g. "4x4"
     unsigned long split_override = 0;  // MOEARC_DECODE_SPLIT (keys per split)
+    float *blk_ws = nullptr;  // attention-block chunk: q, k, v, f16 q, attention output, projection
+    size_t blk_ws_bytes = 0;
     unsigned long mv_rpw_override = 0;  // MOEARC_MATVEC_RPW: rows per wave of the matvec launches
     unsigned mv_waves_override = 0;     // MOEARC_MATVEC_WAVES: 4 or 8 waves per work-group
 };
@@ -511,6 +513,7 @@ void moearc_ctx_destroy(moearc_ctx *c) {
     for (auto e : c->event_pool) hipEventDestroy(e);
     if (c->ws) hipFree(c->ws);
     if (c->counters) hipFree(c->counters);
+    if (c->blk_ws) hipFree(c->blk_ws);
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -995,3 +998,93 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
 }
 
 }  // extern "C"
+
+namespace {
+
+// Run jobs[0..n) (one weight type) in launches of at most MOEARC_MV_MAX_SEG matrix-vector products.
+int mv_launch_all(moearc_ctx *c, unsigned ty, const std::vector<MvJob> &jobs, unsigned long n_cols,
+                  const char *what) {
+    for (size_t i = 0; i < jobs.size(); i += MOEARC_MV_MAX_SEG) {
+        const unsigned n = (unsigned) std::min<size_t>(MOEARC_MV_MAX_SEG, jobs.size() - i);
+        if (const int rc = mv_launch(c, ty, jobs.data() + i, n, n_cols, what, jobs[i].rows, n)) return rc;
+    }
+    return OK;
+}
+
+}  // namespace
+
+int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h, const float *x,
+                            unsigned long n_tok, unsigned long pos0, const int *pos,
+                            const unsigned int *page_ids, const unsigned int *slots) {
+    if (!c || !b || !h || !x || !pos || !page_ids || !slots) return ERR;
+    if (n_tok == 0) return OK;
+    for (int i = 0; i < 4; ++i)
+        if (!b->w[i]) return ERR;
+    if (!b->k_pages || !b->v_pages || !b->block_table) return ERR;
+    const unsigned long E = b->n_embd, H = b->n_head, G = b->n_head_kv, D = b->head_dim;
+    if (H == 0 || G == 0 || D == 0 || E == 0 || H % G != 0) return ERR_ARG;
+    const unsigned long q_rows = H * D, kv_rows = G * D;
+    // the projections' shape checks, then the prefill's, before anything is enqueued
+    for (int i = 0; i < 3; ++i)
+        if (const int rc = mv_check(b->w_type[i], i == 0 ? q_rows : kv_rows, E)) return rc;
+    if (const int rc = mv_check(b->w_type[3], E, q_rows)) return rc;
+    const unsigned long group = H / G;
+    if (D != 64 || !is_pow2(b->page_tokens) || (group != 1 && group != 2 && group != 4 && group != 8) ||
+        pos0 + n_tok > 0xFFFFFFFFul || b->n_rot == 0 || b->n_rot % 2 != 0 || b->n_rot > D)
+        return ERR_ARG;
+
+    // working memory: q, k, v, rotated q, f16 q, attention output, projection
+    const size_t nq = n_tok * q_rows, nkv = n_tok * kv_rows;
+    const size_t floats = nq + 2 * nkv + nq + (nq + 1) / 2 + nq + n_tok * E;
+    if (floats * sizeof(float) > c->blk_ws_bytes) {
+        if (c->blk_ws) {
+            hipStreamSynchronize(c->stream);
+            hipFree(c->blk_ws);
+            c->blk_ws = nullptr;
+            c->blk_ws_bytes = 0;
+        }
+        if (hipMalloc((void **) &c->blk_ws, floats * sizeof(float)) != hipSuccess) return ERR;
+        c->blk_ws_bytes = floats * sizeof(float);
+    }
+    float *q = c->blk_ws, *k = q + nq, *v = k + nkv, *qr = v + nkv;
+    uint16_t *q16 = (uint16_t *) (qr + nq);
+    float *att = qr + nq + (nq + 1) / 2, *proj = att + nq;
+
+    // q, k, v (+ biases): every (token, projection) pair, grouped by weight type
+    {
+        float *outs[3] = {q, k, v};
+        const unsigned long rows[3] = {q_rows, kv_rows, kv_rows};
+        bool done[3] = {false, false, false};
+        for (int i = 0; i < 3; ++i) {
+            if (done[i]) continue;
+            std::vector<MvJob> jobs;
+            for (int j = i; j < 3; ++j) {
+                if (done[j] || b->w_type[j] != b->w_type[i]) continue;
+                done[j] = true;
+                for (unsigned long t = 0; t < n_tok; ++t)
+                    jobs.push_back(MvJob{b->w[j], x + t * E, b->bias[j], outs[j] + t * rows[j], rows[j]});
+            }
+            if (const int rc = mv_launch_all(c, b->w_type[i], jobs, E, "attn_qkv_chunk")) return rc;
+        }
+    }
+    // RoPE of q, narrowed to f16 for the prefill kernel; RoPE of K fused with the K/V append
+    if (const int rc = moearc_rope(c, qr, q, pos, n_tok, H, D, b->n_rot, b->freq_base, b->freq_scale,
+                                   b->ext_factor, b->attn_factor, b->corr_lo, b->corr_hi, 1))
+        return rc;
+    if (const int rc = moearc_quantize_f16(c, q16, qr, nq)) return rc;
+    if (const int rc = moearc_rope_kv_append_chunk(c, b->k_pages, b->v_pages, k, v, pos, page_ids, slots,
+                                                   n_tok, G, D, b->page_tokens, b->n_rot, b->freq_base,
+                                                   b->freq_scale, b->ext_factor, b->attn_factor,
+                                                   b->corr_lo, b->corr_hi, 1, 1u))
+        return rc;
+    if (const int rc = moearc_attn_prefill(c, att, MOEARC_OUT_F32, q16, b->k_pages, b->v_pages,
+                                           b->block_table, b->sinks, n_tok, pos0, b->n_swa, H, G, D,
+                                           b->page_tokens, b->scale, 1u))
+        return rc;
+    // h += W_o attn (+ bias_o)
+    std::vector<MvJob> jobs;
+    for (unsigned long t = 0; t < n_tok; ++t)
+        jobs.push_back(MvJob{b->w[3], att + t * q_rows, b->bias[3], proj + t * E, E});
+    if (const int rc = mv_launch_all(c, b->w_type[3], jobs, q_rows, "attn_proj_chunk")) return rc;
+    return moearc_add(c, h, h, proj, n_tok * E);
+}

@@ -1,0 +1,171 @@
+"""The attention block over prompt chunks (moearc_attn_block_chunk) on the GPU, against the oracle
+composed step by step as the reference engine runs one token at a time (moe.rs:1942-2071):
+projections + biases (orc_matvec_q), NeoX RoPE (orc_rope_yarn), the f16 KV append
+(orc_kv_append_raw), attention as repeated decode (orc_attn_prefill) and the output projection
+added to the residual.
+
+Bar: every attention output within the north star's 2e-3, carried through W_o: per residual
+element |gpu - oracle| <= 2e-3 * sum_c |W_o[r][c]| + 1e-5. The activations are scaled (x ~
+N(0, 0.01)) so that q and k come out O(1), as a normed residual gives them: with scores in the
+thousands the softmax turns a one-ulp f16 difference in a rotated key (f32 angles on the GPU,
+f64 in the oracle) into a different winner, which no attention tolerance covers.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import fixtures as fx
+from moearc_amd import AttnBlockDesc, KvType, RopeScaling
+from moearc_amd.kv import KvGeometry, PagedKvCache
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+E, H, G, D, PT = 256, 8, 2, 64, 16
+
+
+class Block:
+    def __init__(self, ctx, types, seed, biases=True, sinks=True, n_swa=0, n_ctx=256, chunk=64,
+                 scaling=None, freq_base=10000.0):
+        self.types, self.n_swa, self.scaling, self.freq_base = types, n_swa, scaling or RopeScaling(), freq_base
+        shapes = [(H * D, E), (G * D, E), (G * D, E), (E, H * D)]
+        self.w = [fx.synth_blocks(t, r * c // fx.QT_BLOCK[t][1], seed + i)[0] for i, (t, (r, c)) in
+                  enumerate(zip(types, shapes))]
+        self.shapes = shapes
+        self.b = [fx.synth.unit(seed + 10 + i, r).astype(np.float32) * np.float32(0.1) if biases else None
+                  for i, (r, _) in enumerate(shapes)]
+        self.sinks = fx.synth.unit(seed + 20, H).astype(np.float32) if sinks else None
+        geo = KvGeometry.plan(n_ctx, PT, n_swa or None, chunk=chunk)
+        self.ring = n_swa > 0
+        self.n_pages = geo.swa_pages if self.ring else geo.pages + 2
+        self.table = geo.ring_table() if self.ring else None
+        self.pool = None if self.ring else PagedKvCache(self.n_pages, PT, n_ctx)
+        if self.pool is not None:
+            self.pool.begin(7, 0)
+        self.kp = np.zeros(self.n_pages * PT * G * D, np.uint16)  # the oracle's copy of the pages
+        self.vp = np.zeros_like(self.kp)
+        self.d_w = [ctx.upload(w) for w in self.w]
+        self.d_b = [ctx.upload(b) if b is not None else None for b in self.b]
+        self.d_s = ctx.upload(self.sinks) if sinks else None
+        self.d_kp, self.d_vp = ctx.alloc(self.kp.nbytes), ctx.alloc(self.vp.nbytes)
+        ctx.upload_slice(self.d_kp, self.kp)
+        ctx.upload_slice(self.d_vp, self.vp)
+        self.n = 0  # tokens so far
+
+    def places(self, n):
+        if self.ring:
+            pos = np.arange(self.n, self.n + n)
+            return self.table[pos // PT].astype(np.uint32), (pos % PT).astype(np.uint32), self.table
+        pages, slots = self.pool.append_chunk(7, n)
+        return pages, slots, np.array(self.pool.pages_of(7).pages, np.uint32)
+
+    def rope(self, a, pos, heads):
+        s = self.scaling
+        return oracle.rope_yarn(a, pos, len(pos), heads, D, D, self.freq_base, s.freq_scale, s.ext_factor,
+                                s.attn_factor, s.corr_lo, s.corr_hi).astype(np.float32)
+
+    def oracle_chunk(self, h, x, pages, slots, table):
+        n, pos0 = x.shape[0], self.n
+        pos = np.arange(pos0, pos0 + n, dtype=np.int32)
+        proj = []
+        for i, (r, c) in enumerate(self.shapes[:3]):
+            y = np.stack([oracle.matvec_q(self.types[i], self.w[i], x[t], r, c)[0] for t in range(n)])
+            proj.append(y + self.b[i] if self.b[i] is not None else y)
+        q, k, v = proj
+        qr, kr = self.rope(q, pos, H), self.rope(k, pos, G).reshape(n, G * D)
+        for t in range(n):
+            oracle.kv_append_raw(self.kp, self.vp, kr[t], v[t], int(pages[t]), int(slots[t]), G, D, PT,
+                                 oracle.KV_F16)
+        q16 = qr.astype(np.float16).astype(np.float32).reshape(n, H, D)
+        att = oracle.attn_prefill(q16, self.kp, self.vp, table, n, pos0, self.n_swa, H, G, D, PT,
+                                  1.0 / np.sqrt(D), sinks=self.sinks, n_threads=8).reshape(n, H * D)
+        r, c = self.shapes[3]
+        o = np.stack([oracle.matvec_q(self.types[3], self.w[3], att[t], r, c)[0] for t in range(n)])
+        if self.b[3] is not None:
+            o = o + self.b[3]
+        return (h + o).astype(np.float32)
+
+    def desc(self, ctx, d_table):
+        return AttnBlockDesc.make(self.types, self.d_w, self.d_b, self.d_s, self.d_kp, self.d_vp, d_table,
+                                  E, H, G, D, PT, self.n_swa, float(np.float32(1.0 / np.sqrt(D))), D,
+                                  self.freq_base, self.scaling)
+
+    def gpu_chunk(self, ctx, h, x, pages, slots, table):
+        n = x.shape[0]
+        d_h, d_x = ctx.upload(h), ctx.upload(x)
+        pos = np.arange(self.n, self.n + n, dtype=np.int32)
+        ctx.attn_block_chunk(self.desc(ctx, ctx.upload(table)), d_h, d_x, n, self.n, ctx.upload(pos),
+                             ctx.upload(pages), ctx.upload(slots))
+        return ctx.download(d_h, np.float32, (n, E))
+
+    def bound(self):
+        r, c = self.shapes[3]
+        wo = oracle.dequant(self.types[3], self.w[3], r * c // fx.QT_BLOCK[self.types[3]][1]).reshape(r, c)
+        return 2e-3 * np.abs(wo.astype(np.float64)).sum(axis=1) + 1e-5
+
+    def step(self, ctx, n, seed, label):
+        x = (fx.synth.normal(seed, n * E) * 0.1).astype(np.float32).reshape(n, E)
+        h = fx.synth.normal(seed + 1, n * E).astype(np.float32).reshape(n, E)
+        pages, slots, table = self.places(n)
+        got = self.gpu_chunk(ctx, h, x, pages, slots, table)
+        want = self.oracle_chunk(h, x, pages, slots, table)
+        self.n += n
+        err = np.abs(got.astype(np.float64) - want)
+        worst = float(np.max(err / self.bound()))
+        print(f"{label}: {n} tokens at {self.n - n}: worst |gpu - oracle| / bound = {worst:.3f}", flush=True)
+        assert worst <= 1.0, label
+        return got
+
+
+def test_chunks_then_decode_full_attention(ctx):
+    blk = Block(ctx, (8, 8, 8, 8), 0xB10C)
+    blk.step(ctx, 37, 1, "full, Q8_0, chunk 1")
+    blk.step(ctx, 29, 3, "full, Q8_0, chunk 2")
+    blk.step(ctx, 1, 5, "full, Q8_0, decode step")
+
+
+def test_windowed_ring_mixed_types_yarn(ctx):
+    # a windowed block through its ring (sized for window + chunk), sinks, YaRN, four weight types
+    blk = Block(ctx, (1, 8, 12, 14), 0xB20C, n_swa=24, chunk=40,
+                scaling=RopeScaling.yarn(D, 4096, 150000.0, 32.0), freq_base=150000.0)
+    blk.step(ctx, 40, 11, "SWA-24 ring, chunk 1")
+    blk.step(ctx, 33, 13, "SWA-24 ring, chunk 2")
+    blk.step(ctx, 1, 15, "SWA-24 ring, decode step")
+
+
+def test_chunk_equals_token_by_token(ctx):
+    # the chunked call against the reference's shape of work, one token per call, both on the GPU
+    a, b = Block(ctx, (8, 8, 8, 8), 0xB30C, sinks=False), Block(ctx, (8, 8, 8, 8), 0xB30C, sinks=False)
+    n = 21
+    x = (fx.synth.normal(0x77, n * E) * 0.1).astype(np.float32).reshape(n, E)
+    h = fx.synth.normal(0x78, n * E).astype(np.float32).reshape(n, E)
+    pa, sa, ta = a.places(n)
+    chunked = a.gpu_chunk(ctx, h, x, pa, sa, ta)
+    rows = []
+    for t in range(n):
+        p1, s1, t1 = b.places(1)
+        rows.append(b.gpu_chunk(ctx, h[t:t + 1], x[t:t + 1], p1, s1, t1)[0])
+        b.n += 1
+    err = np.abs(chunked.astype(np.float64) - np.stack(rows))
+    worst = float(np.max(err / a.bound()))
+    print(f"chunk of {n} vs {n} single-token calls: worst / bound = {worst:.3f}", flush=True)
+    assert worst <= 1.0
+
+
+def test_refusals(ctx):
+    blk = Block(ctx, (8, 8, 8, 8), 0xB40C)
+    d = blk.desc(ctx, ctx.upload(np.arange(4, dtype=np.uint32)))
+    lib = ctx._lib
+    buf = ctx.alloc(4096)
+    assert lib.moearc_attn_block_chunk(ctx.raw, None, buf.ptr, buf.ptr, 1, 0, buf.ptr, buf.ptr, buf.ptr) == -1
+    d.w_type[3] = 2  # Q4_0: not a format the path expands
+    import ctypes
+    assert lib.moearc_attn_block_chunk(ctx.raw, ctypes.byref(d), buf.ptr, buf.ptr, 1, 0, buf.ptr, buf.ptr,
+                                       buf.ptr) == -2
+    d.w_type[3] = 8
+    d.head_dim = 32
+    assert lib.moearc_attn_block_chunk(ctx.raw, ctypes.byref(d), buf.ptr, buf.ptr, 1, 0, buf.ptr, buf.ptr,
+                                       buf.ptr) == -2
+    ctx.sync()
+    assert KvType.F16 == 1
