@@ -173,6 +173,7 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
         result["out"] = graph_out
         del dks, dvs
         result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
+        result["block_chunk"] = bench_block(ctx, hip)
 
     # per-kernel event timing (eager, profiling context)
     os.environ["MOEARC_PROFILE_EVENTS"] = "1"
@@ -357,6 +358,55 @@ def bench_matvec(ctx, hip, steps):
                       "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
         del inputs
     return res
+
+
+def bench_block(ctx, hip, n_tok=128):
+    """The attention half of one gpt-oss block (Q8_0 projections with biases, sinks, YaRN RoPE,
+    f16 KV in 256-token pages) over a prompt of n_tok tokens: one moearc_attn_block_chunk call
+    against n_tok single-token calls (the reference engine's shape of work, session.rs:378-381).
+    Both timed between HIP events on the context's stream, host submission included (that is
+    the engine's cost too)."""
+    from moearc_amd import AttnBlockDesc, RopeScaling
+    E, Hq, Gk = 2880, H, G
+    rng = np.random.default_rng(0xB10C)
+    shapes = [(Hq * D, E), (Gk * D, E), (Gk * D, E), (E, Hq * D)]
+    ws = []
+    for r, c in shapes:
+        w = rng.integers(0, 256, r * c // 32 * 34, dtype=np.uint8).reshape(-1, 34)
+        w[:, 0:2] = np.frombuffer(np.full(w.shape[0], 0x1800, np.uint16).tobytes(), np.uint8).reshape(-1, 2)
+        ws.append(ctx.upload(w))
+    bs = [ctx.upload((rng.standard_normal(r) * 0.1).astype(np.float32)) for r, _ in shapes]
+    sinks = ctx.upload(rng.standard_normal(Hq).astype(np.float32))
+    pages = (n_tok + PT - 1) // PT
+    kp, vp = ctx.alloc(pages * PT * Gk * D * 2), ctx.alloc(pages * PT * Gk * D * 2)
+    table = ctx.upload(np.arange(pages, dtype=np.uint32))
+    desc = AttnBlockDesc.make([8] * 4, ws, bs, sinks, kp, vp, table, E, Hq, Gk, D, PT, 0, 0.125, D,
+                              150000.0, RopeScaling.yarn(D, 4096, 150000.0, 32.0))
+    x = ctx.upload((rng.standard_normal((n_tok, E)) * 0.05).astype(np.float32))
+    h = ctx.upload(rng.standard_normal((n_tok, E)).astype(np.float32))
+    pos = ctx.upload(np.arange(n_tok, dtype=np.int32))
+    pg = ctx.upload((np.arange(n_tok) // PT).astype(np.uint32))
+    sl = ctx.upload((np.arange(n_tok) % PT).astype(np.uint32))
+    from moearc_amd import DeviceView
+    views = [(DeviceView(h, t * E * 4, E * 4), DeviceView(x, t * E * 4, E * 4), DeviceView(pos, 4 * t, 4),
+              DeviceView(pg, 4 * t, 4), DeviceView(sl, 4 * t, 4)) for t in range(n_tok)]
+    res = {}
+    for label in ("chunked", "token_by_token", "chunked"):
+        ctx.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, ctx.stream)
+        if label == "chunked":
+            ctx.attn_block_chunk(desc, h, x, n_tok, 0, pos, pg, sl)
+        else:
+            for t, (hv, xv, pv, gv, sv) in enumerate(views):
+                ctx.attn_block_chunk(desc, hv, xv, 1, t, pv, gv, sv)
+        hip.record(e1, ctx.stream)
+        ctx.sync()
+        res[label] = hip.elapsed_ms(e0, e1) * 1e3
+    return {"tokens": n_tok, "chunked_us": round(res["chunked"], 1),
+            "token_by_token_us": round(res["token_by_token"], 1),
+            "chunked_us_per_token": round(res["chunked"] / n_tok, 2),
+            "token_by_token_us_per_token": round(res["token_by_token"] / n_tok, 2)}
 
 
 def cpu_baseline(kp, vp, bt, q, sinks):
@@ -613,6 +663,8 @@ def main():
         line["prefill"] = r["prefill"]
     if "projections" in r:
         line["projections"] = r["projections"]
+    if "block_chunk" in r:
+        line["block_chunk"] = r["block_chunk"]
     if "cpu" in r:
         c = r["cpu"]
         line["cpu_baseline"] = {
