@@ -174,6 +174,7 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
         del dks, dvs
         result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
         result["block_chunk"] = bench_block(ctx, hip)
+        result["chunk_projections"] = bench_matmul(ctx, hip)
 
     # per-kernel event timing (eager, profiling context)
     os.environ["MOEARC_PROFILE_EVENTS"] = "1"
@@ -357,6 +358,54 @@ def bench_matvec(ctx, hip, steps):
         res[label] = {"us": round(us, 2), "bytes": nbytes, "hbm_gbs": round(gbs, 0),
                       "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
         del inputs
+    return res
+
+
+# Chunk-form projections on MFMA (moearc_matmul_q) at a config-4 chunk of gpt-oss-20b: (label,
+# type, tokens, rows, columns).
+MM_CASES = [
+    ("attn_q Q8_0 2048 tokens x 4096 x 2880", 8, 2048, 4096, 2880),
+    ("attn.proj Q8_0 2048 tokens x 2880 x 4096", 8, 2048, 2880, 4096),
+    ("attn_q F16 2048 tokens x 4096 x 2880", 1, 2048, 4096, 2880),
+]
+
+
+def bench_matmul(ctx, hip, steps=5):
+    """Each chunk product as a captured graph of `steps` launches (the activation split included),
+    replayed once untimed and once between HIP events. TFLOP/s counts 2 * tokens * rows * cols;
+    the kernel issues twice that on the f16 MFMA (the activation's hi and lo halves)."""
+    from moearc_amd import QuantType
+    res = {}
+    rng = np.random.default_rng(0x33A)
+    for label, ty, n_tok, rows, cols in MM_CASES:
+        qt = QuantType(ty)
+        nbytes = rows * qt.row_bytes(cols)
+        if ty == 1:
+            w = (rng.standard_normal(nbytes // 2) * 0.05).astype(np.float16).view(np.uint8)
+        else:
+            w = rng.integers(0, 256, nbytes, dtype=np.uint8).reshape(-1, 34)
+            w[:, 0:2] = np.frombuffer(np.full(w.shape[0], 0x1800, np.uint16).tobytes(), np.uint8).reshape(-1, 2)
+        dw = ctx.upload(w)
+        dx = ctx.upload(rng.standard_normal((n_tok, cols)).astype(np.float32))
+        db = ctx.upload(rng.standard_normal(rows).astype(np.float32))
+        dy = ctx.alloc(n_tok * rows * 4)
+        ctx.matmul_q(ty, dy, dw, dx, db, n_tok, rows, cols)
+        ctx.sync()
+        graph, exe = hip.capture(ctx.stream, lambda: [ctx.matmul_q(ty, dy, dw, dx, db, n_tok, rows, cols)
+                                                      for _ in range(steps)])
+        e0, e1 = hip.event(), hip.event()
+        hip.launch(exe, ctx.stream)
+        ctx.sync()
+        hip.record(e0, ctx.stream)
+        hip.launch(exe, ctx.stream)
+        hip.record(e1, ctx.stream)
+        ctx.sync()
+        us = hip.elapsed_ms(e0, e1) * 1e3 / steps
+        hip.destroy(graph, exe)
+        tflops = 2.0 * n_tok * rows * cols / us / 1e6
+        res[label] = {"us": round(us, 1), "tflops": round(tflops, 1),
+                      "mfma_f16_frac_issued": round(2 * tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                      "us_per_token": round(us / n_tok, 3)}
     return res
 
 
@@ -665,6 +714,8 @@ def main():
         line["projections"] = r["projections"]
     if "block_chunk" in r:
         line["block_chunk"] = r["block_chunk"]
+    if "chunk_projections" in r:
+        line["chunk_projections"] = r["chunk_projections"]
     if "cpu" in r:
         c = r["cpu"]
         line["cpu_baseline"] = {

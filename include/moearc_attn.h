@@ -205,6 +205,16 @@ int moearc_attn_qkv(moearc_ctx *c, const unsigned int *type_ids, float *const *o
                     const void *const *w, const float *const *bias, const unsigned long *rows,
                     const float *x, unsigned long n_cols);
 
+/* Extension (no counterpart in the reference, which runs one moearc_matvec_q per token): the
+ * projections of a prompt chunk as one MFMA matrix product, y[t][r] = sum_c W[r][c] x[t][c]
+ * (+ bias[r]) for t < n_tok, r < n_rows; x f32 [n_tok][n_cols], y f32 [n_tok][n_rows]. Weights
+ * Q8_0 (8) or F16 (1), W 2-byte aligned. x enters as an f16 hi + lo pair (to 2^-22 relative; each
+ * |x| must stay below 65504), Q8_0 blocks as exact f16 integers scaled by d in f32, so results meet
+ * the matvec bound. Refusals: null c/y/w/x -> -1; another type, n_cols not a multiple of 32, an
+ * odd W address, n_rows, n_tok >= 2^31 -> -2. n_rows or n_tok zero -> 0. */
+int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w, const float *x,
+                    const float *bias, unsigned long n_tok, unsigned long n_rows, unsigned long n_cols);
+
 /* ---- the attention block over a prompt chunk ---------------------------------------------------
  * Extension (no counterpart in the reference, whose prefill runs the whole model one token at a
  * time, session.rs:378-381 and moe.rs:1856-1862): the attention half of one block for n_tok

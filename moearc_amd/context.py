@@ -410,6 +410,17 @@ class Context:
         self.finish(self._lib.moearc_add(self.raw, out.ptr, a.ptr, b.ptr, n), "add")
 
 
+    def matmul_q(self, ty, y: DeviceBuffer, w: DeviceBuffer, x: DeviceBuffer, bias: Optional[DeviceBuffer],
+                 n_tok: int, n_rows: int, n_cols: int) -> None:
+        """A chunk's projection on MFMA: y[t] = W x[t] (+ bias), Q8_0 or F16 weights."""
+        ty = QuantType(ty)
+        w.require("weights", n_rows * ty.row_bytes(n_cols))
+        x.require("activations", n_tok * n_cols * 4)
+        y.require("output", n_tok * n_rows * 4)
+        self.finish(self._lib.moearc_matmul_q(self.raw, int(ty), y.ptr, w.ptr, x.ptr,
+                                              bias.ptr if bias is not None else None, n_tok, n_rows, n_cols),
+                    f"matmul {ty.name}")
+
     def attn_block_chunk(self, desc: "AttnBlockDesc", h: DeviceBuffer, x: DeviceBuffer, n_tok: int,
                          pos0: int, pos: DeviceBuffer, page_ids: DeviceBuffer, slots: DeviceBuffer) -> None:
         """The attention half of one block over n_tok prompt tokens (moe.rs:1942-2071, chunked)."""

@@ -173,3 +173,16 @@ struct MatvecArgs {
     uint32_t wave_buf;     // LDS bytes of one wave's staging buffer
     uint32_t bias_mask;
 };
+
+// Chunk-form projections (matmul.hip): Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the n_tok
+// tokens of a prompt chunk, W Q8_0 (type 8) or F16 (type 1), X given as its f16 hi + lo split.
+#define MOEARC_MM_ROWS 64      // weight rows per work-group (16 per wave)
+#define MOEARC_MM_TOKENS 64    // tokens per work-group
+struct MatmulArgs {
+    const uint8_t *w;
+    const uint16_t *xh, *xl;   // [n_tok][cols] f16: x = hi + lo to within 2^-22 |x|
+    const float *bias;         // [rows] or null
+    float *y;                  // [n_tok][y_stride]
+    uint64_t row_bytes;
+    uint32_t rows, cols, n_tok, y_stride;
+};

@@ -7,3 +7,4 @@
 #include "prefill_fast.hip"
 #include "rope.hip"
 #include "matvec.hip"
+#include "matmul.hip"

@@ -85,6 +85,9 @@ struct moearc_ctx {
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr;
+    hipFunction_t f_mm_q8 = nullptr, f_mm_f16 = nullptr, f_split = nullptr;
+    uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
+    size_t mm_ws_halves = 0;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
     hipFunction_t f_prefill_precise[4] = {};  // the same with p split into f16 hi + lo
     bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
@@ -440,6 +443,9 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_dec_fast[6], "moearc_attn_decode_f16d64_k2w4"},
         {&c->f_dec_merge, "moearc_attn_decode_merge"},
         {&c->f_add, "moearc_add_k"},
+        {&c->f_mm_q8, "moearc_matmul_q8_0_k"},
+        {&c->f_mm_f16, "moearc_matmul_f16_k"},
+        {&c->f_split, "moearc_split_f16_k"},
     };
     for (auto &f : fns) {
         if (hipModuleGetFunction(f.slot, c->module, f.name) != hipSuccess) {
@@ -514,6 +520,7 @@ void moearc_ctx_destroy(moearc_ctx *c) {
     if (c->ws) hipFree(c->ws);
     if (c->counters) hipFree(c->counters);
     if (c->blk_ws) hipFree(c->blk_ws);
+    if (c->mm_ws) hipFree(c->mm_ws);
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -1001,6 +1008,70 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
 
 namespace {
 
+int mm_check(unsigned ty, const void *w, unsigned long n_tok, unsigned long n_rows, unsigned long n_cols) {
+    if (ty != 8u && ty != 1u) return ERR_ARG;
+    if (n_cols % 32 != 0 || ((uintptr_t) w & 1u) || n_rows >= 0x80000000ul || n_tok >= 0x80000000ul ||
+        n_cols >= 0x80000000ul)
+        return ERR_ARG;
+    return OK;
+}
+
+// y = W x over a chunk, x given as its f16 split (xh, xl) of n_tok x n_cols.
+int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, const void *w,
+              const uint16_t *xh, const uint16_t *xl, const float *bias, unsigned long n_tok,
+              unsigned long n_rows, unsigned long n_cols, const char *what) {
+    MatmulArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.xh = xh;
+    a.xl = xl;
+    a.bias = bias;
+    a.y = y;
+    a.row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
+    a.rows = (uint32_t) n_rows;
+    a.cols = (uint32_t) n_cols;
+    a.n_tok = (uint32_t) n_tok;
+    a.y_stride = (uint32_t) y_stride;
+    return launch2d(c, ty == 8u ? c->f_mm_q8 : c->f_mm_f16,
+                    (unsigned) ((n_rows + MOEARC_MM_ROWS - 1) / MOEARC_MM_ROWS),
+                    (unsigned) ((n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS), 256, a, what, n_rows, n_tok);
+}
+
+// The f16 hi / lo split of x (n floats) into the context's buffer; returns its two halves.
+int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl) {
+    if (2 * n > c->mm_ws_halves) {
+        if (c->mm_ws) {
+            hipStreamSynchronize(c->stream);
+            hipFree(c->mm_ws);
+            c->mm_ws = nullptr;
+            c->mm_ws_halves = 0;
+        }
+        if (hipMalloc((void **) &c->mm_ws, 2 * n * sizeof(uint16_t)) != hipSuccess) return ERR;
+        c->mm_ws_halves = 2 * n;
+    }
+    *xh = c->mm_ws;
+    *xl = c->mm_ws + n;
+    struct {
+        const float *x;
+        uint16_t *hi, *lo;
+        uint64_t n;
+    } a{x, *xh, *xl, n};
+    return launch(c, c->f_split, (unsigned) std::min<size_t>((n + 255) / 256, 65536), 256, a, "split_f16", n, 0);
+}
+
+}  // namespace
+
+int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w, const float *x,
+                    const float *bias, unsigned long n_tok, unsigned long n_rows, unsigned long n_cols) {
+    if (!c || !y || !w || !x) return ERR;
+    if (const int rc = mm_check(type_id, w, n_tok, n_rows, n_cols)) return rc;
+    if (n_rows == 0 || n_tok == 0) return OK;
+    uint16_t *xh, *xl;
+    if (const int rc = mm_split(c, x, n_tok * n_cols, &xh, &xl)) return rc;
+    return mm_launch(c, type_id, y, n_rows, w, xh, xl, bias, n_tok, n_rows, n_cols, "matmul");
+}
+
+namespace {
+
 // Run jobs[0..n) (one weight type) in launches of at most MOEARC_MV_MAX_SEG matrix-vector products.
 int mv_launch_all(moearc_ctx *c, unsigned ty, const std::vector<MvJob> &jobs, unsigned long n_cols,
                   const char *what) {
@@ -1050,8 +1121,23 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     uint16_t *q16 = (uint16_t *) (qr + nq);
     float *att = qr + nq + (nq + 1) / 2, *proj = att + nq;
 
-    // q, k, v (+ biases): every (token, projection) pair, grouped by weight type
-    {
+    // q, k, v (+ biases). A chunk of several tokens whose weights the MFMA product takes runs
+    // as one matrix product per projection (the activation split once); the rest as every
+    // (token, projection) pair through the batched matvec, grouped by weight type.
+    const bool mm_qkv = n_tok >= 2 && E % 32 == 0 &&
+                        mm_check(b->w_type[0], b->w[0], n_tok, q_rows, E) == OK &&
+                        mm_check(b->w_type[1], b->w[1], n_tok, kv_rows, E) == OK &&
+                        mm_check(b->w_type[2], b->w[2], n_tok, kv_rows, E) == OK;
+    if (mm_qkv) {
+        uint16_t *xh, *xl;
+        if (const int rc = mm_split(c, x, n_tok * E, &xh, &xl)) return rc;
+        float *outs[3] = {q, k, v};
+        const unsigned long rows[3] = {q_rows, kv_rows, kv_rows};
+        for (int i = 0; i < 3; ++i)
+            if (const int rc = mm_launch(c, b->w_type[i], outs[i], rows[i], b->w[i], xh, xl, b->bias[i], n_tok,
+                                         rows[i], E, "attn_qkv_mm"))
+                return rc;
+    } else {
         float *outs[3] = {q, k, v};
         const unsigned long rows[3] = {q_rows, kv_rows, kv_rows};
         bool done[3] = {false, false, false};
@@ -1082,9 +1168,17 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
                                            b->page_tokens, b->scale, 1u))
         return rc;
     // h += W_o attn (+ bias_o)
-    std::vector<MvJob> jobs;
-    for (unsigned long t = 0; t < n_tok; ++t)
-        jobs.push_back(MvJob{b->w[3], att + t * q_rows, b->bias[3], proj + t * E, E});
-    if (const int rc = mv_launch_all(c, b->w_type[3], jobs, q_rows, "attn_proj_chunk")) return rc;
+    if (n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK) {
+        uint16_t *xh, *xl;
+        if (const int rc = mm_split(c, att, nq, &xh, &xl)) return rc;
+        if (const int rc = mm_launch(c, b->w_type[3], proj, E, b->w[3], xh, xl, b->bias[3], n_tok, E, q_rows,
+                                     "attn_proj_mm"))
+            return rc;
+    } else {
+        std::vector<MvJob> jobs;
+        for (unsigned long t = 0; t < n_tok; ++t)
+            jobs.push_back(MvJob{b->w[3], att + t * q_rows, b->bias[3], proj + t * E, E});
+        if (const int rc = mv_launch_all(c, b->w_type[3], jobs, q_rows, "attn_proj_chunk")) return rc;
+    }
     return moearc_add(c, h, h, proj, n_tok * E);
 }

@@ -48,6 +48,7 @@ def test_code_object_holds_every_kernel_the_runtime_loads():
     src = open(os.path.join(ROOT, "moearc_amd", "csrc", "runtime.cpp")).read()
     kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge)"', src))
     kernels |= {f"moearc_attn_prefill_{v}g{g}" for v in ("", "precise_") for g in (1, 2, 4, 8)}
+    kernels |= {"moearc_matmul_q8_0_k", "moearc_matmul_f16_k", "moearc_split_f16_k"}
     kernels |= {f"moearc_matvec_{t}_p{p}" for t in ("f32", "f16", "q8_0", "q4_k", "q5_k", "q6_k", "mxfp4")
                 for p in (1, 2, 4)}
     assert kernels
@@ -81,6 +82,7 @@ def test_null_context_is_refused_with_minus_one():
     assert lib.moearc_add(None, None, None, None, 4) == -1
     assert lib.moearc_attn_qkv(None, None, None, None, None, None, None, 32) == -1
     assert lib.moearc_attn_block_chunk(None, None, None, None, 1, 0, None, None, None) == -1
+    assert lib.moearc_matmul_q(None, 8, None, None, None, None, 4, 4, 32) == -1
 
 
 def test_missing_build_fails_loudly(monkeypatch):

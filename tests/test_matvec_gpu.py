@@ -203,3 +203,33 @@ def test_matvec_refusals_and_empty_shapes(ctx):
     ctx.matvec_q(QuantType.Q8_0, out, dw, dx, 8, 0)
     assert np.array_equal(ctx.download(out, np.float32, 8), np.zeros(8, np.float32))
     ctx.sync()
+
+
+@pytest.mark.parametrize("ty,n_tok,rows,cols", [
+    (QuantType.Q8_0, 37, 200, 1024), (QuantType.Q8_0, 130, 512, 2880), (QuantType.F16, 67, 96, 512),
+    (QuantType.Q8_0, 2, 4096, 2880), (QuantType.F16, 129, 2880, 4096)], ids=str)
+def test_chunk_matmul_meets_the_matvec_bound(ctx, ty, n_tok, rows, cols):
+    # the MFMA product of a chunk, token by token against the oracle's matvec, at the same bound
+    w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x3A3 + rows)
+    x = fx.synth.unit(0x3A4 + cols, n_tok * cols).reshape(n_tok, cols)
+    bias = fx.synth.unit(0x3A5, rows)
+    y = ctx.alloc(n_tok * rows * 4)
+    ctx.matmul_q(ty, y, ctx.upload(w), ctx.upload(x), ctx.upload(bias), n_tok, rows, cols)
+    got = ctx.download(y, np.float32, (n_tok, rows)).astype(np.float64)
+    worst = 0.0
+    for t in range(n_tok):
+        want, absum = oracle.matvec_q(int(ty), w, x[t], rows, cols, n_threads=16)
+        err = np.abs(got[t] - (want.astype(np.float64) + bias))
+        tol = fx.matvec_tolerance(cols, absum) + 2.0 ** -24 * np.abs(want + bias)  # + the bias add
+        worst = max(worst, float(np.max(err / tol)))
+    print(f"matmul {ty.name} {n_tok}x{rows}x{cols}: worst / bound = {worst:.3f}", flush=True)
+    assert worst <= 1.0
+
+
+def test_chunk_matmul_refusals(ctx):
+    lib = ctx._lib
+    buf = ctx.alloc(1 << 16)
+    assert lib.moearc_matmul_q(ctx.raw, 12, buf.ptr, buf.ptr, buf.ptr, None, 4, 4, 256) == -2  # Q4_K
+    assert lib.moearc_matmul_q(ctx.raw, 8, buf.ptr, buf.ptr, buf.ptr, None, 4, 4, 48) == -2   # not 32k
+    assert lib.moearc_matmul_q(ctx.raw, 8, buf.ptr, buf.ptr + 1, buf.ptr, None, 4, 4, 64) == -2  # odd W
+    assert lib.moearc_matmul_q(ctx.raw, 8, buf.ptr, buf.ptr, buf.ptr, None, 0, 4, 64) == 0
