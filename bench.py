@@ -587,7 +587,8 @@ def bench_configs(steps, warmup):
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
     decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
-    C4 chunk), matvec (the projection cases of MV_CASES, in order), or copy (a 256 MiB device-to-device copy, the
+    C4 chunk), matvec (the projection cases of MV_CASES, in order), matmul (MM_CASES, each as
+    a graph of `steps` launches, replayed twice), or copy (a 256 MiB device-to-device copy, the
     reference size for scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
     from moearc_amd import Context, KvType, OUT_F16
     with Context() as ctx:
@@ -622,6 +623,9 @@ def only(what, steps, warmup):
                     mv_launch(ctx, ty, rows, cols, fused, inputs, i)
                 ctx.sync()
                 del inputs
+        elif what == "matmul":
+            hip = Hip()
+            bench_matmul(ctx, hip, steps=steps)
         elif what == "copy":
             hip = Hip()
             n = 256 << 20
@@ -642,7 +646,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "matvec", "copy"],
+    ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "matvec", "matmul", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
