@@ -176,7 +176,6 @@ struct MatvecArgs {
 
 // Chunk-form projections (matmul.hip): Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the n_tok
 // tokens of a prompt chunk, W Q8_0 (type 8) or F16 (type 1), X given as its f16 hi + lo split.
-#define MOEARC_MM_ROWS 64      // weight rows per work-group (16 per wave)
 #define MOEARC_MM_TOKENS 64    // tokens per work-group
 struct MatmulArgs {
     const uint8_t *w;

@@ -8,7 +8,8 @@
 // scaled by the block's d in f32. F16 weights enter as they are. Activations must stay below
 // 65504 in magnitude (the f16 range of the hi part).
 //
-// Work-group: 4 waves x 16 weight rows, 64 tokens (four 16x16 MFMA tiles per wave). Operand
+// Work-group: 4 waves x RT 16-row tiles, 64 tokens (four 16x16 MFMA tiles per row tile): each
+// activation fragment a wave loads feeds all of its row tiles. Operand
 // layouts (16x16x32 f16): lane l holds row l % 16 of A and column l % 16 of B, eight consecutive
 // k each (the same k for both), and rows 4 (l / 16) .. + 3 of column l % 16 of C.
 #include "common.h"
@@ -19,18 +20,22 @@ typedef _Float16 mm_half8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float mm_f16(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 
-template <uint32_t TY>
+template <uint32_t TY, int RT>
 __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t lr = lane & 15u, lq = lane >> 4;
-    const uint32_t r0 = blockIdx.x * MOEARC_MM_ROWS + 16u * wave;
+    const uint32_t r0 = blockIdx.x * (64u * RT) + 16u * RT * wave;  // RT 16-row tiles per wave
     const uint32_t t0 = blockIdx.y * MOEARC_MM_TOKENS;
     if (r0 >= a.rows) return;  // whole wave past the last row (no barrier in this kernel)
     const uint32_t nb = a.cols / 32u;
-    const uint8_t *wa = a.w + (uint64_t) min(r0 + lr, a.rows - 1u) * a.row_bytes;
-    const uint8_t *wd[4];
+    const uint8_t *wa[RT], *wd[RT][4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) wd[k] = a.w + (uint64_t) min(r0 + 4u * lq + k, a.rows - 1u) * a.row_bytes;
+    for (int rt = 0; rt < RT; ++rt) {
+        wa[rt] = a.w + (uint64_t) min(r0 + 16u * rt + lr, a.rows - 1u) * a.row_bytes;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            wd[rt][k] = a.w + (uint64_t) min(r0 + 16u * rt + 4u * lq + k, a.rows - 1u) * a.row_bytes;
+    }
     const uint16_t *xh[4], *xl[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -38,28 +43,33 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
         xh[j] = a.xh + t * a.cols + 8u * lq;
         xl[j] = a.xl + t * a.cols + 8u * lq;
     }
-    float4_t acc[4];
+    float4_t acc[RT][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rt][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     // One k-block ahead: block b + 1's operands are loaded (unconditionally, the last block's
     // again at the end, so the wait counts are static) before block b's products.
     struct Ops {  // raw loaded words: converted only when used, so a load never waits early
-        uint16_t a[8];
-        uint16_t d[4];
+        uint16_t a[RT][8];
+        uint16_t d[RT][4];
         mm_half8 bh[4], bl[4];
     };
     auto load = [&](uint32_t b, Ops &o) {
-        if constexpr (TY == 8) {  // Q8_0: 34-byte blocks, f16 d then 32 int8
-            const uint16_t *q = (const uint16_t *) (wa + 34u * b + 2u + 8u * lq);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o.a[i] = q[i];
+        for (int rt = 0; rt < RT; ++rt) {
+            if constexpr (TY == 8) {  // Q8_0: 34-byte blocks, f16 d then 32 int8
+                const uint16_t *q = (const uint16_t *) (wa[rt] + 34u * b + 2u + 8u * lq);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) o.d[k] = *(const uint16_t *) (wd[k] + 34u * b);
-        } else {  // F16
-            const uint16_t *h = (const uint16_t *) (wa + 2u * (32u * b + 8u * lq));
+                for (int i = 0; i < 4; ++i) o.a[rt][i] = q[i];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o.a[i] = h[i];
+                for (int k = 0; k < 4; ++k) o.d[rt][k] = *(const uint16_t *) (wd[rt][k] + 34u * b);
+            } else {  // F16
+                const uint16_t *h = (const uint16_t *) (wa[rt] + 2u * (32u * b + 8u * lq));
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o.a[rt][i] = h[i];
+            }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -67,32 +77,35 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
             o.bl[j] = *(const mm_half8 *) (xl[j] + 32u * b);
         }
     };
-    auto operand_a = [&](const Ops &o) {
+    auto operand_a = [&](const Ops &o, int rt) {
         mm_half8 A;
         if constexpr (TY == 8) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                A[2 * i] = (_Float16) (int8_t) (o.a[i] & 0xFFu);
-                A[2 * i + 1] = (_Float16) (int8_t) (o.a[i] >> 8);
+                A[2 * i] = (_Float16) (int8_t) (o.a[rt][i] & 0xFFu);
+                A[2 * i + 1] = (_Float16) (int8_t) (o.a[rt][i] >> 8);
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) A[i] = __builtin_bit_cast(_Float16, o.a[i]);
+            for (int i = 0; i < 8; ++i) A[i] = __builtin_bit_cast(_Float16, o.a[rt][i]);
         }
         return A;
     };
     auto compute = [&](const Ops &o) {
-        const mm_half8 A = operand_a(o);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if constexpr (TY == 8) {
-                float4_t s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bl[j], s, 0, 0, 0);
+        for (int rt = 0; rt < RT; ++rt) {
+            const mm_half8 A = operand_a(o, rt);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) acc[j][k] = fmaf(mm_f16(o.d[k]), s[k], acc[j][k]);
-            } else {
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bh[j], acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bl[j], acc[j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (TY == 8) {
+                    float4_t s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bl[j], s, 0, 0, 0);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc[rt][j][k] = fmaf(mm_f16(o.d[rt][k]), s[k], acc[rt][j][k]);
+                } else {
+                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bh[j], acc[rt][j], 0, 0, 0);
+                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bl[j], acc[rt][j], 0, 0, 0);
+                }
             }
         }
     };
@@ -111,21 +124,27 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     }
     if (b < nb) compute(p);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t t = t0 + 16u * j + lr;
-        if (t >= a.n_tok) continue;
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t r = r0 + 4u * lq + k;
-            if (r < a.rows) a.y[(uint64_t) t * a.y_stride + r] = a.bias ? acc[j][k] + a.bias[r] : acc[j][k];
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = t0 + 16u * j + lr;
+            if (t >= a.n_tok) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t r = r0 + 16u * rt + 4u * lq + k;
+                if (r < a.rows)
+                    a.y[(uint64_t) t * a.y_stride + r] = a.bias ? acc[rt][j][k] + a.bias[r] : acc[rt][j][k];
+            }
         }
-    }
 }
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_k(MatmulArgs a) { matmul_body<8>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_k(MatmulArgs a) { matmul_body<1>(a); }
+// _r1: 16 rows per wave (more work-groups, for short chunks); _r2: 32 rows per wave.
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r1_k(MatmulArgs a) { matmul_body<8, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r2_k(MatmulArgs a) { matmul_body<8, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r1_k(MatmulArgs a) { matmul_body<1, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r2_k(MatmulArgs a) { matmul_body<1, 2>(a); }
 
 // x -> (hi, lo) f16 with hi = f16(x), lo = f16(x - hi), both round-to-nearest-even.
 extern "C" __global__ void moearc_split_f16_k(const float *x, uint16_t *hi, uint16_t *lo, uint64_t n) {

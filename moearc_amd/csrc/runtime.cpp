@@ -85,7 +85,7 @@ struct moearc_ctx {
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr;
-    hipFunction_t f_mm_q8 = nullptr, f_mm_f16 = nullptr, f_split = nullptr;
+    hipFunction_t f_mm_q8[2] = {}, f_mm_f16[2] = {}, f_split = nullptr;  // 16 / 32 rows per wave
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
@@ -443,8 +443,10 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_dec_fast[6], "moearc_attn_decode_f16d64_k2w4"},
         {&c->f_dec_merge, "moearc_attn_decode_merge"},
         {&c->f_add, "moearc_add_k"},
-        {&c->f_mm_q8, "moearc_matmul_q8_0_k"},
-        {&c->f_mm_f16, "moearc_matmul_f16_k"},
+        {&c->f_mm_q8[0], "moearc_matmul_q8_0_r1_k"},
+        {&c->f_mm_q8[1], "moearc_matmul_q8_0_r2_k"},
+        {&c->f_mm_f16[0], "moearc_matmul_f16_r1_k"},
+        {&c->f_mm_f16[1], "moearc_matmul_f16_r2_k"},
         {&c->f_split, "moearc_split_f16_k"},
     };
     for (auto &f : fns) {
@@ -1031,9 +1033,13 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     a.cols = (uint32_t) n_cols;
     a.n_tok = (uint32_t) n_tok;
     a.y_stride = (uint32_t) y_stride;
-    return launch2d(c, ty == 8u ? c->f_mm_q8 : c->f_mm_f16,
-                    (unsigned) ((n_rows + MOEARC_MM_ROWS - 1) / MOEARC_MM_ROWS),
-                    (unsigned) ((n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS), 256, a, what, n_rows, n_tok);
+    // 32 rows per wave halves the activation loads per MFMA, but only pays while the launch still
+    // has about two work-groups per CU; shorter chunks take 16 rows per wave.
+    const unsigned long tok_groups = (n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS;
+    const int r2 = ((n_rows + 127) / 128) * tok_groups >= 512 ? 1 : 0;
+    const unsigned long rows_per_wg = r2 ? 128 : 64;
+    return launch2d(c, ty == 8u ? c->f_mm_q8[r2] : c->f_mm_f16[r2], (unsigned) ((n_rows + rows_per_wg - 1) / rows_per_wg),
+                    (unsigned) tok_groups, 256, a, what, n_rows, n_tok);
 }
 
 // The f16 hi / lo split of x (n floats) into the context's buffer; returns its two halves.

@@ -207,7 +207,9 @@ def test_matvec_refusals_and_empty_shapes(ctx):
 
 @pytest.mark.parametrize("ty,n_tok,rows,cols", [
     (QuantType.Q8_0, 37, 200, 1024), (QuantType.Q8_0, 130, 512, 2880), (QuantType.F16, 67, 96, 512),
-    (QuantType.Q8_0, 2, 4096, 2880), (QuantType.F16, 129, 2880, 4096)], ids=str)
+    (QuantType.Q8_0, 2, 4096, 2880), (QuantType.F16, 129, 2880, 4096),
+    # enough work-groups for the 32-rows-per-wave kernels
+    (QuantType.Q8_0, 512, 8192, 256), (QuantType.F16, 256, 16384, 128)], ids=str)
 def test_chunk_matmul_meets_the_matvec_bound(ctx, ty, n_tok, rows, cols):
     # the MFMA product of a chunk, token by token against the oracle's matvec, at the same bound
     w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x3A3 + rows)
