@@ -22,39 +22,32 @@ __device__ __forceinline__ float mm_f16(uint16_t b) { return (float) __builtin_b
 
 template <uint32_t TY, int RT>
 __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    // The work-group's activation tile of one k-block (64 tokens x 32 k, hi and lo) is staged in
+    // LDS once and read by all four waves: fragment (quarter q, token t) at 16-byte slot q*64 + t,
+    // so the 64 lanes of a fragment read touch 64 consecutive slots. Two buffers; one barrier per
+    // k-block. Each thread copies the quarter tid/64 of token tid%64, hi and lo.
+    __shared__ u32x4_t bsm[2][2][256];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t lr = lane & 15u, lq = lane >> 4;
     const uint32_t r0 = blockIdx.x * (64u * RT) + 16u * RT * wave;  // RT 16-row tiles per wave
     const uint32_t t0 = blockIdx.y * MOEARC_MM_TOKENS;
-    if (r0 >= a.rows) return;  // whole wave past the last row (no barrier in this kernel)
     const uint32_t nb = a.cols / 32u;
-    const uint8_t *wa[RT], *wd[RT][4];
+    const uint8_t *wa[RT];  // this lane's A row (clamped: waves past the last row still stage)
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        wa[rt] = a.w + (uint64_t) min(r0 + 16u * rt + lr, a.rows - 1u) * a.row_bytes;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            wd[rt][k] = a.w + (uint64_t) min(r0 + 16u * rt + 4u * lq + k, a.rows - 1u) * a.row_bytes;
-    }
-    const uint16_t *xh[4], *xl[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint64_t t = min(t0 + 16u * j + lr, a.n_tok - 1u);
-        xh[j] = a.xh + t * a.cols + 8u * lq;
-        xl[j] = a.xl + t * a.cols + 8u * lq;
-    }
+    for (int rt = 0; rt < RT; ++rt) wa[rt] = a.w + (uint64_t) min(r0 + 16u * rt + lr, a.rows - 1u) * a.row_bytes;
+    const uint64_t ct = min(t0 + (tid & 63u), a.n_tok - 1u);
+    const uint16_t *cxh = a.xh + ct * a.cols + 8u * (tid >> 6);
+    const uint16_t *cxl = a.xl + ct * a.cols + 8u * (tid >> 6);
     float4_t acc[RT][4];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[rt][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // One k-block ahead: block b + 1's operands are loaded (unconditionally, the last block's
-    // again at the end, so the wait counts are static) before block b's products.
-    struct Ops {  // raw loaded words: converted only when used, so a load never waits early
+    struct Ops {  // raw loaded words, converted only when used, so a load never waits early
         uint16_t a[RT][8];
-        uint16_t d[RT][4];
-        mm_half8 bh[4], bl[4];
+        uint16_t d[RT];      // the block scale of this lane's A row
+        u32x4_t xh, xl;      // this thread's share of the next activation tile
     };
     auto load = [&](uint32_t b, Ops &o) {
 #pragma unroll
@@ -63,19 +56,19 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                 const uint16_t *q = (const uint16_t *) (wa[rt] + 34u * b + 2u + 8u * lq);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o.a[rt][i] = q[i];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) o.d[rt][k] = *(const uint16_t *) (wd[rt][k] + 34u * b);
+                o.d[rt] = *(const uint16_t *) (wa[rt] + 34u * b);
             } else {  // F16
                 const uint16_t *h = (const uint16_t *) (wa[rt] + 2u * (32u * b + 8u * lq));
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o.a[rt][i] = h[i];
             }
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            o.bh[j] = *(const mm_half8 *) (xh[j] + 32u * b);
-            o.bl[j] = *(const mm_half8 *) (xl[j] + 32u * b);
-        }
+        o.xh = *(const u32x4_t *) (cxh + 32u * b);
+        o.xl = *(const u32x4_t *) (cxl + 32u * b);
+    };
+    auto stage = [&](const Ops &o, uint32_t buf) {
+        bsm[buf][0][(tid >> 6) * 64u + (tid & 63u)] = o.xh;
+        bsm[buf][1][(tid >> 6) * 64u + (tid & 63u)] = o.xl;
     };
     auto operand_a = [&](const Ops &o, int rt) {
         mm_half8 A;
@@ -91,38 +84,57 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
         }
         return A;
     };
-    auto compute = [&](const Ops &o) {
+    auto compute = [&](const Ops &o, uint32_t buf) {
+        mm_half8 bh[4], bl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bh[j] = __builtin_bit_cast(mm_half8, bsm[buf][0][lq * 64u + 16u * j + lr]);
+            bl[j] = __builtin_bit_cast(mm_half8, bsm[buf][1][lq * 64u + 16u * j + lr]);
+        }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const mm_half8 A = operand_a(o, rt);
+            float dk[4];
+            if constexpr (TY == 8) {  // scales of accumulator rows 4 lq + k, from the lanes holding them
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    dk[k] = mm_f16((uint16_t) __builtin_amdgcn_ds_bpermute((int) ((4u * lq + k) << 2), (int) o.d[rt]));
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 if constexpr (TY == 8) {
-                    float4_t s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bl[j], s, 0, 0, 0);
+                    float4_t s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], s, 0, 0, 0);
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) acc[rt][j][k] = fmaf(mm_f16(o.d[rt][k]), s[k], acc[rt][j][k]);
+                    for (int k = 0; k < 4; ++k) acc[rt][j][k] = fmaf(dk[k], s[k], acc[rt][j][k]);
                 } else {
-                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bh[j], acc[rt][j], 0, 0, 0);
-                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, o.bl[j], acc[rt][j], 0, 0, 0);
+                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], acc[rt][j], 0, 0, 0);
+                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], acc[rt][j], 0, 0, 0);
                 }
             }
         }
     };
-    // Ping-pong: the loads of one buffer are issued (and kept in place by a scheduling barrier)
-    // before the other buffer's products; an odd block count leaves a last block for buffer p.
+    // Ping-pong: block b + 1's operands are requested (clamped at the end, so every iteration
+    // issues the same loads) before block b's products; they reach LDS after them, then the
+    // work-group meets once.
     Ops p, q;
     load(0, p);
+    stage(p, 0);
+    __syncthreads();
     uint32_t b = 0;
     for (; b + 1u < nb; b += 2u) {
         load(b + 1u, q);
         __builtin_amdgcn_sched_barrier(0);
-        compute(p);
+        compute(p, 0);
+        stage(q, 1);
+        __syncthreads();
         load(min(b + 2u, nb - 1u), p);
         __builtin_amdgcn_sched_barrier(0);
-        compute(q);
+        compute(q, 1);
+        stage(p, 0);
+        __syncthreads();
     }
-    if (b < nb) compute(p);
+    if (b < nb) compute(p, 0);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
