@@ -175,11 +175,13 @@ struct MatvecArgs {
 };
 
 // Chunk-form projections (matmul.hip): Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the n_tok
-// tokens of a prompt chunk, W Q8_0 (type 8) or F16 (type 1), X given as its f16 hi + lo split.
+// tokens of a prompt chunk, W Q8_0 (8), F16 (1), Q4_K (12), Q5_K (13) or MXFP4 (39), X given as its
+// f16 hi + lo split.
 #define MOEARC_MM_TOKENS 64    // tokens per work-group
 struct MatmulArgs {
     const uint8_t *w;
     const uint16_t *xh, *xl;   // [n_tok][cols] f16: x = hi + lo to within 2^-22 |x|
+    const float *xs;           // [n_tok][cols / 32] block sums of x (Q4_K, Q5_K), else null
     const float *bias;         // [rows] or null
     float *y;                  // [n_tok][y_stride]
     uint64_t row_bytes;

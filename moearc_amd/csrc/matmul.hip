@@ -27,6 +27,7 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     // so the 64 lanes of a fragment read touch 64 consecutive slots. Two buffers; one barrier per
     // k-block. Each thread copies the quarter tid/64 of token tid%64, hi and lo.
     __shared__ u32x4_t bsm[2][2][256];
+    __shared__ float xsm[2][64];  // K-quants: the tile's per-token block sums
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t lr = lane & 15u, lq = lane >> 4;
     const uint32_t r0 = blockIdx.x * (64u * RT) + 16u * RT * wave;  // RT 16-row tiles per wave
@@ -45,9 +46,14 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
         for (int j = 0; j < 4; ++j) acc[rt][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     struct Ops {  // raw loaded words, converted only when used, so a load never waits early
-        uint16_t a[RT][8];
-        uint16_t d[RT];      // the block scale of this lane's A row
+        uint16_t a[RT][8];   // Q8_0 / Q4_K / Q5_K payload words, F16 halves
+        uint16_t h[RT][4];   // Q5_K fifth bits
+        uint16_t d[RT][2];   // Q8_0 d; K-quant d, dmin
+        uint8_t sc[RT][3];   // K-quant scale bytes of the sub-block
+        uint32_t mx[RT][3];  // MXFP4: the aligned dwords around this lane's 8 payload bytes
+        uint8_t e[RT];       // MXFP4 exponent
         u32x4_t xh, xl;      // this thread's share of the next activation tile
+        float xsum;          // threads 0..63: the block sum of token tid
     };
     auto load = [&](uint32_t b, Ops &o) {
 #pragma unroll
@@ -56,21 +62,51 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                 const uint16_t *q = (const uint16_t *) (wa[rt] + 34u * b + 2u + 8u * lq);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o.a[rt][i] = q[i];
-                o.d[rt] = *(const uint16_t *) (wa[rt] + 34u * b);
-            } else {  // F16
+                o.d[rt][0] = *(const uint16_t *) (wa[rt] + 34u * b);
+            } else if constexpr (TY == 1) {  // F16
                 const uint16_t *h = (const uint16_t *) (wa[rt] + 2u * (32u * b + 8u * lq));
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o.a[rt][i] = h[i];
+            } else if constexpr (TY == 12 || TY == 13) {  // K-quants: sub-block s of super-block b / 8
+                const uint32_t s = b & 7u;
+                const uint8_t *sb = wa[rt] + (TY == 12 ? 144u : 176u) * (b >> 3);
+                const uint16_t *q = (const uint16_t *) (sb + (TY == 12 ? 16u : 48u) + 32u * (s >> 1) + 8u * lq);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o.a[rt][i] = q[i];
+                if constexpr (TY == 13) {
+                    const uint16_t *qh = (const uint16_t *) (sb + 16u + 8u * lq);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o.h[rt][i] = qh[i];
+                }
+                o.d[rt][0] = *(const uint16_t *) sb;
+                o.d[rt][1] = *(const uint16_t *) (sb + 2u);
+                o.sc[rt][0] = sb[4u + (s & 3u)];
+                o.sc[rt][1] = sb[8u + (s & 3u)];
+                o.sc[rt][2] = sb[12u + (s & 3u)];
+            } else {  // MXFP4: 17-byte blocks, E8M0 exponent then 16 bytes of nibble pairs
+                const uint8_t *blk = wa[rt] + 17u * b;
+                const uintptr_t at = (uintptr_t) (blk + 1u + 8u * (lq & 1u));
+                const uint32_t *w4 = (const uint32_t *) (at & ~(uintptr_t) 3);
+                o.mx[rt][0] = w4[0];
+                o.mx[rt][1] = w4[1];
+                // the third dword only holds wanted bytes when the eight are unaligned; otherwise
+                // it could lie past the matrix, so the second is read again
+                o.mx[rt][2] = w4[(at & 3u) ? 2 : 1];
+                o.e[rt] = blk[0];
             }
         }
         o.xh = *(const u32x4_t *) (cxh + 32u * b);
         o.xl = *(const u32x4_t *) (cxl + 32u * b);
+        if constexpr (TY == 12 || TY == 13)
+            o.xsum = a.xs[ct * nb + b];
     };
     auto stage = [&](const Ops &o, uint32_t buf) {
         bsm[buf][0][(tid >> 6) * 64u + (tid & 63u)] = o.xh;
         bsm[buf][1][(tid >> 6) * 64u + (tid & 63u)] = o.xl;
+        if constexpr (TY == 12 || TY == 13)
+            if (tid < 64u) xsm[buf][tid] = o.xsum;
     };
-    auto operand_a = [&](const Ops &o, int rt) {
+    auto operand_a = [&](const Ops &o, int rt, uint32_t b) {
         mm_half8 A;
         if constexpr (TY == 8) {
 #pragma unroll
@@ -78,38 +114,92 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                 A[2 * i] = (_Float16) (int8_t) (o.a[rt][i] & 0xFFu);
                 A[2 * i + 1] = (_Float16) (int8_t) (o.a[rt][i] >> 8);
             }
-        } else {
+        } else if constexpr (TY == 1) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) A[i] = __builtin_bit_cast(_Float16, o.a[rt][i]);
+        } else if constexpr (TY == 12 || TY == 13) {  // nibble (+ fifth bit), exact small integers
+            const uint32_t s = b & 7u, sh = 4u * (s & 1u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    uint32_t q = ((uint32_t) (o.a[rt][i] >> (8 * half)) >> sh) & 0xFu;
+                    if constexpr (TY == 13) q |= (((uint32_t) (o.h[rt][i] >> (8 * half)) >> s) & 1u) << 4;
+                    A[2 * i + half] = (_Float16) (uint16_t) q;
+                }
+            }
+        } else {  // MXFP4: E2M1 code points as f16 bits (exact)
+            const uintptr_t at = (uintptr_t) (wa[rt] + 17u * b + 1u + 8u * (lq & 1u));
+            const uint32_t sh = (uint32_t) (at & 3u);
+            const uint32_t lo = __builtin_amdgcn_alignbyte(o.mx[rt][1], o.mx[rt][0], sh);
+            const uint32_t hi = __builtin_amdgcn_alignbyte(o.mx[rt][2], o.mx[rt][1], sh);
+            const uint32_t nsh = 4u * (lq >> 1);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t byte = ((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xFFu;
+                const uint32_t c = (byte >> nsh) & 0xFu, mag = c & 7u;
+                const uint32_t bits = mag == 0u ? 0u : mag == 1u ? 0x3800u : (((mag >> 1) + 14u) << 10) | ((mag & 1u) << 9);
+                A[i] = __builtin_bit_cast(_Float16, (uint16_t) (bits | ((c & 8u) << 12)));
+            }
         }
         return A;
     };
-    auto compute = [&](const Ops &o, uint32_t buf) {
+    // Per-row scale (and min) of this lane's A row for k-block b; moved to the accumulator rows
+    // 4 lq + k with ds_bpermute.
+    auto row_scales = [&](const Ops &o, int rt, uint32_t b, float &sc1, float &mn1) {
+        if constexpr (TY == 8) {
+            sc1 = mm_f16(o.d[rt][0]);
+            mn1 = 0.f;
+        } else if constexpr (TY == 12 || TY == 13) {
+            const uint32_t s = b & 7u;
+            const uint32_t r0b = o.sc[rt][0], r1b = o.sc[rt][1], r2b = o.sc[rt][2];
+            const bool low = s < 4u;  // get_scale_min_k4 (reference.rs:150-160)
+            const uint32_t sc = low ? (r0b & 63u) : ((r2b & 0xFu) | ((r0b >> 6) << 4));
+            const uint32_t m = low ? (r1b & 63u) : ((r2b >> 4) | ((r1b >> 6) << 4));
+            sc1 = mm_f16(o.d[rt][0]) * (float) sc;
+            mn1 = mm_f16(o.d[rt][1]) * (float) m;
+        } else {  // MXFP4: 2^(e - 127)
+            sc1 = __uint_as_float(o.e[rt] ? (uint32_t) o.e[rt] << 23 : 0x00400000u);
+            mn1 = 0.f;
+        }
+    };
+    auto compute = [&](const Ops &o, uint32_t buf, uint32_t b) {
         mm_half8 bh[4], bl[4];
+        float xsv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             bh[j] = __builtin_bit_cast(mm_half8, bsm[buf][0][lq * 64u + 16u * j + lr]);
             bl[j] = __builtin_bit_cast(mm_half8, bsm[buf][1][lq * 64u + 16u * j + lr]);
+            if constexpr (TY == 12 || TY == 13) xsv[j] = xsm[buf][16u * j + lr];
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            const mm_half8 A = operand_a(o, rt);
-            float dk[4];
-            if constexpr (TY == 8) {  // scales of accumulator rows 4 lq + k, from the lanes holding them
+            const mm_half8 A = operand_a(o, rt, b);
+            float dk[4], mk[4];
+            if constexpr (TY != 1) {
+                float sc1, mn1;
+                row_scales(o, rt, b, sc1, mn1);
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    dk[k] = mm_f16((uint16_t) __builtin_amdgcn_ds_bpermute((int) ((4u * lq + k) << 2), (int) o.d[rt]));
+                for (int k = 0; k < 4; ++k) {
+                    const int src = (int) ((4u * lq + k) << 2);
+                    dk[k] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(sc1)));
+                    if constexpr (TY == 12 || TY == 13)
+                        mk[k] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(mn1)));
+                }
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if constexpr (TY == 8) {
+                if constexpr (TY == 1) {
+                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], acc[rt][j], 0, 0, 0);
+                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], acc[rt][j], 0, 0, 0);
+                } else {
                     float4_t s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], s, 0, 0, 0);
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) acc[rt][j][k] = fmaf(dk[k], s[k], acc[rt][j][k]);
-                } else {
-                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], acc[rt][j], 0, 0, 0);
-                    acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], acc[rt][j], 0, 0, 0);
+                    for (int k = 0; k < 4; ++k) {
+                        acc[rt][j][k] = fmaf(dk[k], s[k], acc[rt][j][k]);
+                        if constexpr (TY == 12 || TY == 13) acc[rt][j][k] = fmaf(-mk[k], xsv[j], acc[rt][j][k]);
+                    }
                 }
             }
         }
@@ -125,16 +215,16 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     for (; b + 1u < nb; b += 2u) {
         load(b + 1u, q);
         __builtin_amdgcn_sched_barrier(0);
-        compute(p, 0);
+        compute(p, 0, b);
         stage(q, 1);
         __syncthreads();
         load(min(b + 2u, nb - 1u), p);
         __builtin_amdgcn_sched_barrier(0);
-        compute(q, 1);
+        compute(q, 1, b + 1u);
         stage(p, 0);
         __syncthreads();
     }
-    if (b < nb) compute(p, 0);
+    if (b < nb) compute(p, 0, b);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -153,6 +243,12 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
 }  // namespace
 
 // _r1: 16 rows per wave (more work-groups, for short chunks); _r2: 32 rows per wave.
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r1_k(MatmulArgs a) { matmul_body<12, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r2_k(MatmulArgs a) { matmul_body<12, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r1_k(MatmulArgs a) { matmul_body<13, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r2_k(MatmulArgs a) { matmul_body<13, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r1_k(MatmulArgs a) { matmul_body<39, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r2_k(MatmulArgs a) { matmul_body<39, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r1_k(MatmulArgs a) { matmul_body<8, 1>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r2_k(MatmulArgs a) { matmul_body<8, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r1_k(MatmulArgs a) { matmul_body<1, 1>(a); }
@@ -167,5 +263,18 @@ extern "C" __global__ void moearc_split_f16_k(const float *x, uint16_t *hi, uint
         const _Float16 l = (_Float16) (v - (float) h);
         hi[i] = __builtin_bit_cast(uint16_t, h);
         lo[i] = __builtin_bit_cast(uint16_t, l);
+    }
+}
+
+// xs[i] = the sum of x[32 i .. 32 i + 31], in order, in f32: the per-(token, k-block) activation
+// sums of the K-quant chunk products.
+extern "C" __global__ void moearc_block_sums_k(const float *x, float *xs, uint64_t n_blocks) {
+    for (uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n_blocks;
+         i += (uint64_t) gridDim.x * blockDim.x) {
+        const float *p = x + 32u * i;
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) t += p[j];
+        xs[i] = t;
     }
 }

@@ -85,7 +85,7 @@ struct moearc_ctx {
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr;
-    hipFunction_t f_mm_q8[2] = {}, f_mm_f16[2] = {}, f_split = nullptr;  // 16 / 32 rows per wave
+    hipFunction_t f_mm[5][2] = {}, f_split = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 x 16 / 32 rows per wave
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
@@ -443,10 +443,17 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_dec_fast[6], "moearc_attn_decode_f16d64_k2w4"},
         {&c->f_dec_merge, "moearc_attn_decode_merge"},
         {&c->f_add, "moearc_add_k"},
-        {&c->f_mm_q8[0], "moearc_matmul_q8_0_r1_k"},
-        {&c->f_mm_q8[1], "moearc_matmul_q8_0_r2_k"},
-        {&c->f_mm_f16[0], "moearc_matmul_f16_r1_k"},
-        {&c->f_mm_f16[1], "moearc_matmul_f16_r2_k"},
+        {&c->f_mm[0][0], "moearc_matmul_q8_0_r1_k"},
+        {&c->f_mm[0][1], "moearc_matmul_q8_0_r2_k"},
+        {&c->f_mm[1][0], "moearc_matmul_f16_r1_k"},
+        {&c->f_mm[1][1], "moearc_matmul_f16_r2_k"},
+        {&c->f_mm[2][0], "moearc_matmul_q4_k_r1_k"},
+        {&c->f_mm[2][1], "moearc_matmul_q4_k_r2_k"},
+        {&c->f_mm[3][0], "moearc_matmul_q5_k_r1_k"},
+        {&c->f_mm[3][1], "moearc_matmul_q5_k_r2_k"},
+        {&c->f_mm[4][0], "moearc_matmul_mxfp4_r1_k"},
+        {&c->f_mm[4][1], "moearc_matmul_mxfp4_r2_k"},
+        {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
     };
     for (auto &f : fns) {
@@ -1010,22 +1017,28 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
 
 namespace {
 
+// Chunk-product formats: index into f_mm, or -1.
+int mm_index(unsigned ty) {
+    return ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 39u ? 4 : -1;
+}
+
 int mm_check(unsigned ty, const void *w, unsigned long n_tok, unsigned long n_rows, unsigned long n_cols) {
-    if (ty != 8u && ty != 1u) return ERR_ARG;
-    if (n_cols % 32 != 0 || ((uintptr_t) w & 1u) || n_rows >= 0x80000000ul || n_tok >= 0x80000000ul ||
-        n_cols >= 0x80000000ul)
+    if (mm_index(ty) < 0) return ERR_ARG;
+    if (n_cols % 32 != 0 || n_cols % moearc_mv_be(ty) != 0 || ((uintptr_t) w & 1u) ||
+        n_rows >= 0x80000000ul || n_tok >= 0x80000000ul || n_cols >= 0x80000000ul)
         return ERR_ARG;
     return OK;
 }
 
 // y = W x over a chunk, x given as its f16 split (xh, xl) of n_tok x n_cols.
 int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, const void *w,
-              const uint16_t *xh, const uint16_t *xl, const float *bias, unsigned long n_tok,
+              const uint16_t *xh, const uint16_t *xl, const float *xs, const float *bias, unsigned long n_tok,
               unsigned long n_rows, unsigned long n_cols, const char *what) {
     MatmulArgs a{};
     a.w = static_cast<const uint8_t *>(w);
     a.xh = xh;
     a.xl = xl;
+    a.xs = xs;
     a.bias = bias;
     a.y = y;
     a.row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
@@ -1038,24 +1051,35 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     const unsigned long tok_groups = (n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS;
     const int r2 = ((n_rows + 127) / 128) * tok_groups >= 512 ? 1 : 0;
     const unsigned long rows_per_wg = r2 ? 128 : 64;
-    return launch2d(c, ty == 8u ? c->f_mm_q8[r2] : c->f_mm_f16[r2], (unsigned) ((n_rows + rows_per_wg - 1) / rows_per_wg),
+    return launch2d(c, c->f_mm[mm_index(ty)][r2], (unsigned) ((n_rows + rows_per_wg - 1) / rows_per_wg),
                     (unsigned) tok_groups, 256, a, what, n_rows, n_tok);
 }
 
-// The f16 hi / lo split of x (n floats) into the context's buffer; returns its two halves.
-int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl) {
-    if (2 * n > c->mm_ws_halves) {
+// The f16 hi / lo split of x (n floats, n a multiple of 32) and its 32-element block sums into
+// the context's buffer.
+int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl, float **xs) {
+    const size_t halves = 2 * n + n / 16;  // hi, lo, then n / 32 floats
+    if (halves > c->mm_ws_halves) {
         if (c->mm_ws) {
             hipStreamSynchronize(c->stream);
             hipFree(c->mm_ws);
             c->mm_ws = nullptr;
             c->mm_ws_halves = 0;
         }
-        if (hipMalloc((void **) &c->mm_ws, 2 * n * sizeof(uint16_t)) != hipSuccess) return ERR;
-        c->mm_ws_halves = 2 * n;
+        if (hipMalloc((void **) &c->mm_ws, halves * sizeof(uint16_t)) != hipSuccess) return ERR;
+        c->mm_ws_halves = halves;
     }
     *xh = c->mm_ws;
     *xl = c->mm_ws + n;
+    *xs = (float *) (c->mm_ws + 2 * n);  // 4-byte aligned: n is a multiple of 32
+    struct {
+        const float *x;
+        float *xs;
+        uint64_t n;
+    } bs{x, *xs, n / 32};
+    if (const int rc = launch(c, c->f_bsums, (unsigned) std::min<size_t>((n / 32 + 255) / 256, 65536), 256, bs,
+                              "block_sums", n / 32, 0))
+        return rc;
     struct {
         const float *x;
         uint16_t *hi, *lo;
@@ -1072,8 +1096,9 @@ int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w
     if (const int rc = mm_check(type_id, w, n_tok, n_rows, n_cols)) return rc;
     if (n_rows == 0 || n_tok == 0) return OK;
     uint16_t *xh, *xl;
-    if (const int rc = mm_split(c, x, n_tok * n_cols, &xh, &xl)) return rc;
-    return mm_launch(c, type_id, y, n_rows, w, xh, xl, bias, n_tok, n_rows, n_cols, "matmul");
+    float *xs;
+    if (const int rc = mm_split(c, x, n_tok * n_cols, &xh, &xl, &xs)) return rc;
+    return mm_launch(c, type_id, y, n_rows, w, xh, xl, xs, bias, n_tok, n_rows, n_cols, "matmul");
 }
 
 namespace {
@@ -1136,11 +1161,12 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
                         mm_check(b->w_type[2], b->w[2], n_tok, kv_rows, E) == OK;
     if (mm_qkv) {
         uint16_t *xh, *xl;
-        if (const int rc = mm_split(c, x, n_tok * E, &xh, &xl)) return rc;
+        float *xs;
+        if (const int rc = mm_split(c, x, n_tok * E, &xh, &xl, &xs)) return rc;
         float *outs[3] = {q, k, v};
         const unsigned long rows[3] = {q_rows, kv_rows, kv_rows};
         for (int i = 0; i < 3; ++i)
-            if (const int rc = mm_launch(c, b->w_type[i], outs[i], rows[i], b->w[i], xh, xl, b->bias[i], n_tok,
+            if (const int rc = mm_launch(c, b->w_type[i], outs[i], rows[i], b->w[i], xh, xl, xs, b->bias[i], n_tok,
                                          rows[i], E, "attn_qkv_mm"))
                 return rc;
     } else {
@@ -1176,8 +1202,9 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     // h += W_o attn (+ bias_o)
     if (n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK) {
         uint16_t *xh, *xl;
-        if (const int rc = mm_split(c, att, nq, &xh, &xl)) return rc;
-        if (const int rc = mm_launch(c, b->w_type[3], proj, E, b->w[3], xh, xl, b->bias[3], n_tok, E, q_rows,
+        float *xs;
+        if (const int rc = mm_split(c, att, nq, &xh, &xl, &xs)) return rc;
+        if (const int rc = mm_launch(c, b->w_type[3], proj, E, b->w[3], xh, xl, xs, b->bias[3], n_tok, E, q_rows,
                                      "attn_proj_mm"))
             return rc;
     } else {
