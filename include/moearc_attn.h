@@ -229,8 +229,9 @@ int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w
  *   attn    = chunked prefill over keys [pos0 + t + 1 - n_swa | 0, pos0 + t + 1)   (moearc_attn_prefill)
  *   h      += W_o attn (+ bias_o)           (moearc_matvec_q per token, moearc_add)
  * with every earlier token's K/V already in the pages. n_tok = 1 is one decode step. All pointers
- * are device memory except `b` itself. The projections of a chunk are run token by token through
- * the batched matvec (up to 32 matrix-vector products per launch). */
+ * are device memory except `b` itself. With two or more tokens, projections whose weights
+ * moearc_matmul_q takes run as one MFMA product each; the others token by token through the
+ * batched matvec (up to 32 matrix-vector products per launch). */
 typedef struct moearc_attn_block {
     unsigned int w_type[4];      /* GGUF type ids of W_q, W_k, W_v, W_o */
     const void *w[4];            /* W_q [n_head*head_dim][n_embd], W_k / W_v [n_head_kv*head_dim][n_embd],
