@@ -208,7 +208,7 @@ int moearc_attn_qkv(moearc_ctx *c, const unsigned int *type_ids, float *const *o
 /* Extension (no counterpart in the reference, which runs one moearc_matvec_q per token): the
  * projections of a prompt chunk as one MFMA matrix product, y[t][r] = sum_c W[r][c] x[t][c]
  * (+ bias[r]) for t < n_tok, r < n_rows; x f32 [n_tok][n_cols], y f32 [n_tok][n_rows]. Weights
- * Q8_0 (8), F16 (1), Q4_K (12), Q5_K (13) or MXFP4 (39), W 2-byte aligned. x enters as an f16
+ * Q8_0 (8), F16 (1), Q4_K (12), Q5_K (13), Q6_K (14) or MXFP4 (39), W 2-byte aligned. x enters as an f16
  * hi + lo pair (to 2^-22 relative; each |x| must stay below 65504), quantised payloads as exact
  * f16 integers / E2M1 values, block scales (and K-quant mins, against f32 block sums of x) in f32:
  * results are within 2 (32 + n_cols/32 + 5) 2^-24 sum|w x| per element (the matvec bound plus the

@@ -83,6 +83,19 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                 o.sc[rt][0] = sb[4u + (s & 3u)];
                 o.sc[rt][1] = sb[8u + (s & 3u)];
                 o.sc[rt][2] = sb[12u + (s & 3u)];
+            } else if constexpr (TY == 14) {  // Q6_K: k-block s = (half n, quarter c) of super-block b / 8
+                const uint32_t s = b & 7u, n = s >> 2, c = s & 3u;
+                const uint8_t *sb = wa[rt] + 210u * (b >> 3);
+                const uint16_t *ql = (const uint16_t *) (sb + 64u * n + 32u * (c & 1u) + 8u * lq);
+                const uint16_t *qh = (const uint16_t *) (sb + 128u + 32u * n + 8u * lq);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    o.a[rt][i] = ql[i];
+                    o.h[rt][i] = qh[i];
+                }
+                o.d[rt][0] = *(const uint16_t *) (sb + 208u);
+                o.sc[rt][0] = sb[192u + 8u * n + 2u * c];
+                o.sc[rt][1] = sb[192u + 8u * n + 2u * c + 1u];
             } else {  // MXFP4: 17-byte blocks, E8M0 exponent then 16 bytes of nibble pairs
                 const uint8_t *blk = wa[rt] + 17u * b;
                 const uintptr_t at = (uintptr_t) (blk + 1u + 8u * (lq & 1u));
@@ -128,6 +141,17 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                     A[2 * i + half] = (_Float16) (uint16_t) q;
                 }
             }
+        } else if constexpr (TY == 14) {  // q - 32 in [-32, 31], exact
+            const uint32_t c = (b & 7u) & 3u, shl = 4u * (c >> 1), shh = 2u * c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const uint32_t lo = ((uint32_t) (o.a[rt][i] >> (8 * half)) >> shl) & 0xFu;
+                    const uint32_t hi = ((uint32_t) (o.h[rt][i] >> (8 * half)) >> shh) & 3u;
+                    A[2 * i + half] = (_Float16) ((int) (lo | (hi << 4)) - 32);
+                }
+            }
         } else {  // MXFP4: E2M1 code points as f16 bits (exact)
             const uintptr_t at = (uintptr_t) (wa[rt] + 17u * b + 1u + 8u * (lq & 1u));
             const uint32_t sh = (uint32_t) (at & 3u);
@@ -158,6 +182,10 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
             const uint32_t m = low ? (r1b & 63u) : ((r2b >> 4) | ((r1b >> 6) << 4));
             sc1 = mm_f16(o.d[rt][0]) * (float) sc;
             mn1 = mm_f16(o.d[rt][1]) * (float) m;
+        } else if constexpr (TY == 14) {  // the two 16-wide groups' d * sc
+            const float d = mm_f16(o.d[rt][0]);
+            sc1 = d * (float) (int8_t) o.sc[rt][0];
+            mn1 = d * (float) (int8_t) o.sc[rt][1];
         } else {  // MXFP4: 2^(e - 127)
             sc1 = __uint_as_float(o.e[rt] ? (uint32_t) o.e[rt] << 23 : 0x00400000u);
             mn1 = 0.f;
@@ -183,7 +211,7 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                 for (int k = 0; k < 4; ++k) {
                     const int src = (int) ((4u * lq + k) << 2);
                     dk[k] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(sc1)));
-                    if constexpr (TY == 12 || TY == 13)
+                    if constexpr (TY == 12 || TY == 13 || TY == 14)
                         mk[k] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(mn1)));
                 }
             }
@@ -192,6 +220,19 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
                 if constexpr (TY == 1) {
                     acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], acc[rt][j], 0, 0, 0);
                     acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], acc[rt][j], 0, 0, 0);
+                } else if constexpr (TY == 14) {
+                    // two 16-wide scale groups in one k-block: lanes 0-31 hold group 0's k, 32-63
+                    // group 1's, so each group's sum is an MFMA with the other group's A zeroed
+                    float4_t sg[2];
+#pragma unroll
+                    for (int g = 0; g < 2; ++g) {
+                        const mm_half8 Ag = (lq >> 1) == (uint32_t) g ? A : mm_half8{};
+                        sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ag, bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ag, bl[j], sg[g], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        acc[rt][j][k] = fmaf(mk[k], sg[1][k], fmaf(dk[k], sg[0][k], acc[rt][j][k]));
                 } else {
                     float4_t s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bh[j], float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     s = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bl[j], s, 0, 0, 0);
@@ -247,6 +288,8 @@ extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r1_k(Matmul
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r2_k(MatmulArgs a) { matmul_body<12, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r1_k(MatmulArgs a) { matmul_body<13, 1>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r2_k(MatmulArgs a) { matmul_body<13, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q6_k_r1_k(MatmulArgs a) { matmul_body<14, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q6_k_r2_k(MatmulArgs a) { matmul_body<14, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r1_k(MatmulArgs a) { matmul_body<39, 1>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r2_k(MatmulArgs a) { matmul_body<39, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r1_k(MatmulArgs a) { matmul_body<8, 1>(a); }

@@ -85,7 +85,7 @@ struct moearc_ctx {
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr;
-    hipFunction_t f_mm[5][2] = {}, f_split = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 x 16 / 32 rows per wave
+    hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
@@ -453,6 +453,8 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm[3][1], "moearc_matmul_q5_k_r2_k"},
         {&c->f_mm[4][0], "moearc_matmul_mxfp4_r1_k"},
         {&c->f_mm[4][1], "moearc_matmul_mxfp4_r2_k"},
+        {&c->f_mm[5][0], "moearc_matmul_q6_k_r1_k"},
+        {&c->f_mm[5][1], "moearc_matmul_q6_k_r2_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
     };
@@ -1019,7 +1021,7 @@ namespace {
 
 // Chunk-product formats: index into f_mm, or -1.
 int mm_index(unsigned ty) {
-    return ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 39u ? 4 : -1;
+    return ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 39u ? 4 : ty == 14u ? 5 : -1;
 }
 
 int mm_check(unsigned ty, const void *w, unsigned long n_tok, unsigned long n_rows, unsigned long n_cols) {

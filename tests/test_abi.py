@@ -48,7 +48,7 @@ def test_code_object_holds_every_kernel_the_runtime_loads():
     src = open(os.path.join(ROOT, "moearc_amd", "csrc", "runtime.cpp")).read()
     kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge)"', src))
     kernels |= {f"moearc_attn_prefill_{v}g{g}" for v in ("", "precise_") for g in (1, 2, 4, 8)}
-    kernels |= {f"moearc_matmul_{t}_r{r}_k" for t in ("q8_0", "f16", "q4_k", "q5_k", "mxfp4") for r in (1, 2)}
+    kernels |= {f"moearc_matmul_{t}_r{r}_k" for t in ("q8_0", "f16", "q4_k", "q5_k", "q6_k", "mxfp4") for r in (1, 2)}
     kernels |= {"moearc_split_f16_k", "moearc_block_sums_k"}
     kernels |= {f"moearc_matvec_{t}_p{p}" for t in ("f32", "f16", "q8_0", "q4_k", "q5_k", "q6_k", "mxfp4")
                 for p in (1, 2, 4)}
