@@ -226,7 +226,8 @@ int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w
  *   q, k, v = W_{q,k,v} x (+ biases)        (moearc_attn_qkv, per token)
  *   q, k    = NeoX RoPE at pos[t]           (moearc_rope; K fused with the append below)
  *   K, V    -> pages[page_ids[t]], slot slots[t], f16   (moearc_rope_kv_append_chunk)
- *   attn    = chunked prefill over keys [pos0 + t + 1 - n_swa | 0, pos0 + t + 1)   (moearc_attn_prefill)
+ *   attn    = chunked prefill over keys [pos0 + t + 1 - n_swa | 0, pos0 + t + 1)   (moearc_attn_prefill;
+ *             a single token: moearc_attn_decode with its f32 q, the engine's own decode call)
  *   h      += W_o attn (+ bias_o)           (moearc_matvec_q per token, moearc_add)
  * with every earlier token's K/V already in the pages. n_tok = 1 is one decode step. All pointers
  * are device memory except `b` itself. With two or more tokens, projections whose weights

@@ -1187,20 +1187,28 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
             if (const int rc = mv_launch_all(c, b->w_type[i], jobs, E, "attn_qkv_chunk")) return rc;
         }
     }
-    // RoPE of q, narrowed to f16 for the prefill kernel; RoPE of K fused with the K/V append
+    // RoPE of q (narrowed to f16 for the prefill kernel when there is a chunk); RoPE of K fused
+    // with the K/V append
     if (const int rc = moearc_rope(c, qr, q, pos, n_tok, H, D, b->n_rot, b->freq_base, b->freq_scale,
                                    b->ext_factor, b->attn_factor, b->corr_lo, b->corr_hi, 1))
         return rc;
-    if (const int rc = moearc_quantize_f16(c, q16, qr, nq)) return rc;
+    if (n_tok > 1)
+        if (const int rc = moearc_quantize_f16(c, q16, qr, nq)) return rc;
     if (const int rc = moearc_rope_kv_append_chunk(c, b->k_pages, b->v_pages, k, v, pos, page_ids, slots,
                                                    n_tok, G, D, b->page_tokens, b->n_rot, b->freq_base,
                                                    b->freq_scale, b->ext_factor, b->attn_factor,
                                                    b->corr_lo, b->corr_hi, 1, 1u))
         return rc;
-    if (const int rc = moearc_attn_prefill(c, att, MOEARC_OUT_F32, q16, b->k_pages, b->v_pages,
-                                           b->block_table, b->sinks, n_tok, pos0, b->n_swa, H, G, D,
-                                           b->page_tokens, b->scale, 1u))
+    if (n_tok == 1) {  // one decode step: the split-K decode kernel, f32 q (moe.rs:2044-2060)
+        const unsigned long n_kv = pos0 + 1, kv_begin = b->n_swa && n_kv > b->n_swa ? n_kv - b->n_swa : 0;
+        if (const int rc = moearc_attn_decode(c, att, qr, b->k_pages, b->v_pages, b->block_table, b->sinks, H, G,
+                                              D, kv_begin, n_kv, b->page_tokens, b->scale, 1u))
+            return rc;
+    } else if (const int rc = moearc_attn_prefill(c, att, MOEARC_OUT_F32, q16, b->k_pages, b->v_pages,
+                                                  b->block_table, b->sinks, n_tok, pos0, b->n_swa, H, G, D,
+                                                  b->page_tokens, b->scale, 1u)) {
         return rc;
+    }
     // h += W_o attn (+ bias_o)
     if (n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK) {
         uint16_t *xh, *xl;

@@ -77,7 +77,8 @@ class Block:
         for t in range(n):
             oracle.kv_append_raw(self.kp, self.vp, kr[t], v[t], int(pages[t]), int(slots[t]), G, D, PT,
                                  oracle.KV_F16)
-        q16 = qr.astype(np.float16).astype(np.float32).reshape(n, H, D)
+        # a chunk's q enters the prefill kernel in f16; a single token's stays f32 (the decode call)
+        q16 = (qr.astype(np.float16).astype(np.float32) if n > 1 else qr).reshape(n, H, D)
         att = oracle.attn_prefill(q16, self.kp, self.vp, table, n, pos0, self.n_swa, H, G, D, PT,
                                   1.0 / np.sqrt(D), sinks=self.sinks, n_threads=8).reshape(n, H * D)
         r, c = self.shapes[3]
