@@ -228,7 +228,7 @@ int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w
  *   K, V    -> pages[page_ids[t]], slot slots[t], f16   (moearc_rope_kv_append_chunk)
  *   attn    = chunked prefill over keys [pos0 + t + 1 - n_swa | 0, pos0 + t + 1)   (moearc_attn_prefill;
  *             a single token: moearc_attn_decode with its f32 q, the engine's own decode call)
- *   h      += W_o attn (+ bias_o)           (moearc_matvec_q per token, moearc_add)
+ *   h      += W_o attn (+ bias_o)           (as moearc_attn_out, the residual add in the store)
  * with every earlier token's K/V already in the pages. n_tok = 1 is one decode step. All pointers
  * are device memory except `b` itself. With two or more tokens, projections whose weights
  * moearc_matmul_q takes run as one MFMA product each; the others token by token through the
@@ -256,6 +256,13 @@ typedef struct moearc_attn_block {
 int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h, const float *x,
                             unsigned long n_tok, unsigned long pos0, const int *pos,
                             const unsigned int *page_ids, const unsigned int *slots);
+
+/* Extension (no counterpart in the reference, which runs moearc_matvec_q, then moearc_add of the bias
+ * and moearc_add into the residual for attn.proj, moe.rs:2063-2071): h[r] += W[r] . attn (+ bias[r])
+ * for r < n_rows in one launch, bit-identical to that sequence. Refusals: null c/h/w/attn -> -1;
+ * those of moearc_matvec_q -> -2. */
+int moearc_attn_out(moearc_ctx *c, unsigned int type_id, float *h, const void *w, const float *bias,
+                    const float *attn, unsigned long n_rows, unsigned long n_cols);
 
 /* The stream the context enqueues on (a hipStream_t), so a caller can order its own work. */
 void *moearc_ctx_stream(moearc_ctx *c);

@@ -421,6 +421,16 @@ class Context:
                                               bias.ptr if bias is not None else None, n_tok, n_rows, n_cols),
                     f"matmul {ty.name}")
 
+    def attn_out(self, ty, h: DeviceBuffer, w: DeviceBuffer, bias: Optional[DeviceBuffer], attn: DeviceBuffer,
+                 n_rows: int, n_cols: int) -> None:
+        """h += W attn (+ bias) in one launch (attn.proj and the residual add, moe.rs:2063-2071)."""
+        ty = QuantType(ty)
+        w.require("weights", n_rows * ty.row_bytes(n_cols))
+        attn.require("attention output", n_cols * 4)
+        h.require("residual", n_rows * 4)
+        self.finish(self._lib.moearc_attn_out(self.raw, int(ty), h.ptr, w.ptr, bias.ptr if bias is not None else None,
+                                              attn.ptr, n_rows, n_cols), f"attn out {ty.name}")
+
     def attn_block_chunk(self, desc: "AttnBlockDesc", h: DeviceBuffer, x: DeviceBuffer, n_tok: int,
                          pos0: int, pos: DeviceBuffer, page_ids: DeviceBuffer, slots: DeviceBuffer) -> None:
         """The attention half of one block over n_tok prompt tokens (moe.rs:1942-2071, chunked)."""

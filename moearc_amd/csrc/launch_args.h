@@ -172,6 +172,7 @@ struct MatvecArgs {
     uint32_t x_lds_bytes;  // LDS bytes before the waves' staging buffers
     uint32_t wave_buf;     // LDS bytes of one wave's staging buffer
     uint32_t bias_mask;
+    uint32_t res_mask;     // bit s: out[s][r] += the result (the residual add), else out[s][r] = it
 };
 
 // Chunk-form projections (matmul.hip): Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the n_tok
@@ -186,4 +187,5 @@ struct MatmulArgs {
     float *y;                  // [n_tok][y_stride]
     uint64_t row_bytes;
     uint32_t rows, cols, n_tok, y_stride;
+    uint32_t accumulate;       // 1: y[t][r] += the result (the residual add), else y[t][r] = it
 };

@@ -275,8 +275,11 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint32_t r = r0 + 16u * rt + 4u * lq + k;
-                if (r < a.rows)
-                    a.y[(uint64_t) t * a.y_stride + r] = a.bias ? acc[rt][j][k] + a.bias[r] : acc[rt][j][k];
+                if (r < a.rows) {
+                    float *yp = a.y + (uint64_t) t * a.y_stride + r;
+                    const float v = a.bias ? acc[rt][j][k] + a.bias[r] : acc[rt][j][k];
+                    *yp = a.accumulate ? *yp + v : v;
+                }
             }
         }
 }

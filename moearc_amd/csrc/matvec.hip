@@ -407,6 +407,7 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
         // The row's bias (a.bias[seg] points at readable memory even without one) is requested
         // before the next loads so that waiting for it never waits for them.
         const float bv = a.bias[seg][r];
+        const float rv = a.out[seg][r];  // the residual, when the result is added to it
         issue(min(u + 2u, units - 1u), g, delta_ref, ng_ref);
         __builtin_amdgcn_wave_barrier();
         if (u == 0 || n_slabs > 1u) load_x(sl);
@@ -423,7 +424,10 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
         __builtin_amdgcn_wave_barrier();
         if (sl + 1u == n_slabs) {
             acc = wave_sum_to_lane63(acc);
-            if (lane == 63u) a.out[seg][r] = (a.bias_mask >> seg) & 1u ? acc + bv : acc;
+            if (lane == 63u) {
+                const float y = (a.bias_mask >> seg) & 1u ? acc + bv : acc;
+                a.out[seg][r] = (a.res_mask >> seg) & 1u ? rv + y : y;
+            }
             acc = 0.f;
         }
     };

@@ -710,6 +710,7 @@ struct MvJob {
     const float *bias;
     float *out;
     unsigned long rows;
+    bool residual = false;  // out[r] += the result (out holds the residual)
 };
 
 constexpr unsigned kMvLdsCap = 64u * 1024u;  // dynamic LDS per work-group the launches stay under
@@ -736,6 +737,11 @@ int mv_launch(moearc_ctx *c, unsigned ty, const MvJob *jobs, unsigned n, unsigne
     if (n_cols == 0) {  // empty rows: the sum is 0 (then the bias)
         for (unsigned i = 0; i < n; ++i) {
             if (!jobs[i].rows) continue;
+            if (jobs[i].residual) {  // out += 0 (+ bias)
+                if (jobs[i].bias)
+                    if (const int rc = moearc_add(c, jobs[i].out, jobs[i].out, jobs[i].bias, jobs[i].rows)) return rc;
+                continue;
+            }
             const int rc = jobs[i].bias
                                ? (hipMemcpyAsync(jobs[i].out, jobs[i].bias, jobs[i].rows * 4ul,
                                                  hipMemcpyDeviceToDevice, c->stream) == hipSuccess ? OK : ERR)
@@ -779,6 +785,7 @@ int mv_launch(moearc_ctx *c, unsigned ty, const MvJob *jobs, unsigned n, unsigne
         a.x[i] = jobs[i].x;
         a.bias[i] = jobs[i].bias ? jobs[i].bias : jobs[i].out;
         a.bias_mask |= jobs[i].bias ? 1u << i : 0u;
+        a.res_mask |= jobs[i].residual ? 1u << i : 0u;
         a.out[i] = jobs[i].out;
         a.rows[i] = (uint32_t) jobs[i].rows;
         wgs += (jobs[i].rows + (uint64_t) waves * rpw - 1) / ((uint64_t) waves * rpw);
@@ -845,6 +852,15 @@ int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsign
         uint64_t n;
     } args{out, a, b, n};
     return launch(c, c->f_add, grid, 256, args, "add", n, 0);
+}
+
+int moearc_attn_out(moearc_ctx *c, unsigned int type_id, float *h, const void *w, const float *bias,
+                    const float *attn, unsigned long n_rows, unsigned long n_cols) {
+    if (!c || !h || !w || !attn) return ERR;
+    if (const int rc = mv_check(type_id, n_rows, n_cols)) return rc;
+    if (n_rows == 0) return OK;
+    MvJob j{w, attn, bias, h, n_rows, true};
+    return mv_launch(c, type_id, &j, 1, n_cols, "attn_out", n_rows, 1);
 }
 
 int moearc_attn_qkv(moearc_ctx *c, const unsigned int *type_ids, float *const *out,
@@ -1035,8 +1051,9 @@ int mm_check(unsigned ty, const void *w, unsigned long n_tok, unsigned long n_ro
 // y = W x over a chunk, x given as its f16 split (xh, xl) of n_tok x n_cols.
 int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, const void *w,
               const uint16_t *xh, const uint16_t *xl, const float *xs, const float *bias, unsigned long n_tok,
-              unsigned long n_rows, unsigned long n_cols, const char *what) {
+              unsigned long n_rows, unsigned long n_cols, const char *what, bool accumulate = false) {
     MatmulArgs a{};
+    a.accumulate = accumulate ? 1u : 0u;
     a.w = static_cast<const uint8_t *>(w);
     a.xh = xh;
     a.xl = xl;
@@ -1209,19 +1226,17 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
                                                   b->page_tokens, b->scale, 1u)) {
         return rc;
     }
-    // h += W_o attn (+ bias_o)
+    // h += W_o attn (+ bias_o), the residual add folded into the product's store
+    (void) proj;
     if (n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK) {
         uint16_t *xh, *xl;
         float *xs;
         if (const int rc = mm_split(c, att, nq, &xh, &xl, &xs)) return rc;
-        if (const int rc = mm_launch(c, b->w_type[3], proj, E, b->w[3], xh, xl, xs, b->bias[3], n_tok, E, q_rows,
-                                     "attn_proj_mm"))
-            return rc;
-    } else {
-        std::vector<MvJob> jobs;
-        for (unsigned long t = 0; t < n_tok; ++t)
-            jobs.push_back(MvJob{b->w[3], att + t * q_rows, b->bias[3], proj + t * E, E});
-        if (const int rc = mv_launch_all(c, b->w_type[3], jobs, q_rows, "attn_proj_chunk")) return rc;
+        return mm_launch(c, b->w_type[3], h, E, b->w[3], xh, xl, xs, b->bias[3], n_tok, E, q_rows, "attn_proj_mm",
+                         true);
     }
-    return moearc_add(c, h, h, proj, n_tok * E);
+    std::vector<MvJob> jobs;
+    for (unsigned long t = 0; t < n_tok; ++t)
+        jobs.push_back(MvJob{b->w[3], att + t * q_rows, b->bias[3], h + t * E, E, true});
+    return mv_launch_all(c, b->w_type[3], jobs, q_rows, "attn_proj_chunk");
 }

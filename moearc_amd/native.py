@@ -42,6 +42,7 @@ SIGNATURES = {
     "moearc_attn_qkv": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_ulong]),
     "moearc_attn_block_chunk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong, _c_ulong, _vp, _vp, _vp]),
     "moearc_matmul_q": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _c_ulong, _c_ulong, _c_ulong]),
+    "moearc_attn_out": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _c_ulong, _c_ulong]),
     "moearc_kv_append": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _c_ulong, _c_ulong,
                                         _c_ulong, _u32]),
     "moearc_kv_append_chunk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_ulong,

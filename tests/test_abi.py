@@ -84,6 +84,7 @@ def test_null_context_is_refused_with_minus_one():
     assert lib.moearc_attn_qkv(None, None, None, None, None, None, None, 32) == -1
     assert lib.moearc_attn_block_chunk(None, None, None, None, 1, 0, None, None, None) == -1
     assert lib.moearc_matmul_q(None, 8, None, None, None, None, 4, 4, 32) == -1
+    assert lib.moearc_attn_out(None, 8, None, None, None, None, 4, 32) == -1
 
 
 def test_missing_build_fails_loudly(monkeypatch):

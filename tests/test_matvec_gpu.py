@@ -245,3 +245,20 @@ def test_chunk_matmul_refusals(ctx):
     assert lib.moearc_matmul_q(ctx.raw, 8, buf.ptr, buf.ptr, buf.ptr, None, 4, 4, 48) == -2   # not 32k
     assert lib.moearc_matmul_q(ctx.raw, 8, buf.ptr, buf.ptr + 1, buf.ptr, None, 4, 4, 64) == -2  # odd W
     assert lib.moearc_matmul_q(ctx.raw, 8, buf.ptr, buf.ptr, buf.ptr, None, 0, 4, 64) == 0
+
+
+@pytest.mark.parametrize("ty", [QuantType.Q8_0, QuantType.MXFP4, QuantType.F16], ids=lambda t: t.name)
+def test_attn_out_is_bit_identical_to_matvec_then_two_adds(ctx, ty):
+    # moe.rs:2063-2071: proj = W attn; proj += bias; h += proj
+    rows, cols = 2880, 4096
+    w, attn = fx.matvec_case(int(ty), rows, cols, 0xA770 + int(ty))
+    bias, h = fx.synth.unit(0xA771, rows), fx.synth.normal(0xA772, rows)
+    dw, da, db = ctx.upload(w), ctx.upload(attn), ctx.upload(bias)
+    proj, dh = ctx.alloc(rows * 4), ctx.upload(h)
+    ctx.matvec_q(ty, proj, dw, da, rows, cols)
+    ctx.add(proj, proj, db, rows)
+    ctx.add(dh, dh, proj, rows)
+    want = ctx.download(dh, np.float32, rows)
+    dh2 = ctx.upload(h)
+    ctx.attn_out(ty, dh2, dw, db, da, rows, cols)
+    assert np.array_equal(ctx.download(dh2, np.float32, rows), want)
