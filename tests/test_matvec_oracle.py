@@ -162,3 +162,19 @@ def test_unknown_types_and_ragged_rows_are_refused():
         oracle.dequant(2, b"\0" * 18, 1)
     with pytest.raises(oracle.OracleRefusal):
         oracle.matvec_q(Q4_K, np.zeros(144 * 4, np.uint8), np.zeros(300, np.float32), 4, 300)
+
+
+def test_f16_hi_lo_split_carries_f32_to_2_pow_minus_22():
+    # The chunk product's precision model (moearc_split_f16_k): hi = f16(x), lo = f16(x - hi)
+    # leaves |x - hi - lo| <= 2^-22 |x| for normal values, and at most half of f16's smallest
+    # subnormal (2^-25) below; every f32 below 65504 in magnitude splits without overflow.
+    rng = np.random.default_rng(22)
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32),
+                        (rng.standard_normal(50000) * 1e3).astype(np.float32),
+                        (rng.standard_normal(50000) * 1e-4).astype(np.float32),
+                        np.float32([65504.0, -65504.0, 6.1e-5, 5.9e-8, 1.0 + 2.0 ** -23])])
+    hi = x.astype(np.float16)
+    lo = (x - hi.astype(np.float32)).astype(np.float16)
+    assert np.all(np.isfinite(hi)) and np.all(np.isfinite(lo))
+    resid = np.abs(x.astype(np.float64) - hi.astype(np.float64) - lo.astype(np.float64))
+    assert np.all(resid <= 2.0 ** -22 * np.abs(x.astype(np.float64)) + 2.0 ** -25)
