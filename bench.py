@@ -3,21 +3,26 @@
 Workload (the config the metric is quoted on): single-sequence decode,
 B=1, 32768 keys, 64 query heads over 8 KV heads, head_dim 64, f16 KV in 256-token pages through a
 random page permutation, per-head f32 sinks, full causal, f16 output. A step is one attention layer
-call. Inputs are N(0,1) from a seed (synthetic data; there is no model).
+call (the split-K launch and the merge launch). Inputs are N(0,1) from a seed (synthetic data;
+there is no model).
 
-* Timed region: K steps captured in one HIP graph on the library's stream and replayed once,
-  bracketed by stream synchronisations; every step reads a different one of 6 KV copies (384 MiB)
-  so the 256 MB Infinity Cache cannot serve repeats. value = algorithmic bytes per step / step time.
-* roofline: the dominant kernel (the split-K kernel) timed with HIP events on the library stream
-  over K eager steps; achieved = algorithmic bytes per launch / its average duration, against
-  8 TB/s. traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-  summary (profiles/decode_c2_pmc.md), when present.
+* Timed region: K steps captured in one HIP graph on the library's stream and replayed, bracketed
+  by stream synchronisations; every step reads a different one of 8 KV copies (512 MiB) so the
+  256 MB Infinity Cache cannot serve repeats. The replay is repeated REPS times (the first
+  discarded, bench/PROTOCOL.md:73-87); value = algorithmic bytes per step / median step time.
+* roofline: the whole call (split + merge) at the replay's step time, against 8 TB/s; frac_split
+  beside it from the split launch alone (HIP events on the library stream, eager, with
+  MOEARC_PROFILE_KERNELS=1). traffic = HBM bytes per call from the committed rocprofv3
+  FETCH_SIZE/WRITE_SIZE summary (profiles/decode_c2_pmc.md), when present.
+* configs: BASELINE configs 1, 3 (SWA-128 and full) and 5, timed the same way.
 * prefill: BASELINE config 4 (2048 new + 2048 cached tokens), full causal and SWA-128, MFMA
-  utilisation = algorithmic flops / time / 2.5 PFLOP/s (dense f16).
-* rope_kv_append_chunk: the fused RoPE-K + f16 K/V append of the same config-4 chunk (HBM-bound;
-  bytes = f32 K/V in + f16 K/V out + position/page/slot per token).
+  utilisation = algorithmic flops / time / 2.5 PFLOP/s (dense f16); also as top-level keys.
+* rope_kv_append_chunk: the fused RoPE-K + f16 K/V append of the same config-4 chunk.
+* launch_overhead: moearc_amd/launch_overhead (examples/launch_overhead.rs:21-125 over the C ABI).
 * cpu_baseline: the CPU oracle (a C restatement of the reference's f64 CPU twin,
-  reference.rs:821-873, plus the sink) timed on this host on a bounded sample of the same decode.
+  reference.rs:821-873, plus the sink) timed on this host on a bounded sample of the same decode,
+  single thread as the reference runs it, REPS invocations after a discarded first, with the
+  1-minute load average read before each, nproc and the CPU model stated; plus an OpenMP figure.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10]
 """
@@ -25,9 +30,12 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import math
 import os
+import statistics
+import subprocess
 import sys
 import time
 
@@ -40,7 +48,8 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 H, G, D, PT = 64, 8, 64, 256
 N_KV = 32768
-COPIES = 6
+COPIES = 8
+REPS = 6  # timed repetitions; the first is discarded
 
 # algorithmic bytes per C2 step: K + V (f16) + q (f32) + sinks (f32) + out (f16)
 C2_BYTES = 2 * N_KV * G * D * 2 + H * D * 4 + H * 4 + H * D * 2
@@ -119,14 +128,42 @@ def decode_inputs(seed=0xC2):
 
 
 def pmc_traffic(path):
-    """HBM bytes per launch of the split kernel from the committed rocprofv3 summary."""
+    """HBM bytes per decode call (split + merge) from the committed rocprofv3 summary."""
     if not os.path.exists(path):
         return None
-    vals = {}
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch"):
+        if line.startswith("traffic_bytes_per_call"):
             return float(line.split()[1])
-    return vals or None
+    return None
+
+
+def rep_stats(xs):
+    """mean, sd, median over the repetitions after the first (bench/PROTOCOL.md:73-87)."""
+    kept = xs[1:] if len(xs) > 1 else xs
+    return {"n": len(kept), "mean": round(statistics.mean(kept), 3),
+            "sd": round(statistics.stdev(kept), 3) if len(kept) > 1 else 0.0,
+            "median": round(statistics.median(kept), 3), "all": [round(x, 3) for x in xs]}
+
+
+def graph_timed(hip, ctx, step, steps, warmup, reps=REPS):
+    """Per-step microseconds of `steps` calls captured in one graph, replayed `reps` times."""
+    for i in range(warmup):
+        step(i)
+    ctx.sync()
+    graph, exe = hip.capture(ctx.stream, lambda: [step(i) for i in range(steps)])
+    hip.launch(exe, ctx.stream)  # one untimed replay
+    ctx.sync()
+    out = []
+    for _ in range(reps):
+        e0, e1 = hip.event(), hip.event()
+        ctx.sync()
+        hip.record(e0, ctx.stream)
+        hip.launch(exe, ctx.stream)
+        hip.record(e1, ctx.stream)
+        ctx.sync()
+        out.append(hip.elapsed_ms(e0, e1) * 1e3 / steps)
+    hip.destroy(graph, exe)
+    return out
 
 
 def run(steps, warmup, skip_cpu=False, skip_prefill=False):
@@ -137,7 +174,7 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
     result = {}
 
     with Context() as ctx:
-        stream = ctx.stream
+        result["device"] = ctx.device_name()
         dks = [ctx.upload(kp) for _ in range(COPIES)]
         dvs = [ctx.upload(vp) for _ in range(COPIES)]
         dq, dbt, ds = ctx.upload(q), ctx.upload(bt), ctx.upload(sinks)
@@ -148,36 +185,23 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
             ctx.attn_decode_batched(dout, dq, dks[i % COPIES], dvs[i % COPIES], dbt, N_KV // PT, kb,
                                     nk, ds, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
 
-        for i in range(warmup):
-            step(i)
+        step(0)
         ctx.sync()
         eager_out = ctx.download(dout, np.float16, (H, D)).astype(np.float32)
-        graph, exe = hip.capture(stream, lambda: [step(i) for i in range(steps)])
-        e0, e1 = hip.event(), hip.event()
-        hip.launch(exe, stream)  # one untimed replay
-        ctx.sync()
-        ctx.sync()
         t0 = time.perf_counter()
-        hip.record(e0, stream)
-        hip.launch(exe, stream)
-        hip.record(e1, stream)
-        ctx.sync()
-        t1 = time.perf_counter()
-        gpu_ms = hip.elapsed_ms(e0, e1)
-        hip.destroy(graph, exe)
+        result["step_us_reps"] = graph_timed(hip, ctx, step, steps, warmup)
+        result["wall_s"] = time.perf_counter() - t0
         graph_out = ctx.download(dout, np.float16, (H, D)).astype(np.float32)
-        wall_ms = (t1 - t0) * 1e3
-        result["step_us_gpu"] = gpu_ms * 1e3 / steps
-        result["step_us_wall"] = wall_ms * 1e3 / steps
         result["graph_equals_eager"] = bool(np.array_equal(graph_out, eager_out))
         result["out"] = graph_out
         del dks, dvs
+        result["configs"] = bench_configs(ctx, hip, steps, warmup)
         result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
         result["block_chunk"] = bench_block(ctx, hip)
         result["chunk_projections"] = bench_matmul(ctx, hip)
 
-    # per-kernel event timing (eager, profiling context)
-    os.environ["MOEARC_PROFILE_EVENTS"] = "1"
+    # per-kernel event timing (eager): the call under the reference's key, its launches apart
+    os.environ["MOEARC_PROFILE_KERNELS"] = "1"
     try:
         with Context() as ctx:
             dks = [ctx.upload(kp) for _ in range(COPIES)]
@@ -194,15 +218,27 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
             ctx.sync()
             rep = ctx.profile_events_report()
             result["events"] = {k: v[0] / v[1] / 1e3 for k, v in rep.items()}
-
+            del dks, dvs
             if not skip_prefill:
                 result["prefill"] = bench_prefill(ctx, steps=max(5, steps // 5), warmup=3)
     finally:
-        os.environ.pop("MOEARC_PROFILE_EVENTS", None)
+        os.environ.pop("MOEARC_PROFILE_KERNELS", None)
 
+    result["launch_overhead"] = launch_overhead()
     if not skip_cpu:
         result["cpu"] = cpu_baseline(kp, vp, bt, q, sinks)
     return result
+
+
+def launch_overhead():
+    """The reference's launch-overhead example (examples/launch_overhead.rs) over the C ABI."""
+    exe = os.path.join(ROOT, "moearc_amd", "launch_overhead")
+    if not os.path.exists(exe):
+        return None
+    res = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if res.returncode != 0:
+        return {"error": res.stderr.strip()[-200:]}
+    return json.loads(res.stdout.strip().splitlines()[-1])
 
 
 def bench_prefill(ctx, steps, warmup):
@@ -458,130 +494,135 @@ def bench_block(ctx, hip, n_tok=128):
             "token_by_token_us_per_token": round(res["token_by_token"] / n_tok, 2)}
 
 
+def host_info():
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "cpu_model": model}
+
+
 def cpu_baseline(kp, vp, bt, q, sinks):
-    """The oracle (f64, two-pass, sequential heads: the reference's CPU twin) on this host."""
+    """The oracle (f64, two-pass, sequential heads: the reference's CPU twin) on this host, after
+    bench/PROTOCOL.md:50-58 and :73-87: REPS invocations of a bounded sample (the first discarded),
+    the 1-minute load average read before each, mean +- sd and median reported."""
     from oracle import oracle
     oracle.lib()
     bt1 = np.ascontiguousarray(bt, np.uint32)
-    t0 = time.perf_counter()
-    n = 0
-    while True:  # single thread, as the reference runs it; a bounded ~10 s sample
-        oracle.attn_decode(q, kp, vp, bt1, H, G, D, 0, N_KV, PT, 0.125, kv_type=1, sinks=sinks)
-        n += 1
-        if time.perf_counter() - t0 > 10.0 or n >= 40:
-            break
-    st_s = (time.perf_counter() - t0) / n
-    threads = min(16, os.cpu_count() or 1)
+    calls_per_rep = 2
+    single, loads = [], []
+    for _ in range(REPS):  # single thread, as the reference runs it
+        loads.append(os.getloadavg()[0])
+        t0 = time.perf_counter()
+        for _ in range(calls_per_rep):
+            oracle.attn_decode(q, kp, vp, bt1, H, G, D, 0, N_KV, PT, 0.125, kv_type=1, sinks=sinks)
+        single.append((time.perf_counter() - t0) / calls_per_rep * 1e6)
+    threads = min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count() or 1)
     qb = q.reshape(1, H, D)
     kb, nk = np.zeros(1, np.uint32), np.full(1, N_KV, np.uint32)
-    t0 = time.perf_counter()
-    m = 0
-    while True:
-        oracle.attn_decode_batched(qb, kp, vp, bt1.reshape(1, -1), kb, nk, H, G, D, PT, 0.125,
-                                   sinks=sinks, n_threads=threads)
-        m += 1
-        if time.perf_counter() - t0 > 5.0 or m >= 200:
-            break
-    mt_s = (time.perf_counter() - t0) / m
-    return {"single_us": st_s * 1e6, "single_calls": n, "mt_us": mt_s * 1e6, "mt_calls": m,
-            "threads": threads}
+    multi = []
+    for _ in range(REPS):
+        t0 = time.perf_counter()
+        for _ in range(4):
+            oracle.attn_decode_batched(qb, kp, vp, bt1.reshape(1, -1), kb, nk, H, G, D, PT, 0.125,
+                                       sinks=sinks, n_threads=threads)
+        multi.append((time.perf_counter() - t0) / 4 * 1e6)
+    return {"single_us": rep_stats(single), "calls_per_rep": calls_per_rep, "loadavg_1m": loads,
+            "mt_us": rep_stats(multi), "threads": threads, **host_info()}
 
 
-def bench_configs(steps, warmup):
-    """BASELINE configs 1, 3 and 5 (decode), reported one JSON line each; config 2 is the main line.
+def bench_configs(ctx, hip, steps, warmup):
+    """BASELINE configs 1, 3 (SWA-128 and full) and 5 (decode); config 2 is the main line.
     K/V are random finite f16 bit patterns (|x| < 2) -- timing does not depend on their values --
     in 256-token pages. Each config touches more than the 256 MB Infinity Cache per replay cycle:
     config 1 rotates 40 contiguous copies, config 3 rotates 40 random block tables over a pool of
     every sequence's pages, config 5 reads 2 GiB per call. Algorithmic bytes: K/V read
-    (2 KiB per key), q (16 KiB) and f16 out (8 KiB) per sequence, sinks, block-table entries."""
-    from moearc_amd import Context, KvType, OUT_F16
-    hip = Hip()
+    (2 KiB per key), q (16 KiB) and f16 out (8 KiB) per sequence, sinks, block-table entries.
+    Each entry: median step time over REPS graph replays (the first discarded)."""
+    from moearc_amd import KvType, OUT_F16
     rng = np.random.default_rng(0xD5)
     row = G * D
+    out = {}
 
     def pages_of(n_pages):
         bits = rng.integers(0, 1 << 16, size=n_pages * PT * row, dtype=np.uint16)
         return bits & np.uint16(0xBFFF)  # exponent below 31: finite, |x| < 2
 
-    def timed(ctx, step):
-        for i in range(warmup):
-            step(i)
-        ctx.sync()
-        graph, exe = hip.capture(ctx.stream, lambda: [step(i) for i in range(steps)])
-        hip.launch(exe, ctx.stream)  # one untimed replay
-        ctx.sync()
-        e0, e1 = hip.event(), hip.event()
-        hip.record(e0, ctx.stream)
-        hip.launch(exe, ctx.stream)
-        hip.record(e1, ctx.stream)
-        ctx.sync()
-        us = hip.elapsed_ms(e0, e1) * 1e3 / steps
-        hip.destroy(graph, exe)
-        return us
-
-    def emit(name, us, nbytes, b):
+    def emit(name, reps, nbytes, b):
+        st = rep_stats(reps)
+        us = st["median"]
         gbs = nbytes / us / 1e3
-        print(json.dumps({"config": name, "us_per_layer": round(us, 2), "algorithmic_bytes": nbytes,
-                          "gbs": round(gbs, 1), "pct_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
-                          "tokens_per_s": round(b * 1e6 / us, 0)}), flush=True)
+        out[name] = {"us_per_layer": round(us, 2), "us_reps": st, "algorithmic_bytes": nbytes,
+                     "gbs": round(gbs, 1), "pct_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                     "tokens_per_s": round(b * 1e6 / us, 0)}
 
     seq_bytes = H * D * 4 + H * D * 2  # q f32 in, f16 out
-    with Context() as ctx:
-        q32 = rng.standard_normal((32, H, D), dtype=np.float32)
-        dq, ds = ctx.upload(q32), ctx.upload(rng.standard_normal(H, dtype=np.float32))
+    q32 = rng.standard_normal((32, H, D), dtype=np.float32)
+    dq, ds = ctx.upload(q32), ctx.upload(rng.standard_normal(H, dtype=np.float32))
 
-        # C1: B=1, 4096 keys, contiguous pages
-        n1 = 4096
-        copies = 40
-        dk1 = [ctx.upload(pages_of(n1 // PT)) for _ in range(copies)]
-        dv1 = [ctx.upload(pages_of(n1 // PT)) for _ in range(copies)]
-        dbt1 = ctx.upload(np.arange(n1 // PT, dtype=np.uint32))
-        out1 = ctx.alloc(H * D * 2)
-        kb1, nk1 = np.zeros(1, np.uint32), np.full(1, n1, np.uint32)
-        us = timed(ctx, lambda i: ctx.attn_decode_batched(out1, dq, dk1[i % copies], dv1[i % copies], dbt1,
-                                                          n1 // PT, kb1, nk1, ds, H, G, D, PT, 0.125,
-                                                          KvType.F16, out_type=OUT_F16))
-        emit("C1 decode B=1, 4096 keys, full, contiguous pages", us,
-             n1 * 2 * row * 2 + seq_bytes + H * 4 + 4 * (n1 // PT), 1)
-        del dk1, dv1
+    # C1: B=1, 4096 keys, contiguous pages
+    n1 = 4096
+    copies = 40
+    dk1 = [ctx.upload(pages_of(n1 // PT)) for _ in range(copies)]
+    dv1 = [ctx.upload(pages_of(n1 // PT)) for _ in range(copies)]
+    dbt1 = ctx.upload(np.arange(n1 // PT, dtype=np.uint32))
+    out1 = ctx.alloc(H * D * 2)
+    kb1, nk1 = np.zeros(1, np.uint32), np.full(1, n1, np.uint32)
+    reps = graph_timed(hip, ctx, lambda i: ctx.attn_decode_batched(
+        out1, dq, dk1[i % copies], dv1[i % copies], dbt1, n1 // PT, kb1, nk1, ds, H, G, D, PT, 0.125,
+        KvType.F16, out_type=OUT_F16), steps, warmup)
+    emit("C1 decode B=1, 4096 keys, full, contiguous pages", reps,
+         n1 * 2 * row * 2 + seq_bytes + H * 4 + 4 * (n1 // PT), 1)
+    del dk1, dv1
 
-        # C3: B=32, lengths ~U[1024, 32768], random page tables, SWA-128 and full
-        lens = np.random.default_rng(33).integers(1024, 32769, size=32).astype(np.uint32)
-        npg = [-(-int(n) // PT) for n in lens]
-        pool = sum(npg)
-        dk3, dv3 = ctx.upload(pages_of(pool)), ctx.upload(pages_of(pool))
-        stride = max(npg)
-        bts = []
-        for _ in range(copies):
-            perm = rng.permutation(pool).astype(np.uint32)
-            t = np.zeros((32, stride), np.uint32)
-            off = 0
-            for s, p in enumerate(npg):
-                t[s, :p] = perm[off:off + p]
-                off += p
-            bts.append(ctx.upload(t))
-        out3 = ctx.alloc(32 * H * D * 2)
-        for window in (0, 128):
-            kb = np.maximum(lens.astype(np.int64) - window, 0).astype(np.uint32) if window else np.zeros_like(lens)
-            span = (lens.astype(np.int64) - kb.astype(np.int64))
-            first, last = kb.astype(np.int64) // PT, (lens.astype(np.int64) - 1) // PT
-            us = timed(ctx, lambda i: ctx.attn_decode_batched(out3, dq, dk3, dv3, bts[i % copies], stride, kb,
-                                                              lens, ds, H, G, D, PT, 0.125, KvType.F16,
-                                                              out_type=OUT_F16))
-            emit(f"C3 decode B=32 ragged U[1024,32768], {'SWA-128' if window else 'full'}", us,
-                 int(span.sum()) * 2 * row * 2 + 32 * seq_bytes + H * 4 + 4 * int((last - first + 1).sum()), 32)
-        del dk3, dv3, bts
+    # C3: B=32, lengths ~U[1024, 32768], random page tables, SWA-128 and full
+    lens = np.random.default_rng(33).integers(1024, 32769, size=32).astype(np.uint32)
+    npg = [-(-int(n) // PT) for n in lens]
+    pool = sum(npg)
+    dk3, dv3 = ctx.upload(pages_of(pool)), ctx.upload(pages_of(pool))
+    stride = max(npg)
+    bts = []
+    for _ in range(copies):
+        perm = rng.permutation(pool).astype(np.uint32)
+        t = np.zeros((32, stride), np.uint32)
+        off = 0
+        for s_, p in enumerate(npg):
+            t[s_, :p] = perm[off:off + p]
+            off += p
+        bts.append(ctx.upload(t))
+    out3 = ctx.alloc(32 * H * D * 2)
+    for window in (128, 0):
+        kb = np.maximum(lens.astype(np.int64) - window, 0).astype(np.uint32) if window else np.zeros_like(lens)
+        span = (lens.astype(np.int64) - kb.astype(np.int64))
+        first, last = kb.astype(np.int64) // PT, (lens.astype(np.int64) - 1) // PT
+        reps = graph_timed(hip, ctx, lambda i: ctx.attn_decode_batched(
+            out3, dq, dk3, dv3, bts[i % copies], stride, kb, lens, ds, H, G, D, PT, 0.125, KvType.F16,
+            out_type=OUT_F16), steps, warmup)
+        emit(f"C3 decode B=32 ragged U[1024,32768], {'SWA-128' if window else 'full'}", reps,
+             int(span.sum()) * 2 * row * 2 + 32 * seq_bytes + H * 4 + 4 * int((last - first + 1).sum()), 32)
+    del dk3, dv3, bts
 
-        # C5: B=8 x 131072 keys, full
-        n5, b5 = 131072, 8
-        p5 = n5 // PT
-        dk5, dv5 = ctx.upload(pages_of(b5 * p5)), ctx.upload(pages_of(b5 * p5))
-        dbt5 = ctx.upload(rng.permutation(b5 * p5).astype(np.uint32).reshape(b5, p5))
-        out5 = ctx.alloc(b5 * H * D * 2)
-        kb5, nk5 = np.zeros(b5, np.uint32), np.full(b5, n5, np.uint32)
-        us = timed(ctx, lambda i: ctx.attn_decode_batched(out5, dq, dk5, dv5, dbt5, p5, kb5, nk5, ds, H, G, D,
-                                                          PT, 0.125, KvType.F16, out_type=OUT_F16))
-        emit("C5 decode B=8 x 131072 keys, full", us, b5 * n5 * 2 * row * 2 + b5 * seq_bytes + H * 4 + 4 * b5 * p5, b5)
+    # C5: B=8 x 131072 keys, full
+    n5, b5 = 131072, 8
+    p5 = n5 // PT
+    dk5, dv5 = ctx.upload(pages_of(b5 * p5)), ctx.upload(pages_of(b5 * p5))
+    dbt5 = ctx.upload(rng.permutation(b5 * p5).astype(np.uint32).reshape(b5, p5))
+    out5 = ctx.alloc(b5 * H * D * 2)
+    kb5, nk5 = np.zeros(b5, np.uint32), np.full(b5, n5, np.uint32)
+    reps = graph_timed(hip, ctx, lambda i: ctx.attn_decode_batched(
+        out5, dq, dk5, dv5, dbt5, p5, kb5, nk5, ds, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16),
+        max(4, steps // 4), 2)
+    emit("C5 decode B=8 x 131072 keys, full", reps, b5 * n5 * 2 * row * 2 + b5 * seq_bytes + H * 4 + 4 * b5 * p5, b5)
+    del dk5, dv5
+    return out
 
 
 def only(what, steps, warmup):
@@ -662,14 +703,19 @@ def main():
         only(args.only, args.steps, args.warmup)
         return
     if args.configs:
-        bench_configs(args.steps, args.warmup)
+        from moearc_amd import Context
+        with Context() as ctx:
+            for name, entry in bench_configs(ctx, Hip(), args.steps, args.warmup).items():
+                print(json.dumps({"config": name, **entry}), flush=True)
         return
     r = run(args.steps, args.warmup, args.skip_cpu, args.skip_prefill)
 
-    step_us = r["step_us_gpu"]
+    st = rep_stats(r["step_us_reps"])
+    step_us = st["median"]
     gbs = C2_BYTES / step_us / 1e3
-    split_us = r["events"].get("attn_decode.split r64 m64")
-    ach = C2_BYTES / split_us / 1e3 if split_us else None
+    ev = r["events"]
+    split_us = ev.get("kernel attn_decode.split r64 m64")
+    merge_us = ev.get("kernel attn_decode.merge r64 m64")
     # parity spot check against the oracle (f64) on the same inputs
     from oracle import oracle
     kp, vp, bt, q, sinks = decode_inputs()
@@ -695,44 +741,83 @@ def main():
             "global_batch": 1, "seq_len": N_KV, "parallelism": "single GPU",
         },
         "us_per_layer": round(step_us, 2),
-        "us_per_layer_wall": round(r["step_us_wall"], 2),
+        "us_per_layer_reps": st,
         "pct_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
         "tokens_per_s": round(1e6 / step_us, 0),
-        "kernel_us": {k: round(v, 2) for k, v in r["events"].items()},
         "graph_replay_equals_eager": r["graph_equals_eager"],
         "parity_max_abs_err": err,
         "roofline": {
             "bound": "hbm",
-            "achieved": round(ach, 1) if ach else None,
+            "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4) if ach else None,
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "moearc_attn_decode_f16d64 (split-K)",
-            "bytes_per_launch": C2_BYTES,
+            "scope": "whole decode call (split-K launch + merge launch), graph-replay step time",
+            "bytes_per_call": C2_BYTES,
+            "frac_split": round(C2_BYTES / split_us / 1e3 / HBM_PEAK_GBS, 4) if split_us else None,
+            "split_us_events": round(split_us, 2) if split_us else None,
+            "merge_us_events": round(merge_us, 2) if merge_us else None,
+            "call_us_events": round(ev["attn_decode r64 m64"], 2) if "attn_decode r64 m64" in ev else None,
         },
+        "device": r.get("device"),
+        "commit": git_head(),
+        "source_sha16": source_sha16(),
     }
     if "prefill" in r:
-        line["prefill"] = r["prefill"]
-    if "projections" in r:
-        line["projections"] = r["projections"]
-    if "block_chunk" in r:
-        line["block_chunk"] = r["block_chunk"]
-    if "chunk_projections" in r:
-        line["chunk_projections"] = r["chunk_projections"]
+        pf = r["prefill"]
+        line["prefill_full_mfma_util"] = pf["full"]["mfma_util"]
+        line["prefill_full_us"] = pf["full"]["us"]
+        line["prefill_swa128_hbm_frac"] = pf["swa128"]["roofline_frac"]
+        line["prefill_swa128_us"] = pf["swa128"]["us"]
+        line["prefill"] = pf
+    line["configs"] = r["configs"]
+    line["launch_overhead"] = r["launch_overhead"]
+    for k in ("projections", "block_chunk", "chunk_projections"):
+        if k in r:
+            line[k] = r[k]
     if "cpu" in r:
         c = r["cpu"]
+        us = c["single_us"]["mean"]
         line["cpu_baseline"] = {
-            "value": round(C2_BYTES / c["single_us"] / 1e3, 3),
+            "value": round(C2_BYTES / us / 1e3, 4),
             "unit": "GB/s",
             "cores": 1,
             "kind": "port",
-            "sample": f"C2 decode, {c['single_calls']} calls of the f64 oracle, one thread "
-                      f"({c['single_us'] / 1e3:.1f} ms/call)",
-            "multithread": {"threads": c["threads"], "us_per_call": round(c["mt_us"], 1),
-                            "value": round(C2_BYTES / c["mt_us"] / 1e3, 3)},
+            "sample": f"C2 decode (the whole 32768-key call), {c['calls_per_rep']} calls per invocation x "
+                      f"{c['single_us']['n']} invocations after a discarded first, of the f64 oracle on one "
+                      f"thread: {us / 1e3:.1f} +- {c['single_us']['sd'] / 1e3:.1f} ms per call",
+            "us_per_call": c["single_us"],
+            "loadavg_1m_before_each": [round(x, 2) for x in c["loadavg_1m"]],
+            "nproc": c["nproc"], "affinity_cpus": c["affinity_cpus"], "cpu_model": c["cpu_model"],
+            "multithread": {"threads": c["threads"], "us_per_call": c["mt_us"],
+                            "value": round(C2_BYTES / c["mt_us"]["mean"] / 1e3, 3)},
         }
     print(json.dumps(line), flush=True)
+
+
+def git_head():
+    try:
+        res = subprocess.run(["git", "-C", ROOT, "rev-parse", "HEAD"], capture_output=True, text=True,
+                             timeout=10)
+        return res.stdout.strip() or None if res.returncode == 0 else None
+    except (OSError, subprocess.SubprocessError):
+        return None
+
+
+def source_sha16():
+    """Digest of the sources this line was measured with (the device code, host runtime, headers and
+    this file), so the line can be matched to a tree where git history is absent."""
+    h = hashlib.sha256()
+    files = [os.path.join(ROOT, "bench.py")]
+    for d in ("moearc_amd/csrc", "include"):
+        full = os.path.join(ROOT, d)
+        files += [os.path.join(full, f) for f in sorted(os.listdir(full))
+                  if f.endswith((".hip", ".cpp", ".h", ".inc", ".py"))]
+    for f in files:
+        h.update(os.path.relpath(f, ROOT).encode())
+        h.update(open(f, "rb").read())
+    return h.hexdigest()[:16]
 
 
 if __name__ == "__main__":

@@ -32,7 +32,8 @@ typedef struct moearc_ctx moearc_ctx;
 
 /* ffi.rs:20, kernels.cpp:804-828. Opens a stream on the current HIP device and loads the
  * kernels' code object with hipModuleLoad. NULL when no device or the code object is missing.
- * MOEARC_PROFILE_EVENTS=1 records a HIP event pair around every attention launch. */
+ * MOEARC_PROFILE_EVENTS=1 brackets every tracked call with a HIP event pair (see the report);
+ * MOEARC_PROFILE_KERNELS=1 also brackets every kernel launch inside a call, and untracked calls. */
 moearc_ctx *moearc_ctx_create(void);
 /* ffi.rs:21, kernels.cpp:830. Waits for the stream, then frees everything the context owns. */
 void moearc_ctx_destroy(moearc_ctx *c);
@@ -40,9 +41,16 @@ void moearc_ctx_destroy(moearc_ctx *c);
 int moearc_profile_events_enabled(moearc_ctx *c);
 /* ffi.rs:23, kernels.cpp:841-846. Forget recorded times. */
 int moearc_profile_events_reset(moearc_ctx *c);
-/* ffi.rs:24-28, kernels.cpp:852-871. One "key nanoseconds calls" line per kernel shape; waits for
- * the recorded launches. Keys are "attn_decode r{n_heads} m{head_dim}" (kernels.cpp:1905-1916),
- * "attn_prefill r{n_heads} m{head_dim}" and "kv_append r{n_kv_heads} m{head_dim}". */
+/* ffi.rs:24-28, kernels.cpp:852-871. One "key nanoseconds calls" line per key; waits for the
+ * recorded launches. Every tracked call is recorded once, under one key, as the reference records
+ * each submission: "attn_decode r{n_heads} m{head_dim}" for a whole decode call (split and merge
+ * launches, windowed and full layers alike; kernels.cpp:1905-1916), "mvq {type} r{rows} m1",
+ * "mvq_batched {type} r{rows} m{n_mat}" and "mv_generic r{rows} m1" (F32/F16 weights) for the
+ * matvecs (kernels.cpp:1057-1111, :1168-1196); this library's own entry points under their names
+ * ("attn_prefill r{n_heads} m{head_dim}", "attn_qkv {type} ...", ...). Entry points the reference
+ * does not track (zero, add, kv_append, quantize_f16, rope, matvec_f32) add no key. With
+ * MOEARC_PROFILE_KERNELS=1, kernels are also recorded on their own as "kernel {name} r.. m.." --
+ * nested inside their call's bracket, so those keys must not be added to the call keys. */
 int moearc_profile_events_report(moearc_ctx *c, char *out, unsigned long cap);
 /* ffi.rs:29, kernels.cpp:879-882. Block until the stream drains; reports a device fault. */
 int moearc_sync(moearc_ctx *c);
@@ -243,6 +251,10 @@ typedef struct moearc_attn_block {
     const unsigned int *block_table; /* the sequence's pages (a windowed block: its ring table) */
     unsigned long n_embd, n_head, n_head_kv, head_dim, page_tokens;
     unsigned long n_swa;         /* 0: full attention */
+    unsigned long ring_pages;    /* a windowed block read through a ring table: the ring's pages, so the
+                                    chunk is refused unless its keys fit (n_tok + n_swa - 1 <=
+                                    ring_pages * page_tokens: later tokens of a chunk would otherwise
+                                    overwrite keys earlier rows still attend to); 0: not a ring */
     float scale;                 /* attention scale, 1/sqrt(head_dim) */
     unsigned long n_rot;         /* rotated dimensions */
     float freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi;  /* as moearc_rope */
@@ -251,8 +263,9 @@ typedef struct moearc_attn_block {
 /* h f32 [n_tok][n_embd] (updated in place), x f32 [n_tok][n_embd] (attn.norm's output), pos i32,
  * page_ids / slots u32 [n_tok] (the tokens' cache places, as moearc_kv_pool_append_chunk returns
  * them), tokens at positions pos0 .. pos0 + n_tok - 1. Working memory is the context's (grown on
- * demand, kept). Refusals: null c, b, h, x, pos, page_ids or slots -> -1; then those of the calls
- * above, in that order (nothing is enqueued for a refusal found before the first launch). */
+ * demand, kept). Refusals: null c, b, h, x, pos, page_ids or slots -> -1; a ring too small for the
+ * chunk (see ring_pages) -> -2; then those of the calls above, in that order (nothing is enqueued
+ * for a refusal found before the first launch). */
 int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h, const float *x,
                             unsigned long n_tok, unsigned long pos0, const int *pos,
                             const unsigned int *page_ids, const unsigned int *slots);

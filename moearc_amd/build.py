@@ -1,12 +1,14 @@
 """Builds the native library in-tree.
 
-Two artefacts, both written next to this file:
+Three artefacts, all written next to this file:
 
 * ``moearc_attn_gfx950.co`` -- the device code object (every kernel, one translation unit), built
   by ``hipcc --genco`` for gfx950 only and loaded at context creation with ``hipModuleLoad``;
 * ``libmoearc_attn.so`` -- the host runtime behind the C ABI in ``include/moearc_attn.h`` and the
   KV page pool of ``include/moearc_kv.h``, built by the host compiler against the HIP runtime API
-  (no device code in it).
+  (no device code in it);
+* ``launch_overhead`` -- the submission-cost measurement of the reference's
+  ``examples/launch_overhead.rs``, a C++ program over the C ABI (run by ``bench.py``).
 
 Run ``python -m moearc_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -25,6 +27,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 CODE_OBJECT = os.path.join(HERE, "moearc_attn_gfx950.co")
 LIBRARY = os.path.join(HERE, "libmoearc_attn.so")
+LAUNCH_OVERHEAD = os.path.join(HERE, "launch_overhead")
 
 # Packed-FP32 instructions stay disabled (v_pk_fma_f32 and friends are not emitted).
 # -fno-honor-nans: no kernel tests for NaN (the f16 codec classifies NaNs by their bits), and
@@ -33,7 +36,7 @@ LIBRARY = os.path.join(HERE, "libmoearc_attn.so")
 # VGPRs and back around each rescale branch of the prefill loop.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-O3", "-std=c++17",
-    "-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    "-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
@@ -62,6 +65,11 @@ def build(verbose: bool = False) -> None:
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl",
           "-Wl,-rpath," + os.path.join(ROCM, "lib")], verbose)
     os.replace(tmp_so, LIBRARY)
+    tmp_exe = LAUNCH_OVERHEAD + ".tmp"
+    _run([cxx, "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", INCLUDE,
+          os.path.join(CSRC, "launch_overhead.cpp"), "-o", tmp_exe, "-L", HERE, "-lmoearc_attn",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp_exe, LAUNCH_OVERHEAD)
 
 
 if __name__ == "__main__":

@@ -465,13 +465,14 @@ class AttnBlockDesc(ctypes.Structure):
                 ("sinks", ctypes.c_void_p), ("k_pages", ctypes.c_void_p), ("v_pages", ctypes.c_void_p),
                 ("block_table", ctypes.c_void_p), ("n_embd", ctypes.c_ulong), ("n_head", ctypes.c_ulong),
                 ("n_head_kv", ctypes.c_ulong), ("head_dim", ctypes.c_ulong), ("page_tokens", ctypes.c_ulong),
-                ("n_swa", ctypes.c_ulong), ("scale", ctypes.c_float), ("n_rot", ctypes.c_ulong),
+                ("n_swa", ctypes.c_ulong), ("ring_pages", ctypes.c_ulong), ("scale", ctypes.c_float), ("n_rot", ctypes.c_ulong),
                 ("freq_base", ctypes.c_float), ("freq_scale", ctypes.c_float), ("ext_factor", ctypes.c_float),
                 ("attn_factor", ctypes.c_float), ("corr_lo", ctypes.c_float), ("corr_hi", ctypes.c_float)]
 
     @staticmethod
     def make(types, ws, biases, sinks, k_pages, v_pages, block_table, n_embd, n_head, n_head_kv,
-             head_dim, page_tokens, n_swa, scale, n_rot, freq_base, scaling: "RopeScaling | None" = None):
+             head_dim, page_tokens, n_swa, scale, n_rot, freq_base, scaling: "RopeScaling | None" = None,
+             ring_pages: int = 0):
         s = scaling or RopeScaling()
         d = AttnBlockDesc()
         for i in range(4):
@@ -482,6 +483,7 @@ class AttnBlockDesc(ctypes.Structure):
         d.k_pages, d.v_pages, d.block_table = k_pages.ptr, v_pages.ptr, block_table.ptr
         d.n_embd, d.n_head, d.n_head_kv, d.head_dim = n_embd, n_head, n_head_kv, head_dim
         d.page_tokens, d.n_swa, d.scale, d.n_rot, d.freq_base = page_tokens, n_swa, scale, n_rot, freq_base
+        d.ring_pages = ring_pages
         d.freq_scale, d.ext_factor, d.attn_factor = s.freq_scale, s.ext_factor, s.attn_factor
         d.corr_lo, d.corr_hi = s.corr_lo, s.corr_hi
         # the descriptor holds raw device pointers: keep their buffers alive as long as it lives

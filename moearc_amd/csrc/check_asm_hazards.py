@@ -11,7 +11,10 @@ N + 1 for `s_nop N`):
      registers (same-size back-to-back accumulation is forwarded) but not read them as A or B;
   2. a VALU result is not read by an MFMA within VALU_MFMA_WAIT wait states;
   3. no register that an asm-issued `ds_read*` or block-table `global_load_dword` writes is touched
-     between the load and the `s_waitcnt` that retires it (loads counted in program order).
+     between the load and the `s_waitcnt` that retires it (loads counted in program order);
+  4. an inline-asm statement that writes m0 (the LDS base of the DMA copies; a register the compiler
+     owns, so no asm may list it as clobbered) first saves it to an SGPR and ends by restoring it
+     from that SGPR, which nothing in between writes -- in every kernel of the code object.
 
 Usage: python check_asm_hazards.py [kernel-name-prefix ...]   (default: moearc_attn_prefill_g)
 Exit status 1 when a hazard is found.
@@ -27,6 +30,7 @@ MFMA_WAIT = 20      # 16-pass XDL result -> VALU: 18 on gfx940, 19 on gfx950, on
 VALU_MFMA_WAIT = 2  # VALU result -> MFMA source
 FLAGS = ["--offload-arch=gfx950", "--cuda-device-only", "-S", "-O3", "-std=c++17",
          "-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+         "-mllvm", "-amdgpu-kernarg-preload-count=14",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
@@ -185,8 +189,54 @@ def load_hazards(ins):
     return out
 
 
+def m0_hazards(lines):
+    """Check 4 over the raw assembly: every ;;#ASMSTART .. ;;#ASMEND region that writes m0 saves
+    it first (s_mov_b32 sN, m0) and restores it last (s_mov_b32 m0, sN), sN untouched between."""
+    out = []
+    region = None
+    for l in lines + [";;#ASMSTART"]:
+        t = l.split(";")[0].strip()
+        if ";;#ASMSTART" in l:
+            region = []
+            continue
+        if ";;#ASMEND" in l:
+            if region is not None:
+                out += _m0_region(region)
+            region = None
+            continue
+        if region is not None and t and not t.endswith(":") and not t.startswith("."):
+            region.append(t)
+    return out
+
+
+def _m0_region(ins):
+    writes_m0 = [i for i, t in enumerate(ins) if re.match(r"s_\w+ m0\b", t)]
+    if not writes_m0:
+        return []
+    saves = [i for i, t in enumerate(ins) if re.fullmatch(r"s_mov_b32 s\d+, m0", t)]
+    if not saves or saves[0] > writes_m0[0]:
+        return [f"[{ins[writes_m0[0]]}]: m0 written before it is saved"]
+    reg = ins[saves[0]].split()[1].rstrip(",")
+    last = writes_m0[-1]
+    if ins[last] != f"s_mov_b32 m0, {reg}":
+        return [f"[{ins[last]}]: the statement's last m0 write does not restore it from {reg}"]
+    for t in ins[saves[0] + 1:last]:
+        if re.match(rf"\S+ {reg}\b", t) or re.match(rf"\S+ s\[(\d+):(\d+)\]", t) and \
+                int(re.match(rf"\S+ s\[(\d+):(\d+)\]", t).group(1)) <= int(reg[1:]) <= \
+                int(re.match(rf"\S+ s\[(\d+):(\d+)\]", t).group(2)):
+            return [f"[{t}]: overwrites the saved m0 in {reg}"]
+    for t in ins[last + 1:]:
+        if re.match(r"(global|buffer)_load\S*_lds|global_load_lds", t):
+            return [f"[{t}]: an LDS copy after m0 was restored"]
+    return []
+
+
 def main(prefixes):
     lines = compile_asm()
+    m0 = m0_hazards(lines)
+    print(f"inline asm writing m0: {len(m0)} hazards")
+    for p in m0[:10]:
+        print("   ", p)
     heads = [l.split(";")[0].rstrip() for l in lines]
     names = sorted({h[:-1] for h in heads if re.match(r"^[A-Za-z_]\w*:$", h)
                     and any(h.startswith(p) for p in prefixes)})
@@ -201,7 +251,7 @@ def main(prefixes):
     if not names:
         print("no kernel matches", prefixes)
         return 1
-    return 1 if bad else 0
+    return 1 if bad or m0 else 0
 
 
 if __name__ == "__main__":

@@ -307,6 +307,9 @@ def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jn, l
 
 
 def generate():
+    # m0 (the LDS base of the copies) is the compiler's register: saved here, restored at the one
+    # exit, so the statement leaves it as it found it and needs no m0 clobber
+    ins("s_mov_b32 s86, m0")
     # ---- prologue: entries of tiles 0 and 1, their copies, entries of tiles 2 and 3, step 0 ----
     ins("s_mov_b32 s80, 0")
     pid_load(0, 80, "pro_p0")
@@ -383,6 +386,7 @@ def generate():
     ins("s_setpc_b64 s[66:67]")
     # ---- end: every copy and read has landed; the last MFMA results are readable ----
     ins("pff_end:")
+    ins("s_mov_b32 m0, s86")
     ins("s_waitcnt vmcnt(0) lgkmcnt(0)")
     ins("s_nop 7")
     ins("s_nop 7")

@@ -44,18 +44,23 @@ extern "C" __global__ void moearc_kv_append_k(void *k_pages, void *v_pages, cons
     }
 }
 
-// A chunk of tokens: token t goes to (page_ids[t], slots[t]). A slot outside the page is skipped
-// (the host cannot see device-resident slots, so the bound is enforced here).
+// A chunk of tokens: token t goes to (page_ids[t], slots[t]). The host cannot see device-resident
+// slots, so the bound is enforced here: a token whose slot lies outside the page is not written,
+// and the refusal is recorded in *err (1), which the host reads back at its next synchronisation
+// and reports as a failed call.
 extern "C" __global__ void moearc_kv_append_chunk_k(void *k_pages, void *v_pages, const float *k,
                                                     const float *v, const uint32_t *page_ids,
                                                     const uint32_t *slots, uint64_t n_tok,
                                                     uint64_t row, uint64_t page_tokens,
-                                                    uint32_t kv_type) {
+                                                    uint32_t kv_type, uint32_t *err) {
     const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= n_tok * row) return;
     const uint64_t t = g / row, i = g - t * row;
     const uint32_t slot = slots[t];
-    if (slot >= page_tokens) return;
+    if (slot >= page_tokens) {
+        if (i == 0) *(volatile uint32_t *) err = 1u;  // every writer stores the same value
+        return;
+    }
     const uint64_t dst = ((uint64_t) page_ids[t] * page_tokens + slot) * row + i;
     if (kv_type == MOEARC_KV_F16) {
         ((uint16_t *) k_pages)[dst] = f32_to_f16_bits(k[g]);

@@ -12,46 +12,43 @@
 #define MOEARC_MAX_SEQS_PER_LAUNCH 64
 
 
-// Partial-result record of one decode work item (one split of one KV head of one sequence),
-// written to the workspace when a KV head's span is split across work-groups:
-//   [0, 16)          running max per query head of the group (log2 domain)
-//   [16, 32)         running denominator per head
-//   [32, 32 + 64*16) un-normalised output, [head][dim]
-#define MOEARC_PARTIAL_FLOATS (32 + 64 * 16)
-
-// Work-groups of the split merge per (sequence, query head): each combines 64 / MOEARC_MERGE_PARTS
-// output channels.
-#define MOEARC_MERGE_PARTS 4
+// Partial results of a split decode, written by the split kernel when a sequence's span is split
+// across work items (one work item = one split of one sequence) and combined by the merge kernel.
+// Head-major, so the records of one query head are contiguous:
+//   rec_o[(h * n_items + item) * 64 + d]   un-normalised output (f32)
+//   rec_ml[(h * n_items + item) * 2 + 0/1] running max (log2 domain) / denominator (f32)
 #define MOEARC_MERGE_THREADS 256
 
-// Kernel arguments of the split-K decode. Passed by value; the per-sequence arrays let one launch
-// serve a ragged batch. Work item `it` (one (sequence, split) pair) covers the work-groups
-// it * nkb + kbi for every KV-head block kbi, so consecutive work-groups -- which the dispatcher
-// places on consecutive XCDs -- take consecutive KV-head blocks of the same split.
+
+// Kernel arguments of the split-K decode that are not preloaded scalars (the leading kernel
+// arguments carry the KV and block-table bases, q, sequence 0's span, split and item count, and
+// the geometry). Passed by value; the per-sequence arrays let one launch serve a ragged batch.
+// Work item `it` (one (sequence, split) pair) covers the work-groups it * nkb + kbi for every
+// KV-head block kbi, so consecutive work-groups -- which the dispatcher places on consecutive XCDs
+// -- take consecutive KV-head blocks of the same split.
 struct DecodeArgs {
     const float *q;               // [n_seqs][n_heads][64] f32
-    const uint16_t *k_pages;      // f16 bits, [page][slot][kv_head][64]
-    const uint16_t *v_pages;
     const uint32_t *block_tables; // row b at block_tables + b * bt_stride
     const float *sinks;           // [n_heads] or null
     void *out;                    // [n_seqs][n_heads][64], f32 or f16
-    float *ws;                    // partial records, one per work-group
-    uint32_t *counters;           // [sequence][KV-head block] arrival counts, zero between launches;
-                                  // non-null: the last work-group of a block merges its splits
+    float *rec_o;                 // partial records (see above)
+    float *rec_ml;
     uint64_t bt_stride;
-    uint32_t n_heads;
-    uint32_t n_kv_heads;
-    uint32_t group;               // n_heads / n_kv_heads, at most 16
-    uint32_t pt_shift;            // log2(page_tokens)
+    uint32_t n_items;             // work items of the launch (records per head)
     uint32_t out_f16;
     float scale_log2e;            // scale * log2(e)
     uint32_t n_seqs;
-    uint32_t nkb;                 // KV-head blocks per work item (KV heads / heads per work-group)
     uint32_t item_begin[MOEARC_MAX_SEQS_PER_LAUNCH + 1]; // first work item of each sequence; entries
                                                          // n_seqs .. the end: the work-item count
     uint32_t kv_begin[MOEARC_MAX_SEQS_PER_LAUNCH];       // key span [kv_begin, n_kv)
     uint32_t n_kv[MOEARC_MAX_SEQS_PER_LAUNCH];
-    uint32_t split_len[MOEARC_MAX_SEQS_PER_LAUNCH];      // keys per split (a multiple of 32)
+    uint32_t split_len[MOEARC_MAX_SEQS_PER_LAUNCH];      // keys per split (a multiple of the chunk)
+};
+
+// The merge kernel's per-sequence item ranges (sequence 0's end is a preloaded argument). One
+// spare entry keeps the kernel's argument block a multiple of 8 bytes, the host struct's size.
+struct MergeArgs {
+    uint32_t item_begin[MOEARC_MAX_SEQS_PER_LAUNCH + 2];
 };
 
 // General decode (any head_dim <= 1024, f32 or f16 KV, any page size, any group).

@@ -128,8 +128,12 @@ __device__ __forceinline__ void pf_read_vt(u32x2_t (&r)[4], uint32_t base) {
 // LDS DMA of 16 bytes per lane from a wave-uniform global base plus a per-lane 32-bit offset to
 // LDS address lds + 16 * lane (the scalar-base form: no 64-bit address arithmetic per lane).
 __device__ __forceinline__ void pf_copy16(const void *sbase, uint32_t voff, uint32_t lds) {
-    // M0 is read by the DMA one wait state after it is written
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+    // M0 is read by the DMA one wait state after it is written; it is the compiler's register, so
+    // the statement saves it first and restores it after the DMA has issued (no m0 clobber)
+    uint32_t m0_saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(m0_saved) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
 template <int GROUP>

@@ -95,13 +95,14 @@ extern "C" __global__ void moearc_rope_k(float *dst, const float *src, const int
 }
 
 // A prefill chunk's K (rotated) and V to (page_ids[t], slots[t]); k, v f32 [n_tok][n_kv_heads][head_dim].
-// A slot outside the page is skipped, as in moearc_kv_append_chunk. Grid as moearc_rope_k's.
+// A slot outside the page is not written and is recorded in *err, as in moearc_kv_append_chunk.
+// Grid as moearc_rope_k's.
 extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_pages, const float *k,
                                                          const float *v, const int *pos,
                                                          const uint32_t *page_ids, const uint32_t *slots,
                                                          uint64_t n_tok, uint32_t n_kv_heads,
                                                          uint32_t head_dim, uint64_t page_tokens,
-                                                         uint32_t kv_type, RopeParams r) {
+                                                         uint32_t kv_type, RopeParams r, uint32_t *err) {
     const uint32_t nslot = (head_dim + 1u) >> 1;
     const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= n_tok * nslot) return;
@@ -127,7 +128,10 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
     const uint32_t slot = slots[t], page = page_ids[t];
     const int p = pos[t];
     asm volatile("" ::"v"(page), "v"(p));  // keeps the two loads above the branch
-    if (slot >= page_tokens) return;
+    if (slot >= page_tokens) {
+        if (j == 0) *(volatile uint32_t *) err = 1u;  // every writer stores the same value
+        return;
+    }
     if (rot) {
         const float2_t cs = rope_factors(r, p, j);
 #pragma unroll

@@ -10,6 +10,7 @@
 #include "moearc_attn.h"
 
 #include <cmath>
+#include <cstddef>
 
 #include <hip/hip_runtime_api.h>
 
@@ -80,7 +81,7 @@ struct moearc_ctx {
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
     hipFunction_t f_rope = nullptr, f_rope_append_chunk = nullptr;
     hipFunction_t f_dec_general = nullptr;
-    hipFunction_t f_dec_fast[7] = {};  // KV heads x waves per head: 1x4, 1x16, 2x8, 4x4, 8x2, 1x8, 2x4
+    hipFunction_t f_dec_fast[2] = {};  // split kernels (kDecodeVariants)
     hipFunction_t f_dec_merge = nullptr;
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
@@ -91,16 +92,23 @@ struct moearc_ctx {
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
     hipFunction_t f_prefill_precise[4] = {};  // the same with p split into f16 hi + lo
     bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
-    bool profiling = false;
+    bool profiling = false;        // MOEARC_PROFILE_EVENTS=1: one event bracket per tracked call
+    bool profile_kernels = false;  // MOEARC_PROFILE_KERNELS=1: also every kernel inside a call
+    int scope_depth = 0;           // > 0 while an entry point's own bracket is open
+    // Errors found after a call returned 0, reported by the next moearc_sync: a device word the
+    // chunk-append kernels set when a device-resident slot lies outside its page (err_armed: a
+    // launch that can set it was enqueued since the last check), and a failed HIP call in an
+    // entry point that returns nothing (moearc_free_device).
+    uint32_t *err_word = nullptr;
+    bool err_armed = false;
+    bool deferred_error = false;
     std::vector<Pending> pending;
     std::vector<KernelTime> totals;
     std::vector<hipEvent_t> event_pool;
-    // split-K workspace: one partial record per work-group of the split kernel
+    // split-K workspace: the partial records of the split kernel (per query head and work item)
     float *ws = nullptr;
     size_t ws_floats = 0;
-    uint32_t *counters = nullptr;  // fused-merge arrival counters
-    size_t counters_n = 0;
-    int decode_variant_override = -1;  // MOEARC_DECODE_VARIANT, e.g. "4x4"
+    int decode_variant_override = -1;  // MOEARC_DECODE_VARIANT, e.g. "4x2x4"
     unsigned long split_override = 0;  // MOEARC_DECODE_SPLIT (keys per split)
     float *blk_ws = nullptr;  // attention-block chunk: q, k, v, f16 q, attention output, projection
     size_t blk_ws_bytes = 0;
@@ -146,12 +154,29 @@ void flush_events(moearc_ctx *c) {
 void record_bracket(moearc_ctx *c, hipEvent_t start, const char *what, unsigned long r,
                     unsigned long m) {
     hipEvent_t e1 = take_event(c);
-    if (!e1) return;
-    hipEventRecord(e1, c->stream);
+    if (!e1) {
+        c->event_pool.push_back(start);
+        return;
+    }
+    if (hipEventRecord(e1, c->stream) != hipSuccess) {
+        c->event_pool.push_back(start);
+        c->event_pool.push_back(e1);
+        return;
+    }
     char key[96];
     std::snprintf(key, sizeof(key), "%s r%lu m%lu", what, r, m);
     c->pending.push_back(Pending{key, start, e1});
     if (c->pending.size() >= 16384) flush_events(c);
+}
+
+// Whether a launch keyed `what` gets its own event bracket. Each tracked call is recorded once
+// under one key, as the reference records each submission (kernels.cpp:1905-1916): a kernel
+// launched inside a call that holds its own bracket (scope_depth > 0), or one whose entry point
+// the reference does not track (what == nullptr), is recorded only with MOEARC_PROFILE_KERNELS=1,
+// under "kernel <what>" -- consumers that sum every key then still count each call once.
+bool tracks(const moearc_ctx *c, const char *what) {
+    if (!c->profiling) return false;
+    return c->profile_kernels || (what && c->scope_depth == 0);
 }
 
 // Launch `f` with one by-value argument block. With profiling on, a HIP event pair brackets the
@@ -159,53 +184,50 @@ void record_bracket(moearc_ctx *c, hipEvent_t start, const char *what, unsigned 
 template <typename Args>
 int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, unsigned block,
              const Args &args, const char *what, unsigned long r, unsigned long m,
-             unsigned lds_bytes = 0) {
+             unsigned lds_bytes = 0, const char *kernel = nullptr) {
     if (!f) return ERR;
     hipEvent_t e0 = nullptr;
-    if (c->profiling && (e0 = take_event(c))) hipEventRecord(e0, c->stream);
+    const bool own = what && c->scope_depth == 0;  // this launch is the whole tracked call
+    if (tracks(c, what) && (e0 = take_event(c))) {
+        if (hipEventRecord(e0, c->stream) != hipSuccess) {
+            c->event_pool.push_back(e0);
+            e0 = nullptr;
+        }
+    }
     size_t size = sizeof(Args);
     void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *) &args, HIP_LAUNCH_PARAM_BUFFER_SIZE,
                       &size, HIP_LAUNCH_PARAM_END};
     const hipError_t err =
         hipModuleLaunchKernel(f, grid, grid_y, 1, block, 1, 1, lds_bytes, c->stream, nullptr, config);
-    if (e0) record_bracket(c, e0, what, r, m);
+    if (e0) {
+        if (own) {
+            record_bracket(c, e0, what, r, m);
+        } else {
+            char k[80];
+            std::snprintf(k, sizeof(k), "kernel %s", kernel ? kernel : (what ? what : "?"));
+            record_bracket(c, e0, k, r, m);
+        }
+    }
     return err == hipSuccess ? OK : ERR;
 }
 
 template <typename Args>
 int launch(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned block, const Args &args,
-           const char *what, unsigned long r, unsigned long m) {
-    return launch2d(c, f, grid, 1, block, args, what, r, m);
+           const char *what, unsigned long r, unsigned long m, const char *kernel = nullptr) {
+    return launch2d(c, f, grid, 1, block, args, what, r, m, 0, kernel);
 }
 
 int ensure_workspace(moearc_ctx *c, size_t floats) {
     if (floats <= c->ws_floats) return OK;
     if (c->ws) {
-        hipStreamSynchronize(c->stream);  // the previous workspace may still be in use
-        hipFree(c->ws);
+        // the previous workspace may still be read by queued launches
+        if (hipStreamSynchronize(c->stream) != hipSuccess) return ERR;
+        if (hipFree(c->ws) != hipSuccess) return ERR;
         c->ws = nullptr;
         c->ws_floats = 0;
     }
     if (hipMalloc((void **) &c->ws, floats * sizeof(float)) != hipSuccess) return ERR;
     c->ws_floats = floats;
-    return OK;
-}
-
-// Arrival counters of the fused decode merge. Each launch's last work-group per block resets its
-// counter, so they only need zeroing when allocated (by the zero kernel, on the stream).
-int ensure_counters(moearc_ctx *c, size_t n) {
-    if (n <= c->counters_n) return OK;
-    if (c->counters) {
-        hipStreamSynchronize(c->stream);
-        hipFree(c->counters);
-        c->counters = nullptr;
-        c->counters_n = 0;
-    }
-    n = std::max<size_t>(n, 1024);
-    if (hipMalloc((void **) &c->counters, n * sizeof(uint32_t)) != hipSuccess) return ERR;
-    const int rc = moearc_zero(c, (float *) c->counters, n);
-    if (rc) return rc;
-    c->counters_n = n;
     return OK;
 }
 
@@ -215,112 +237,180 @@ struct SeqSpan {
     uint32_t begin, end;
 };
 
+// The key spans of a decode call: the single call's (begin0, end0), or the batched call's host
+// arrays. Read in place, so the dispatch allocates nothing on the host either.
+struct SpanList {
+    const unsigned int *kv_begin = nullptr, *n_kv = nullptr;
+    uint32_t begin0 = 0, end0 = 0;
+    size_t n = 0;
+    SeqSpan at(size_t i) const { return kv_begin ? SeqSpan{kv_begin[i], n_kv[i]} : SeqSpan{begin0, end0}; }
+};
+
 // The split-K kernel masks keys with -inf scores before multiplying by scale*log2(e) and takes
 // its running maximum on raw scores, so it needs a positive, finite scale; any other scale runs on
 // the general kernel.
 bool fast_decode_ok(unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
                     unsigned long page_tokens, unsigned int kv_type, float scale) {
-    return kv_type == 1u && head_dim == 64 && n_heads / n_kv_heads <= 16 && is_pow2(page_tokens) &&
-           page_tokens <= (1ul << 30) && scale > 0.f && scale <= 3.0e38f;
+    return kv_type == 1u && head_dim == 64 && n_heads / n_kv_heads <= 16 && n_kv_heads <= 0xFFFFul &&
+           is_pow2(page_tokens) && page_tokens <= (1ul << 30) && scale > 0.f && scale <= 3.0e38f;
 }
 
-// Block-table entries the split-K kernel stages in LDS per work-group (PT_CAP in the kernel).
-constexpr uint64_t kPageTableCap = 1024;
-
-// Split-K decode variants: KV heads per work-group x waves per KV head (moearc_attn_decode_f16d64_*).
-// Split-K decode variants: kb KV heads x wpk waves per work-group (kernel f_dec_fast[kernel]), the
-// work-group count the split length aims for, and whether the splits are merged inside the launch
-// (by the last work-group of each block to finish) rather than by the merge kernel.
+// Split-K decode variants (moearc_attn_decode_f16d64_k<kb>w<wpk>t<tiles>): kb KV heads x wpk
+// waves per work-group, each wave computing `tiles` 32-key tiles per chunk with all of their loads
+// in flight; the work-group count the split length aims for.
 struct DecodeVariant {
     const char *name;
-    int kernel;
-    unsigned kb, wpk, target_wgs;
-    bool fused;
+    unsigned kb, wpk, tiles, target_wgs;
 };
-constexpr int kNumDecodeVariants = 8;
+constexpr int kNumDecodeVariants = 2;
 constexpr DecodeVariant kDecodeVariants[kNumDecodeVariants] = {
-    {"1x4", 0, 1, 4, 384, false},  {"1x16", 1, 1, 16, 384, false}, {"2x8", 2, 2, 8, 384, false},
-    {"4x4", 3, 4, 4, 384, false},  {"8x2", 4, 8, 2, 384, false},   {"1x4f", 0, 1, 4, 256, true},
-    {"1x8", 5, 1, 8, 384, false},  {"2x4", 6, 2, 4, 384, false},
+    {"4x2x4", 4, 2, 4, 256},  // 8 waves (2 per SIMD at 214 VGPRs): one work-group per CU
+    {"1x4x1", 1, 4, 1, 1024}, // 4 waves, many small work-groups: short spans, windows
 };
 
-// Variant and keys per split. A work-group reads kb*128 bytes of each key row (kb KV heads; four
-// keep HBM accesses row-local) with wpk waves per head; the split is sized so that the launch has
-// about the variant's target work-group count, rounded up to whole 32-key tiles per wave. Returns
-// false when a split would span more pages than the kernel stages.
-bool plan_split(moearc_ctx *c, const std::vector<SeqSpan> &spans, unsigned long G,
-                unsigned long page_tokens, int &variant, std::vector<uint32_t> &split_len) {
-    variant = G >= 4 ? 3 : (G == 2 ? 2 : (G == 1 ? 1 : 3));
-    if (c->decode_variant_override >= 0) variant = c->decode_variant_override;
-    uint64_t keys = 0;
-    for (auto &s : spans) keys += (uint64_t) (s.end - s.begin);
-    auto base_of = [&](int v) {
-        const uint64_t nkb = (G + kDecodeVariants[v].kb - 1) / kDecodeVariants[v].kb;
-        const uint64_t target_wgs = kDecodeVariants[v].target_wgs;
-        return (keys * nkb + target_wgs - 1) / target_wgs;
-    };
-    // Too few keys to give the 4-head work-groups full splits (short contexts, windowed layers):
-    // one-head work-groups of 4 waves give 4x the work-groups (measured: 4K keys 12.4 -> 10.4 us,
-    // 32 sequences of SWA-128 10.5 -> 7.8 us).
-    if (c->decode_variant_override < 0 && variant == 3 && base_of(3) < 32ull * kDecodeVariants[3].wpk)
-        variant = 0;
-    const unsigned wpk = kDecodeVariants[variant].wpk;
-    const uint64_t quantum = 32ull * wpk;  // one tile per wave
-    uint64_t base = base_of(variant);
-    split_len.resize(spans.size());
-    for (size_t i = 0; i < spans.size(); ++i) {
-        uint64_t len = c->split_override ? c->split_override : base;
-        len = std::max<uint64_t>(len, quantum);
-        len = (len + quantum - 1) / quantum * quantum;
-        if (len / page_tokens + 2 > kPageTableCap) return false;
-        split_len[i] = (uint32_t) std::min<uint64_t>(len, 0x40000000ull);
+// Variant and keys per split. The long-span variant reads 512 contiguous bytes of every key row
+// per work-group and keeps 32 KiB per wave in flight; it is used when the launch's keys give it
+// at least ~3/4 of a work-group per CU at one chunk per wave (config 2's 32768 keys give exactly
+// one), else the one-KV-head variant, which gives 8x the work-groups per key. The split length is
+// the shortest whole number of chunks for which the launch has at most the variant's target
+// work-group count (all resident at once: a second round of work-groups would start only as the
+// first finishes and double the time); ragged spans make the count a step function of the length,
+// hence the search.
+void plan_split(const moearc_ctx *c, const SeqSpan *spans, size_t cnt, unsigned long G, int &variant,
+                uint32_t &split_len) {
+    uint64_t keys = 0, longest = 0;
+    for (size_t i = 0; i < cnt; ++i) {
+        keys += (uint64_t) (spans[i].end - spans[i].begin);
+        longest = std::max<uint64_t>(longest, spans[i].end - spans[i].begin);
     }
-    return true;
+    auto nkb_of = [&](int v) { return (G + kDecodeVariants[v].kb - 1) / kDecodeVariants[v].kb; };
+    auto chunk_of = [&](int v) { return 32ull * kDecodeVariants[v].wpk * kDecodeVariants[v].tiles; };
+    variant = keys * nkb_of(0) / chunk_of(0) >= 192 ? 0 : 1;
+    if (c->decode_variant_override >= 0) variant = c->decode_variant_override;
+    const uint64_t quantum = chunk_of(variant), nkb = nkb_of(variant);
+    const uint64_t target = kDecodeVariants[variant].target_wgs;
+    auto wgs_at = [&](uint64_t len) {
+        uint64_t items = 0;
+        for (size_t i = 0; i < cnt; ++i) items += (spans[i].end - spans[i].begin + len - 1) / len;
+        return items * nkb;
+    };
+    uint64_t lo = 1, hi = std::max<uint64_t>(1, (longest + quantum - 1) / quantum);  // in chunks
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi) / 2;
+        if (wgs_at(mid * quantum) <= target) hi = mid;
+        else lo = mid + 1;
+    }
+    uint64_t len = c->split_override ? c->split_override : lo * quantum;
+    len = std::max<uint64_t>(len, quantum);
+    len = (len + quantum - 1) / quantum * quantum;
+    split_len = (uint32_t) std::min<uint64_t>(len, 0x40000000ull);
+}
+
+// Launch layouts. The leading scalars are the kernel's preloaded arguments (the code object is
+// built with kernarg preloading of 14 dwords); the struct follows at its natural alignment, as the
+// kernel's parameter list places it.
+struct DecodeLaunch {
+    const uint16_t *k_pages, *v_pages;
+    const uint32_t *bt0;
+    const float *q0;
+    uint32_t kvb0, nkv0, slen0, next0;
+    uint32_t geo0, geo1;
+    DecodeArgs a;
+};
+struct MergeLaunch {
+    const float *rec_o, *rec_ml;
+    void *out;
+    const float *sinks;
+    uint32_t n_items, next0, n_heads, out_f16;
+    MergeArgs m;
+};
+static_assert(offsetof(DecodeLaunch, a) == 56, "decode kernel argument layout");
+static_assert(offsetof(MergeLaunch, m) == 48 && sizeof(MergeLaunch) == 48 + sizeof(MergeArgs),
+              "merge kernel argument layout");
+static_assert(sizeof(DecodeLaunch) == 56 + sizeof(DecodeArgs), "decode kernel argument layout");
+
+// Where a decode call keeps its partial records: the context's workspace (grown on demand), or a
+// fixed buffer of `cap` floats that the call must fit (the allocation-free entry point).
+struct RecordSpace {
+    float *fixed = nullptr;
+    size_t cap = 0;
+};
+
+// The spans of launch group s0 (at most MOEARC_MAX_SEQS_PER_LAUNCH sequences) into sub[].
+size_t group_spans(const SpanList &spans, size_t s0, SeqSpan *sub) {
+    const size_t cnt = std::min<size_t>(MOEARC_MAX_SEQS_PER_LAUNCH, spans.n - s0);
+    for (size_t i = 0; i < cnt; ++i) sub[i] = spans.at(s0 + i);
+    return cnt;
+}
+
+// Work items (splits over all sequences) of a launch group under its plan.
+uint64_t group_items(const SeqSpan *sub, size_t cnt, uint32_t split_len) {
+    uint64_t items = 0;
+    for (size_t i = 0; i < cnt; ++i) items += (sub[i].end - sub[i].begin + (uint64_t) split_len - 1) / split_len;
+    return items;
 }
 
 int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
                        const void *k_pages, const void *v_pages, const unsigned int *block_tables,
-                       unsigned long bt_stride, const std::vector<SeqSpan> &spans,
-                       const float *sinks, unsigned long n_heads, unsigned long n_kv_heads,
-                       unsigned long head_dim, unsigned long page_tokens, float scale,
-                       unsigned int kv_type, size_t nseq, size_t per);
+                       unsigned long bt_stride, const SpanList &spans, const float *sinks,
+                       unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
+                       unsigned long page_tokens, float scale, unsigned int kv_type, RecordSpace rs);
 
 int decode_launch(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
                   const void *k_pages, const void *v_pages, const unsigned int *block_tables,
-                  unsigned long bt_stride, const std::vector<SeqSpan> &spans, const float *sinks,
+                  unsigned long bt_stride, const SpanList &spans, const float *sinks,
                   unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
-                  unsigned long page_tokens, float scale, unsigned int kv_type) {
-    const size_t nseq = spans.size();
-    const size_t per = MOEARC_MAX_SEQS_PER_LAUNCH;
-    // With profiling on, the whole call is one bracket under the reference's key; the kernels it
-    // launches are also timed under their own keys.
+                  unsigned long page_tokens, float scale, unsigned int kv_type, RecordSpace rs = {}) {
+    // A fixed record buffer must hold every launch group's records: checked for all groups before
+    // anything is enqueued, so a refusal leaves the stream untouched.
+    if (rs.fixed && fast_decode_ok(n_heads, n_kv_heads, head_dim, page_tokens, kv_type, scale)) {
+        SeqSpan sub[MOEARC_MAX_SEQS_PER_LAUNCH];
+        for (size_t s0 = 0; s0 < spans.n; s0 += MOEARC_MAX_SEQS_PER_LAUNCH) {
+            const size_t cnt = group_spans(spans, s0, sub);
+            int variant = 0;
+            uint32_t split_len = 0;
+            plan_split(c, sub, cnt, n_kv_heads, variant, split_len);
+            const uint64_t items = group_items(sub, cnt, split_len);
+            if (items > cnt && (uint64_t) n_heads * items * 66u > rs.cap) return ERR_ARG;
+        }
+    }
+    // With profiling on, the whole call (split and merge launches, SWA and full layers alike) is
+    // one bracket under the reference's key "attn_decode r<n_heads> m<head_dim>"
+    // (kernels.cpp:1905-1916); its kernels are timed on their own only with
+    // MOEARC_PROFILE_KERNELS=1. The allocation-free entry point records no events.
     hipEvent_t call0 = nullptr;
-    if (c->profiling && (call0 = take_event(c))) hipEventRecord(call0, c->stream);
+    if (!rs.fixed && tracks(c, "attn_decode") && (call0 = take_event(c))) {
+        if (hipEventRecord(call0, c->stream) != hipSuccess) {
+            c->event_pool.push_back(call0);
+            call0 = nullptr;
+        }
+    }
+    ++c->scope_depth;
     const int rc_all = decode_launch_body(c, out, out_f16, q, k_pages, v_pages, block_tables,
                                           bt_stride, spans, sinks, n_heads, n_kv_heads, head_dim,
-                                          page_tokens, scale, kv_type, nseq, per);
+                                          page_tokens, scale, kv_type, rs);
+    --c->scope_depth;
     if (call0) record_bracket(c, call0, "attn_decode", n_heads, head_dim);
     return rc_all;
 }
 
 int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const float *q,
                        const void *k_pages, const void *v_pages, const unsigned int *block_tables,
-                       unsigned long bt_stride, const std::vector<SeqSpan> &spans,
-                       const float *sinks, unsigned long n_heads, unsigned long n_kv_heads,
-                       unsigned long head_dim, unsigned long page_tokens, float scale,
-                       unsigned int kv_type, size_t nseq, size_t per) {
+                       unsigned long bt_stride, const SpanList &spans, const float *sinks,
+                       unsigned long n_heads, unsigned long n_kv_heads, unsigned long head_dim,
+                       unsigned long page_tokens, float scale, unsigned int kv_type, RecordSpace rs) {
     const bool fast_shape = fast_decode_ok(n_heads, n_kv_heads, head_dim, page_tokens, kv_type, scale);
-    for (size_t s0 = 0; s0 < nseq; s0 += per) {
-        const size_t cnt = std::min(per, nseq - s0);
+    SeqSpan sub[MOEARC_MAX_SEQS_PER_LAUNCH];
+    for (size_t s0 = 0; s0 < spans.n; s0 += MOEARC_MAX_SEQS_PER_LAUNCH) {
+        const size_t cnt = group_spans(spans, s0, sub);
         const float *qb = q + s0 * n_heads * head_dim;
         const size_t out_off = s0 * n_heads * head_dim * (out_f16 ? 2 : 4);
         void *ob = (char *) out + out_off;
         const unsigned int *btb = block_tables + s0 * bt_stride;
-        std::vector<SeqSpan> sub(spans.begin() + s0, spans.begin() + s0 + cnt);
-        int variant = 3;
-        std::vector<uint32_t> split_len;
-        const bool fast = fast_shape && plan_split(c, sub, n_kv_heads, page_tokens, variant, split_len);
-        if (!fast) {
+        int variant = 0;
+        uint32_t split_len = 0;
+        if (fast_shape) plan_split(c, sub, cnt, n_kv_heads, variant, split_len);
+        if (!fast_shape) {
             DecodeGeneralArgs a{};
             a.q = qb;
             a.k_pages = k_pages;
@@ -338,61 +428,102 @@ int decode_launch_body(moearc_ctx *c, void *out, unsigned int out_f16, const flo
             a.scale = scale;
             a.n_seqs = (uint32_t) cnt;
             for (size_t i = 0; i < cnt; ++i) {
-                a.kv_begin[i] = spans[s0 + i].begin;
-                a.n_kv[i] = spans[s0 + i].end;
+                a.kv_begin[i] = sub[i].begin;
+                a.n_kv[i] = sub[i].end;
             }
             const int rc = launch(c, c->f_dec_general, (unsigned) (cnt * n_heads), 256, a,
                                   "attn_decode.general", n_heads, head_dim);
             if (rc) return rc;
             continue;
         }
-        DecodeArgs a{};
+        const DecodeVariant &dv = kDecodeVariants[variant];
+        const size_t nkb = (n_kv_heads + dv.kb - 1) / dv.kb;
+        DecodeLaunch L{};
+        DecodeArgs &a = L.a;
         a.q = qb;
-        a.k_pages = (const uint16_t *) k_pages;
-        a.v_pages = (const uint16_t *) v_pages;
         a.block_tables = btb;
         a.sinks = sinks;
         a.out = ob;
         a.bt_stride = bt_stride;
-        a.n_heads = (uint32_t) n_heads;
-        a.n_kv_heads = (uint32_t) n_kv_heads;
-        a.group = (uint32_t) (n_heads / n_kv_heads);
-        a.pt_shift = log2u(page_tokens);
         a.out_f16 = out_f16;
         a.scale_log2e = scale * 1.4426950408889634f;
         a.n_seqs = (uint32_t) cnt;
-        const unsigned kb = kDecodeVariants[variant].kb, wpk = kDecodeVariants[variant].wpk;
-        const size_t nkb = (n_kv_heads + kb - 1) / kb;
-        a.nkb = (uint32_t) nkb;
         uint32_t items = 0;
         for (size_t i = 0; i < cnt; ++i) {
             a.item_begin[i] = items;
             a.kv_begin[i] = sub[i].begin;
             a.n_kv[i] = sub[i].end;
-            a.split_len[i] = split_len[i];
-            items += (sub[i].end - sub[i].begin + split_len[i] - 1) / split_len[i];
+            a.split_len[i] = split_len;
+            const uint64_t n_split = (sub[i].end - sub[i].begin + (uint64_t) split_len - 1) / split_len;
+            if (items + n_split > 0x7FFFFFFFull) return ERR_ARG;
+            items += (uint32_t) n_split;
         }
         for (size_t i = cnt; i <= MOEARC_MAX_SEQS_PER_LAUNCH; ++i) a.item_begin[i] = items;
         const size_t wgs = (size_t) items * nkb;
         if (wgs > 0x7FFFFFFFull) return ERR_ARG;
-        if (ensure_workspace(c, (size_t) items * n_kv_heads * MOEARC_PARTIAL_FLOATS)) return ERR;
-        a.ws = c->ws;
         const bool any_split = items > cnt;  // some sequence has more than one split
-        const bool fused = kDecodeVariants[variant].fused && any_split;
-        if (fused) {
-            if (ensure_counters(c, cnt * nkb)) return ERR;
-            a.counters = c->counters;
+        if (any_split) {
+            const size_t rec = (size_t) n_heads * items;
+            float *ws = rs.fixed;
+            if (ws) {
+                if (rec * 66 > rs.cap) return ERR_ARG;  // checked for every group before the first launch
+            } else {
+                if (ensure_workspace(c, rec * 66)) return ERR;
+                ws = c->ws;
+            }
+            a.rec_o = ws;
+            a.rec_ml = ws + rec * 64;
         }
-        const int rc = launch(c, c->f_dec_fast[kDecodeVariants[variant].kernel], (unsigned) wgs,
-                              64u * kb * wpk, a, "attn_decode.split", n_heads, head_dim);
+        a.n_items = items;
+        L.k_pages = (const uint16_t *) k_pages;
+        L.v_pages = (const uint16_t *) v_pages;
+        L.bt0 = btb;
+        L.q0 = qb;
+        L.kvb0 = a.kv_begin[0];
+        L.nkv0 = a.n_kv[0];
+        L.slen0 = a.split_len[0];
+        L.next0 = a.item_begin[1];
+        L.geo0 = log2u(page_tokens) | (uint32_t) n_kv_heads << 16;
+        L.geo1 = (uint32_t) nkb | (uint32_t) (n_heads / n_kv_heads) << 16;
+        const int rc = launch(c, c->f_dec_fast[variant], (unsigned) wgs, 64u * dv.kb * dv.wpk, L,
+                              "attn_decode.split", n_heads, head_dim);
         if (rc) return rc;
-        if (any_split && !fused) {
-            const int rm = launch2d(c, c->f_dec_merge, (unsigned) (n_heads * MOEARC_MERGE_PARTS), (unsigned) cnt,
-                                    c->merge_threads, a, "attn_decode.merge", n_heads, head_dim);
+        if (any_split) {
+            MergeLaunch M{};
+            M.rec_o = a.rec_o;
+            M.rec_ml = a.rec_ml;
+            M.out = ob;
+            M.sinks = sinks;
+            M.n_items = items;
+            M.next0 = a.item_begin[1];
+            M.n_heads = (uint32_t) n_heads;
+            M.out_f16 = out_f16;
+            for (size_t i = 0; i <= MOEARC_MAX_SEQS_PER_LAUNCH; ++i) M.m.item_begin[i] = a.item_begin[i];
+            M.m.item_begin[MOEARC_MAX_SEQS_PER_LAUNCH + 1] = items;
+            const int rm = launch2d(c, c->f_dec_merge, (unsigned) n_heads, (unsigned) cnt, c->merge_threads,
+                                    M, "attn_decode.merge", n_heads, head_dim);
             if (rm) return rm;
         }
     }
     return OK;
+}
+
+// Frees everything a (possibly half-built) context holds and returns nullptr. Teardown has no
+// caller to report a failure to (moearc_ctx_destroy returns nothing, ffi.rs:21), so the results
+// of these calls are deliberately dropped.
+moearc_ctx *release(moearc_ctx *c) {
+    if (c->stream) (void) hipStreamSynchronize(c->stream);
+    for (auto &p : c->pending) {
+        (void) hipEventDestroy(p.start);
+        (void) hipEventDestroy(p.stop);
+    }
+    for (auto e : c->event_pool) (void) hipEventDestroy(e);
+    for (void *p : {(void *) c->ws, (void *) c->blk_ws, (void *) c->mm_ws, (void *) c->err_word})
+        if (p) (void) hipFree(p);
+    if (c->module) (void) hipModuleUnload(c->module);
+    if (c->stream) (void) hipStreamDestroy(c->stream);
+    delete c;
+    return nullptr;
 }
 
 }  // namespace
@@ -402,27 +533,20 @@ extern "C" {
 moearc_ctx *moearc_ctx_create(void) {
     auto *c = new moearc_ctx();
     int n = 0;
-    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
-        delete c;
-        return nullptr;
-    }
-    if (hipGetDevice(&c->device) != hipSuccess) {
-        delete c;
-        return nullptr;
-    }
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || hipGetDevice(&c->device) != hipSuccess)
+        return release(c);
     // Default priority, in-order (the reference's in-order queue, kernels.cpp:806-810).
-    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
-        delete c;
-        return nullptr;
-    }
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return release(c);
     const char *co_env = std::getenv("MOEARC_CODE_OBJECT");
     const std::string co = co_env ? std::string(co_env) : library_dir() + "/moearc_attn_gfx950.co";
     if (hipModuleLoad(&c->module, co.c_str()) != hipSuccess) {
         std::fprintf(stderr, "moearc: cannot load code object %s\n", co.c_str());
-        hipStreamDestroy(c->stream);
-        delete c;
-        return nullptr;
+        return release(c);
     }
+    const uint32_t zero = 0;
+    if (hipMalloc((void **) &c->err_word, 256) != hipSuccess ||
+        hipMemcpy(c->err_word, &zero, 4, hipMemcpyHostToDevice) != hipSuccess)
+        return release(c);
     struct {
         hipFunction_t *slot;
         const char *name;
@@ -434,14 +558,9 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_rope, "moearc_rope_k"},
         {&c->f_rope_append_chunk, "moearc_rope_kv_append_chunk_k"},
         {&c->f_dec_general, "moearc_attn_decode_general_k"},
-        {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k1w4"},
-        {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w16"},
-        {&c->f_dec_fast[2], "moearc_attn_decode_f16d64_k2w8"},
-        {&c->f_dec_fast[3], "moearc_attn_decode_f16d64_k4w4"},
-        {&c->f_dec_fast[4], "moearc_attn_decode_f16d64_k8w2"},
-        {&c->f_dec_fast[5], "moearc_attn_decode_f16d64_k1w8"},
-        {&c->f_dec_fast[6], "moearc_attn_decode_f16d64_k2w4"},
-        {&c->f_dec_merge, "moearc_attn_decode_merge"},
+        {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k4w2t4"},
+        {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w4t1"},
+        {&c->f_dec_merge, "moearc_attn_decode_merge_p1"},
         {&c->f_add, "moearc_add_k"},
         {&c->f_mm[0][0], "moearc_matmul_q8_0_r1_k"},
         {&c->f_mm[0][1], "moearc_matmul_q8_0_r2_k"},
@@ -461,20 +580,14 @@ moearc_ctx *moearc_ctx_create(void) {
     for (auto &f : fns) {
         if (hipModuleGetFunction(f.slot, c->module, f.name) != hipSuccess) {
             std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), f.name);
-            hipModuleUnload(c->module);
-            hipStreamDestroy(c->stream);
-            delete c;
-            return nullptr;
+            return release(c);
         }
     }
     int merge_threads = 0;
     if (hipFuncGetAttribute(&merge_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_dec_merge) !=
             hipSuccess || merge_threads != MOEARC_MERGE_THREADS) {
         std::fprintf(stderr, "moearc: cannot read the merge kernel's work-group size\n");
-        hipModuleUnload(c->module);
-        hipStreamDestroy(c->stream);
-        delete c;
-        return nullptr;
+        return release(c);
     }
     c->merge_threads = (unsigned) merge_threads;
     if (const char *pp = std::getenv("MOEARC_PREFILL_PRECISE")) c->prefill_precise = pp[0] == '1';
@@ -485,10 +598,7 @@ moearc_ctx *moearc_ctx_create(void) {
         hipFunction_t *slot = precise ? &c->f_prefill_precise[i & 3] : &c->f_prefill[i & 3];
         if (hipModuleGetFunction(slot, c->module, name) != hipSuccess) {
             std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), name);
-            hipModuleUnload(c->module);
-            hipStreamDestroy(c->stream);
-            delete c;
-            return nullptr;
+            return release(c);
         }
     }
     for (int t = 0; t < 7; ++t) {
@@ -498,10 +608,7 @@ moearc_ctx *moearc_ctx_create(void) {
             std::snprintf(name, sizeof(name), "moearc_matvec_%s_p%u", kMvNames[t], 1u << i);
             if (hipModuleGetFunction(&c->f_mv[t][i], c->module, name) != hipSuccess) {
                 std::fprintf(stderr, "moearc: code object %s lacks kernel %s\n", co.c_str(), name);
-                hipModuleUnload(c->module);
-                hipStreamDestroy(c->stream);
-                delete c;
-                return nullptr;
+                return release(c);
             }
         }
     }
@@ -511,7 +618,9 @@ moearc_ctx *moearc_ctx_create(void) {
         if (v == 4 || v == 8) c->mv_waves_override = (unsigned) v;
     }
     const char *ev = std::getenv("MOEARC_PROFILE_EVENTS");
-    c->profiling = ev && ev[0] == '1';
+    const char *ek = std::getenv("MOEARC_PROFILE_KERNELS");
+    c->profile_kernels = ek && ek[0] == '1';
+    c->profiling = (ev && ev[0] == '1') || c->profile_kernels;
     if (const char *w = std::getenv("MOEARC_DECODE_VARIANT")) {
         for (int i = 0; i < kNumDecodeVariants; ++i)
             if (std::strcmp(w, kDecodeVariants[i].name) == 0) c->decode_variant_override = i;
@@ -522,19 +631,7 @@ moearc_ctx *moearc_ctx_create(void) {
 
 void moearc_ctx_destroy(moearc_ctx *c) {
     if (!c) return;
-    hipStreamSynchronize(c->stream);
-    for (auto &p : c->pending) {
-        hipEventDestroy(p.start);
-        hipEventDestroy(p.stop);
-    }
-    for (auto e : c->event_pool) hipEventDestroy(e);
-    if (c->ws) hipFree(c->ws);
-    if (c->counters) hipFree(c->counters);
-    if (c->blk_ws) hipFree(c->blk_ws);
-    if (c->mm_ws) hipFree(c->mm_ws);
-    if (c->module) hipModuleUnload(c->module);
-    if (c->stream) hipStreamDestroy(c->stream);
-    delete c;
+    release(c);
 }
 
 // The host computes theta_scale as the reference does before its launch (kernels.cpp:1406).
@@ -575,7 +672,7 @@ int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
     } a{dst, src, pos, n_tokens, (uint32_t) n_heads, (uint32_t) head_dim,
         rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
     return launch2d(c, c->f_rope, (unsigned) ((threads + 255) / 256), (unsigned) groups, 256, a,
-                    "rope", n_heads, head_dim);
+                    nullptr, n_heads, head_dim, 0, "rope");
 }
 
 int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
@@ -604,9 +701,12 @@ int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, con
         uint64_t pt;
         uint32_t kv_type;
         RopeParams r;
+        uint32_t *err;
     } a{k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, (uint32_t) n_kv_heads,
         (uint32_t) head_dim, page_tokens, kv_type,
-        rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
+        rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox),
+        c->err_word};
+    c->err_armed = true;
     return launch2d(c, c->f_rope_append_chunk, (unsigned) ((threads + 255) / 256), (unsigned) groups,
                     256, a, "rope_kv_append_chunk", n_kv_heads, head_dim);
 }
@@ -643,7 +743,24 @@ int moearc_profile_events_report(moearc_ctx *c, char *out, unsigned long cap) {
 
 int moearc_sync(moearc_ctx *c) {
     if (!c) return ERR;
-    return hipStreamSynchronize(c->stream) == hipSuccess ? OK : ERR;
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return ERR;
+    bool failed = c->deferred_error;
+    c->deferred_error = false;
+    if (c->err_armed) {
+        c->err_armed = false;
+        uint32_t word = 0;
+        if (hipMemcpyAsync(&word, c->err_word, 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+            hipStreamSynchronize(c->stream) != hipSuccess)
+            return ERR;
+        if (word != 0) {
+            const uint32_t zero = 0;
+            if (hipMemcpyAsync(c->err_word, &zero, 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+                hipStreamSynchronize(c->stream) != hipSuccess)
+                return ERR;
+            failed = true;
+        }
+    }
+    return failed ? ERR : OK;
 }
 
 int moearc_zero(moearc_ctx *c, float *dst, unsigned long n) {
@@ -654,14 +771,18 @@ int moearc_zero(moearc_ctx *c, float *dst, unsigned long n) {
         float *d;
         uint64_t n;
     } a{dst, n};
-    return launch(c, c->f_zero, grid, 256, a, "zero", n, 0);
+    return launch(c, c->f_zero, grid, 256, a, nullptr, n, 0, "zero");
 }
 
 int moearc_device_name(moearc_ctx *c, char *out, unsigned long cap) {
     if (!c || !out || cap == 0) return ERR;
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, c->device) != hipSuccess) return ERR;
-    std::snprintf(out, cap, "%s (%s)", p.name, p.gcnArchName);
+    char name[256] = {0};
+    if (p.name[0]) std::snprintf(name, sizeof(name), "%s", p.name);
+    else if (hipDeviceGetName(name, (int) sizeof(name), c->device) != hipSuccess || !name[0])
+        std::snprintf(name, sizeof(name), "device %d", c->device);
+    std::snprintf(out, cap, "%s (%s, %d CUs)", name, p.gcnArchName, p.multiProcessorCount);
     return OK;
 }
 
@@ -674,8 +795,8 @@ void *moearc_alloc_device(moearc_ctx *c, unsigned long bytes) {
 
 void moearc_free_device(moearc_ctx *c, void *p) {
     if (!c || !p) return;
-    hipStreamSynchronize(c->stream);
-    hipFree(p);
+    // no return code in the reference's signature (ffi.rs:33): a failure surfaces at moearc_sync
+    if (hipStreamSynchronize(c->stream) != hipSuccess || hipFree(p) != hipSuccess) c->deferred_error = true;
 }
 
 int moearc_copy_h2d(moearc_ctx *c, void *dst, const void *src, unsigned long bytes) {
@@ -801,10 +922,22 @@ int mv_launch(moearc_ctx *c, unsigned ty, const MvJob *jobs, unsigned n, unsigne
     a.rpw = rpw;
     a.x_in_lds = x_in_lds;
     a.x_lds_bytes = (uint32_t) x_bytes;
-    char key[48];
-    std::snprintf(key, sizeof(key), "%s %s", what, kMvKeys[t]);
-    return launch2d(c, c->f_mv[t][li], (unsigned) wgs, 1, 64u * waves, a, key, key_r, key_m,
-                    (unsigned) (x_bytes + (uint64_t) waves * wave_buf));
+    // Keys of the reference's matvec entry points (kernels.cpp:1057-1111, :1168-1196): "mvq <type>"
+    // and "mvq_batched <type>" for the block formats, "mv_generic ... m1" for F32/F16 weights;
+    // moearc_matvec_f32 is not tracked there (what == nullptr); this build's fused entry points
+    // keep their own names with the type appended.
+    char key[48], kname[48];
+    const bool generic = ty == 0u || ty == 1u;
+    const bool ref_entry = what && (std::strcmp(what, "mvq") == 0 || std::strcmp(what, "mvq_batched") == 0);
+    if (ref_entry && generic) {
+        std::snprintf(key, sizeof(key), "mv_generic");
+        key_m = 1;
+    } else if (what) {
+        std::snprintf(key, sizeof(key), "%s %s", what, kMvKeys[t]);
+    }
+    std::snprintf(kname, sizeof(kname), "matvec %s", kMvKeys[t]);
+    return launch2d(c, c->f_mv[t][li], (unsigned) wgs, 1, 64u * waves, a, what ? key : nullptr, key_r,
+                    key_m, (unsigned) (x_bytes + (uint64_t) waves * wave_buf), kname);
 }
 
 }  // namespace
@@ -839,7 +972,7 @@ int moearc_matvec_f32(moearc_ctx *c, float *out, const float *w, const float *x,
     if (n_rows == 0) return OK;
     if (const int rc = mv_check(0, n_rows, n_cols)) return rc;
     const MvJob j{w, x, nullptr, out, n_rows};
-    return mv_launch(c, 0, &j, 1, n_cols, "mvf32", n_rows, 1);
+    return mv_launch(c, 0, &j, 1, n_cols, nullptr, n_rows, 1);
 }
 
 int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsigned long n) {
@@ -851,7 +984,7 @@ int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsign
         const float *a, *b;
         uint64_t n;
     } args{out, a, b, n};
-    return launch(c, c->f_add, grid, 256, args, "add", n, 0);
+    return launch(c, c->f_add, grid, 256, args, nullptr, n, 0, "add");
 }
 
 int moearc_attn_out(moearc_ctx *c, unsigned int type_id, float *h, const void *w, const float *bias,
@@ -896,7 +1029,7 @@ int moearc_quantize_f16(moearc_ctx *c, void *dst, const float *src, unsigned lon
         const float *s;
         uint64_t n;
     } a{dst, src, n};
-    return launch(c, c->f_quant, grid, 256, a, "quantize_f16", n, 0);
+    return launch(c, c->f_quant, grid, 256, a, nullptr, n, 0, "quantize_f16");
 }
 
 int moearc_kv_append(moearc_ctx *c, void *k_pages, void *v_pages, const float *k, const float *v,
@@ -913,7 +1046,7 @@ int moearc_kv_append(moearc_ctx *c, void *k_pages, void *v_pages, const float *k
         uint64_t base, row;
         uint32_t kv_type;
     } a{k_pages, v_pages, k, v, ((uint64_t) page_id * page_tokens + slot) * row, row, kv_type};
-    return launch(c, c->f_append, (unsigned) ((row + 255) / 256), 256, a, "kv_append", n_kv_heads,
+    return launch(c, c->f_append, (unsigned) ((row + 255) / 256), 256, a, nullptr, n_kv_heads,
                   head_dim);
 }
 
@@ -934,7 +1067,9 @@ int moearc_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const fl
         const uint32_t *pages, *slots;
         uint64_t n_tok, row, pt;
         uint32_t kv_type;
-    } a{k_pages, v_pages, k, v, page_ids, slots, n_tok, row, page_tokens, kv_type};
+        uint32_t *err;
+    } a{k_pages, v_pages, k, v, page_ids, slots, n_tok, row, page_tokens, kv_type, c->err_word};
+    c->err_armed = true;
     return launch(c, c->f_append_chunk, (unsigned) ((total + 255) / 256), 256, a, "kv_append_chunk",
                   n_kv_heads, head_dim);
 }
@@ -953,7 +1088,10 @@ int moearc_attn_decode(moearc_ctx *c, float *out, const float *q, const void *k_
     if (kv_begin >= n_kv) return ERR_ARG;
     if (head_dim > 1024) return ERR_ARG;
     if (n_kv > 0xFFFFFFFFul) return ERR_ARG;  // keys are indexed in 32 bits on the device
-    std::vector<SeqSpan> spans{SeqSpan{(uint32_t) kv_begin, (uint32_t) n_kv}};
+    SpanList spans;
+    spans.begin0 = (uint32_t) kv_begin;
+    spans.end0 = (uint32_t) n_kv;
+    spans.n = 1;
     const unsigned long bt_stride = (n_kv + page_tokens - 1) / page_tokens;
     return decode_launch(c, out, 0u, q, k_pages, v_pages, block_table, bt_stride, spans, sinks,
                          n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type);
@@ -973,12 +1111,14 @@ int moearc_attn_decode_batched(moearc_ctx *c, void *out, unsigned int out_type, 
         return ERR_ARG;
     if (n_heads % n_kv_heads != 0) return ERR_ARG;
     if (head_dim > 1024) return ERR_ARG;
-    std::vector<SeqSpan> spans(n_seqs);
     for (unsigned long b = 0; b < n_seqs; ++b) {
         if (n_kv[b] == 0 || kv_begin[b] >= n_kv[b]) return ERR_ARG;
         if ((n_kv[b] + page_tokens - 1) / page_tokens > bt_stride) return ERR_ARG;
-        spans[b] = SeqSpan{kv_begin[b], n_kv[b]};
     }
+    SpanList spans;
+    spans.kv_begin = kv_begin;
+    spans.n_kv = n_kv;
+    spans.n = n_seqs;
     return decode_launch(c, out, out_type, q, k_pages, v_pages, block_tables, bt_stride, spans,
                          sinks, n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type);
 }
@@ -1080,8 +1220,7 @@ int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **
     const size_t halves = 2 * n + n / 16;  // hi, lo, then n / 32 floats
     if (halves > c->mm_ws_halves) {
         if (c->mm_ws) {
-            hipStreamSynchronize(c->stream);
-            hipFree(c->mm_ws);
+            if (hipStreamSynchronize(c->stream) != hipSuccess || hipFree(c->mm_ws) != hipSuccess) return ERR;
             c->mm_ws = nullptr;
             c->mm_ws_halves = 0;
         }
@@ -1153,14 +1292,20 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     if (D != 64 || !is_pow2(b->page_tokens) || (group != 1 && group != 2 && group != 4 && group != 8) ||
         pos0 + n_tok > 0xFFFFFFFFul || b->n_rot == 0 || b->n_rot % 2 != 0 || b->n_rot > D)
         return ERR_ARG;
+    // A windowed block read through a ring: the chunk's K/V are written before its queries attend,
+    // so while the first query attends the live keys run from its window start to the chunk's last
+    // token, n_tok + n_swa - 1 of them; a smaller ring would let later tokens overwrite keys that
+    // earlier rows still read.
+    if (b->n_swa > 0 && b->ring_pages > 0 &&
+        (unsigned long long) n_tok + b->n_swa - 1 > (unsigned long long) b->ring_pages * b->page_tokens)
+        return ERR_ARG;
 
     // working memory: q, k, v, rotated q, f16 q, attention output, projection
     const size_t nq = n_tok * q_rows, nkv = n_tok * kv_rows;
     const size_t floats = nq + 2 * nkv + nq + (nq + 1) / 2 + nq + n_tok * E;
     if (floats * sizeof(float) > c->blk_ws_bytes) {
         if (c->blk_ws) {
-            hipStreamSynchronize(c->stream);
-            hipFree(c->blk_ws);
+            if (hipStreamSynchronize(c->stream) != hipSuccess || hipFree(c->blk_ws) != hipSuccess) return ERR;
             c->blk_ws = nullptr;
             c->blk_ws_bytes = 0;
         }

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol():
 def test_code_object_holds_every_kernel_the_runtime_loads():
     blob = open(native.CODE_OBJECT, "rb").read()
     src = open(os.path.join(ROOT, "moearc_amd", "csrc", "runtime.cpp")).read()
-    kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_w\d+|moearc_attn_decode_merge)"', src))
+    kernels = set(re.findall(r'"(moearc_\w+_k|moearc_attn_decode_f16d64_k\d+w\d+t\d+|moearc_attn_decode_merge)"', src))
     kernels |= {f"moearc_attn_prefill_{v}g{g}" for v in ("", "precise_") for g in (1, 2, 4, 8)}
     kernels |= {f"moearc_matmul_{t}_r{r}_k" for t in ("q8_0", "f16", "q4_k", "q5_k", "q6_k", "mxfp4") for r in (1, 2)}
     kernels |= {"moearc_split_f16_k", "moearc_block_sums_k"}
@@ -92,3 +92,52 @@ def test_missing_build_fails_loudly(monkeypatch):
     monkeypatch.setattr(native, "LIBRARY", "/nonexistent/libmoearc_attn.so")
     with pytest.raises(native.NativeLibraryMissing):
         native.load()
+
+
+def _c_arity(path):
+    src = open(path).read()
+    out = {}
+    for m in re.finditer(r"^(?:int|void|void \*|moearc_ctx \*)\s*\*?\s*(moearc_\w+)\s*\(([^;]*?)\);", src,
+                         re.M | re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("void", "") else args.count(",") + 1
+    return out
+
+
+def _rust_arity(path):
+    src = open(path).read()
+    out = {}
+    for m in re.finditer(r"pub fn (moearc_\w+)\s*\((.*?)\)\s*(?:->|;)", src, re.S):
+        args = m.group(2).strip().rstrip(",")
+        out[m.group(1)] = 0 if not args else args.count(",") + 1
+    return out
+
+
+def test_rust_ffi_crate_declares_the_headers():
+    # crates/moearc-hip/src/{ffi,kv_ffi}.rs are hand-written like the reference's ffi.rs: every C
+    # declaration appears there once, with the same number of arguments
+    c = {**_c_arity(os.path.join(ROOT, "include", "moearc_attn.h")),
+         **_c_arity(os.path.join(ROOT, "include", "moearc_kv.h"))}
+    rs = {**_rust_arity(os.path.join(ROOT, "crates", "moearc-hip", "src", "ffi.rs")),
+          **_rust_arity(os.path.join(ROOT, "crates", "moearc-hip", "src", "kv_ffi.rs"))}
+    assert c and set(c) == set(rs)
+    assert {k: c[k] for k in c} == {k: rs[k] for k in c}
+
+
+def test_rust_block_descriptor_matches_the_header():
+    # the moearc_attn_block field order, as declared in C, in the Rust struct and in the ctypes one
+    hdr = open(os.path.join(ROOT, "include", "moearc_attn.h")).read()
+    body = hdr[hdr.index("typedef struct moearc_attn_block {"):hdr.index("} moearc_attn_block;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    c_fields = []
+    for decl in body.split("{", 1)[1].split(";"):
+        decl = decl.strip()
+        if decl:
+            c_fields += [re.sub(r"[\*\[\]0-9]", "", n).strip().split()[-1] for n in decl.split(",")]
+    rs = open(os.path.join(ROOT, "crates", "moearc-hip", "src", "ffi.rs")).read()
+    rs_body = rs[rs.index("pub struct MoearcAttnBlock {"):]
+    rs_body = rs_body[:rs_body.index("}")]
+    rs_fields = re.findall(r"pub (\w+):", rs_body)
+    from moearc_amd.context import AttnBlockDesc
+    py_fields = [f[0] for f in AttnBlockDesc._fields_]
+    assert c_fields == rs_fields == py_fields

@@ -22,13 +22,19 @@ from oracle import oracle
 
 pytestmark = pytest.mark.gpu
 
-E, H, G, D, PT = 256, 8, 2, 64, 16
+TOY = dict(E=256, H=8, G=2, D=64, PT=16)
+# gpt-oss-20b's attention block: 2880-wide residual, 64 query heads over 8 KV heads (group 8, the
+# prefill_g8 kernel), head_dim 64, 256-token pages
+GPT_OSS = dict(E=2880, H=64, G=8, D=64, PT=256)
 
 
 class Block:
     def __init__(self, ctx, types, seed, biases=True, sinks=True, n_swa=0, n_ctx=256, chunk=64,
-                 scaling=None, freq_base=10000.0):
+                 scaling=None, freq_base=10000.0, dims=TOY, x_scale=0.1):
         self.types, self.n_swa, self.scaling, self.freq_base = types, n_swa, scaling or RopeScaling(), freq_base
+        self.E, self.H, self.G, self.D, self.PT = (dims[k] for k in ("E", "H", "G", "D", "PT"))
+        self.x_scale = x_scale
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
         shapes = [(H * D, E), (G * D, E), (G * D, E), (E, H * D)]
         self.w = [fx.synth_blocks(t, r * c // fx.QT_BLOCK[t][1], seed + i)[0] for i, (t, (r, c)) in
                   enumerate(zip(types, shapes))]
@@ -54,6 +60,7 @@ class Block:
         self.n = 0  # tokens so far
 
     def places(self, n):
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
         if self.ring:
             pos = np.arange(self.n, self.n + n)
             return self.table[pos // PT].astype(np.uint32), (pos % PT).astype(np.uint32), self.table
@@ -61,11 +68,13 @@ class Block:
         return pages, slots, np.array(self.pool.pages_of(7).pages, np.uint32)
 
     def rope(self, a, pos, heads):
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
         s = self.scaling
         return oracle.rope_yarn(a, pos, len(pos), heads, D, D, self.freq_base, s.freq_scale, s.ext_factor,
                                 s.attn_factor, s.corr_lo, s.corr_hi).astype(np.float32)
 
     def oracle_chunk(self, h, x, pages, slots, table):
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
         n, pos0 = x.shape[0], self.n
         pos = np.arange(pos0, pos0 + n, dtype=np.int32)
         proj = []
@@ -88,11 +97,13 @@ class Block:
         return (h + o).astype(np.float32)
 
     def desc(self, ctx, d_table):
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
         return AttnBlockDesc.make(self.types, self.d_w, self.d_b, self.d_s, self.d_kp, self.d_vp, d_table,
                                   E, H, G, D, PT, self.n_swa, float(np.float32(1.0 / np.sqrt(D))), D,
-                                  self.freq_base, self.scaling)
+                                  self.freq_base, self.scaling, ring_pages=self.n_pages if self.ring else 0)
 
     def gpu_chunk(self, ctx, h, x, pages, slots, table):
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
         n = x.shape[0]
         d_h, d_x = ctx.upload(h), ctx.upload(x)
         pos = np.arange(self.n, self.n + n, dtype=np.int32)
@@ -101,12 +112,13 @@ class Block:
         return ctx.download(d_h, np.float32, (n, E))
 
     def bound(self):
-        r, c = self.shapes[3]
+        r, c = self.shapes[3]  # noqa: E501
         wo = oracle.dequant(self.types[3], self.w[3], r * c // fx.QT_BLOCK[self.types[3]][1]).reshape(r, c)
         return 2e-3 * np.abs(wo.astype(np.float64)).sum(axis=1) + 1e-5
 
     def step(self, ctx, n, seed, label):
-        x = (fx.synth.normal(seed, n * E) * 0.1).astype(np.float32).reshape(n, E)
+        E, H, G, D, PT = self.E, self.H, self.G, self.D, self.PT
+        x = (fx.synth.normal(seed, n * E) * self.x_scale).astype(np.float32).reshape(n, E)
         h = fx.synth.normal(seed + 1, n * E).astype(np.float32).reshape(n, E)
         pages, slots, table = self.places(n)
         got = self.gpu_chunk(ctx, h, x, pages, slots, table)
@@ -129,16 +141,31 @@ def test_chunks_then_decode_full_attention(ctx):
 def test_windowed_ring_mixed_types_yarn(ctx):
     # a windowed block through its ring (sized for window + chunk), sinks, YaRN, four weight types
     blk = Block(ctx, (1, 8, 12, 14), 0xB20C, n_swa=24, chunk=40,
-                scaling=RopeScaling.yarn(D, 4096, 150000.0, 32.0), freq_base=150000.0)
+                scaling=RopeScaling.yarn(TOY["D"], 4096, 150000.0, 32.0), freq_base=150000.0)
     blk.step(ctx, 40, 11, "SWA-24 ring, chunk 1")
     blk.step(ctx, 33, 13, "SWA-24 ring, chunk 2")
     blk.step(ctx, 1, 15, "SWA-24 ring, decode step")
 
 
+@pytest.mark.parametrize("n_swa", [0, 128])
+def test_gpt_oss_shape_chunks_then_decode(ctx, n_swa):
+    # the block at gpt-oss-20b's shape: Q8_0 projections with biases, sinks, YaRN (factor 32 over a
+    # 4096-token original context, base 150000), group-8 prefill, a full layer through pool pages and
+    # a windowed (SWA-128) layer through its ring; two chunks then a decode step. Activations scaled
+    # so q and k come out O(1) at 2880 columns.
+    blk = Block(ctx, (8, 8, 8, 8), 0xB50C + n_swa, n_swa=n_swa, n_ctx=512, chunk=160,
+                scaling=RopeScaling.yarn(64, 4096, 150000.0, 32.0), freq_base=150000.0, dims=GPT_OSS,
+                x_scale=0.03)
+    label = f"gpt-oss {'SWA-128 ring' if n_swa else 'full'}"
+    blk.step(ctx, 160, 21, f"{label}, chunk 1")
+    blk.step(ctx, 97, 23, f"{label}, chunk 2")
+    blk.step(ctx, 1, 25, f"{label}, decode step")
+
+
 def test_chunk_equals_token_by_token(ctx):
     # the chunked call against the reference's shape of work, one token per call, both on the GPU
     a, b = Block(ctx, (8, 8, 8, 8), 0xB30C, sinks=False), Block(ctx, (8, 8, 8, 8), 0xB30C, sinks=False)
-    n = 21
+    n, E = 21, a.E
     x = (fx.synth.normal(0x77, n * E) * 0.1).astype(np.float32).reshape(n, E)
     h = fx.synth.normal(0x78, n * E).astype(np.float32).reshape(n, E)
     pa, sa, ta = a.places(n)
@@ -165,6 +192,11 @@ def test_refusals(ctx):
     assert lib.moearc_attn_block_chunk(ctx.raw, ctypes.byref(d), buf.ptr, buf.ptr, 1, 0, buf.ptr, buf.ptr,
                                        buf.ptr) == -2
     d.w_type[3] = 8
+    # a windowed block whose ring cannot hold the chunk's keys (n_tok + n_swa - 1 > ring tokens)
+    d.n_swa, d.ring_pages = 24, 2  # 32 ring tokens
+    assert lib.moearc_attn_block_chunk(ctx.raw, ctypes.byref(d), buf.ptr, buf.ptr, 10, 0, buf.ptr, buf.ptr,
+                                       buf.ptr) == -2
+    d.n_swa, d.ring_pages = 0, 0
     d.head_dim = 32
     assert lib.moearc_attn_block_chunk(ctx.raw, ctypes.byref(d), buf.ptr, buf.ptr, 1, 0, buf.ptr, buf.ptr,
                                        buf.ptr) == -2

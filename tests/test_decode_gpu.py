@@ -184,6 +184,40 @@ def test_kv_append_chunk_equals_token_appends(ctx):
     assert np.array_equal(ctx.download(a_v, np.uint16, pool), want_v)
 
 
+@pytest.mark.parametrize("fused", [False, True])
+def test_out_of_page_slot_is_refused_at_sync(fused):
+    # The slots live on the device, so the host cannot refuse a slot outside its page when the
+    # call is made; the kernel leaves that token unwritten and the next synchronisation fails. The
+    # other tokens land, and the next call starts clean.
+    from moearc_amd import Failed
+    from moearc_amd import RopeKind
+    G, D, pt, pages, n_tok = 2, 64, 16, 3, 5
+    row = G * D
+    rows = fx.synth.normal(9, n_tok * row).reshape(n_tok, row)
+    page_ids = np.array([0, 1, 2, 1, 0], np.uint32)
+    slots = np.array([3, pt, 7, 15, 0], np.uint32)  # token 1's slot lies outside the page
+    with Context() as cx:
+        pool = pages * pt * row
+        kp, vp = cx.upload(np.zeros(pool, np.uint16)), cx.upload(np.zeros(pool, np.uint16))
+        dk, dv = cx.upload(rows), cx.upload(rows)
+        dpg, dsl = cx.upload(page_ids), cx.upload(slots)
+        if fused:
+            cx.rope_kv_append_chunk(kp, vp, dk, dv, cx.upload(np.arange(n_tok, dtype=np.int32)), dpg, dsl,
+                                    n_tok, G, D, pt, D, 10000.0, kind=RopeKind.NEOX, kv=KvType.F16)
+        else:
+            cx.kv_append_chunk(kp, vp, dk, dv, dpg, dsl, n_tok, G, D, pt, KvType.F16)
+        with pytest.raises(Failed):
+            cx.sync()
+        got = cx.download(vp, np.uint16, pool).reshape(pages, pt, row)
+        for t in (0, 2, 3, 4):
+            assert np.array_equal(got[page_ids[t], slots[t]], fx.synth.f16_bits(rows[t]))
+        assert np.count_nonzero(got) == 4 * row  # nothing else written
+        # a clean call afterwards synchronises without error
+        good = np.array([0, 1, 2, 1, 0], np.uint32) * 0 + np.arange(n_tok, dtype=np.uint32)
+        cx.kv_append_chunk(kp, vp, dk, dv, dpg, cx.upload(good), n_tok, G, D, pt, KvType.F16)
+        cx.sync()
+
+
 # ---- gpt-oss shape on the split-K MFMA kernel ----------------------------------------------------
 
 @pytest.mark.parametrize("golden,kv_begin", [("ns_decode_full", 0), ("ns_decode_swa128", 172)])
@@ -242,12 +276,13 @@ def test_single_key_closed_form_with_sink(ctx):
 
 
 def test_forced_splits_and_variants(monkeypatch):
-    # every work-group shape, with many splits (merged by the second launch) and with few
+    # both work-group shapes, with many splits (merged by the second launch), several chunks per
+    # wave (the chunk loop), and one split (finished in place)
     c = fx.north_star_case(0xAB, 5000, pt=256, spike_frac=0.01)
     want = oracle.attn_decode(c.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, 0, c.n_kv, c.pt,
                               float(c.scale), kv_type=1, sinks=c.sinks)
-    for variant, split in (("1x4", 128), ("1x16", 512), ("2x8", 256), ("4x4", 128), ("4x4", 4096),
-                           ("8x2", 64), ("4x4", 8192)):
+    for variant, split in (("4x2x4", 256), ("4x2x4", 1024), ("4x2x4", 4096), ("4x2x4", 8192),
+                           ("1x4x1", 128), ("1x4x1", 640), ("1x4x1", 8192)):
         monkeypatch.setenv("MOEARC_DECODE_VARIANT", variant)
         monkeypatch.setenv("MOEARC_DECODE_SPLIT", str(split))
         with Context() as cx:
@@ -258,16 +293,16 @@ def test_forced_splits_and_variants(monkeypatch):
 
 
 def test_merge_over_many_rounds(monkeypatch):
-    # 313 splits: each merge lane takes more than one round of records
+    # 157 splits: each merge lane takes more than one round of records (128 per round)
     c = fx.north_star_case(0xAC, 20000, pt=64, spike_frac=0.01)
     want = oracle.attn_decode(c.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, 0, c.n_kv, c.pt,
                               float(c.scale), kv_type=1, sinks=c.sinks)
-    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "8x2")
-    monkeypatch.setenv("MOEARC_DECODE_SPLIT", "64")
+    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "1x4x1")
+    monkeypatch.setenv("MOEARC_DECODE_SPLIT", "128")
     with Context() as cx:
         b = _upload_case(cx, c)
         got = _decode(cx, c, b, 0)
-        _report("variant=8x2 split=64 n_kv=20000", got, want, TOL_NS)
+        _report("variant=1x4x1 split=128 n_kv=20000", got, want, TOL_NS)
 
 
 @pytest.mark.parametrize("scale", [-0.125, 0.0])
@@ -287,12 +322,13 @@ def test_batched_ragged_decode(ctx):
     _batched_ragged(ctx)
 
 
-def test_batched_ragged_decode_fused(monkeypatch):
-    # the same with the in-launch merge: one arrival counter per (sequence, KV head)
-    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "1x4f")
+@pytest.mark.parametrize("variant", ["4x2x4", "1x4x1"])
+def test_batched_ragged_decode_each_variant(monkeypatch, variant):
+    # the same batch with each work-group shape forced, twice per context (records reused)
+    monkeypatch.setenv("MOEARC_DECODE_VARIANT", variant)
     with Context() as cx:
         _batched_ragged(cx)
-        _batched_ragged(cx)  # counters reset by the previous launches
+        _batched_ragged(cx)
 
 
 def _batched_ragged(ctx):
@@ -406,13 +442,14 @@ def test_large_q_magnitudes(ctx):
         _report(f"q x {mult:g}", got, want, TOL_NS)
 
 
-@pytest.mark.parametrize("n_kv,kv_begin,pt,split", [(32768, 0, 256, 0), (5000, 123, 32, 0),
-                                                     (1500, 0, 16, 128), (9000, 8000, 64, 128)])
-def test_fused_merge_variant(monkeypatch, n_kv, kv_begin, pt, split):
-    """The fused variant merges the splits inside the launch (the last work-group of each KV head
-    to finish). Three calls per context, each on different data, so a stale record or a counter
-    left non-zero would show; the batched call covers several sequences' counters at once."""
-    monkeypatch.setenv("MOEARC_DECODE_VARIANT", "1x4f")
+@pytest.mark.parametrize("variant,n_kv,kv_begin,pt,split", [
+    ("4x2x4", 32768, 0, 256, 0), ("4x2x4", 5000, 123, 32, 0), ("1x4x1", 1500, 0, 16, 128),
+    ("1x4x1", 9000, 8000, 64, 128), ("4x2x4", 70000, 1000, 16, 0)])
+def test_repeated_calls_on_fresh_data(monkeypatch, variant, n_kv, kv_begin, pt, split):
+    """Three calls per context, each on different data, so a record left over from an earlier
+    call (the workspace is reused, never cleared) would show; pages smaller than a tile and spans
+    that start mid-page exercise the per-lane block-table walk."""
+    monkeypatch.setenv("MOEARC_DECODE_VARIANT", variant)
     if split:
         monkeypatch.setenv("MOEARC_DECODE_SPLIT", str(split))
     with Context() as cx:
@@ -422,5 +459,5 @@ def test_fused_merge_variant(monkeypatch, n_kv, kv_begin, pt, split):
             got = _decode(cx, c, b, kv_begin)
             want = oracle.attn_decode(c.q, c.k_raw, c.v_raw, c.bt, c.H, c.G, c.D, kv_begin, n_kv, pt,
                                       float(c.scale), kv_type=1, sinks=c.sinks)
-            _report(f"fused n_kv={n_kv} begin={kv_begin} pt={pt} split={split} rep={rep}", got, want,
-                    TOL_NS)
+            _report(f"{variant} n_kv={n_kv} begin={kv_begin} pt={pt} split={split} rep={rep}", got,
+                    want, TOL_NS)

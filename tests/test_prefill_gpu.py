@@ -2,8 +2,8 @@
 
 Golden fixtures pin a small gpt-oss-shaped chunk; the oracle covers every GQA group the kernel
 supports, windowed and full layers, ragged chunk ends and page sizes; at BASELINE config 4's full
-size (2048 new tokens after 2048 cached) rows are sampled for the oracle and every row is checked
-for finiteness. The bar is the north star's: max-abs error <= 2e-3 on the output.
+size (2048 new tokens after 2048 cached) six rows of every 32-token query tile -- its first and last
+among them -- are compared with the oracle and every row is checked for finiteness. The bar is the north star's: max-abs error <= 2e-3 on the output.
 """
 from __future__ import annotations
 
@@ -109,19 +109,31 @@ def test_precise_variant_against_oracle(monkeypatch):
             _report(f"precise prefill n_swa={n_swa}", got[g["rows"]], g["expected"], 1e-5)
 
 
+# Rows of config 4 compared with the oracle: residues modulo 32, the default kernel's query tile
+# (256 rows per work-group / group 8 = 32 tokens). Every tile's first and last row (0, 31), the rows
+# either side of the 16-token mid-point (15, 16), and rows 1 and 30; with pos0 = 2048 these are also
+# the rows whose causal diagonal (and, at n_swa = 128, window start) falls on the first, second,
+# second-to-last and last key of a 32-key chunk, where the kernel's per-chunk mask tests switch.
+C4_RESIDUES = (0, 1, 15, 16, 30, 31)
+
+
 @pytest.mark.parametrize("n_swa", [0, 128])
 def test_config4_full_size(ctx, n_swa):
     # 2048 new tokens after 2048 cached, 64q/8kv, d64, f16, sinks
     pc = fx.prefill_case(0xC4, n_q=2048, pos0=2048, pt=256)
+    want = np.full((pc.n_q, pc.H, pc.D), np.nan, np.float32)
+    for r in C4_RESIDUES:
+        part = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q,
+                                   pc.pos0, n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale),
+                                   sinks=pc.sinks, rows=(r, 2048, 32), n_threads=16)
+        want[r::32] = part[r::32]
+    rows = np.sort(np.concatenate([np.arange(r, 2048, 32) for r in C4_RESIDUES]))
+    assert rows.size == 64 * len(C4_RESIDUES) and np.isfinite(want[rows]).all()
     for out_type in (OUT_F32, OUT_F16):
         got = _run(ctx, pc, n_swa, out_type=out_type)
         assert np.isfinite(got).all()
-        want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q,
-                                   pc.pos0, n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale),
-                                   sinks=pc.sinks, rows=(3, 2048, 97), n_threads=8)
-        rows = np.arange(3, 2048, 97)
-        _report(f"config 4 n_swa={n_swa} out={'f16' if out_type else 'f32'} ({rows.size} rows)",
-                got[rows], want[rows])
+        _report(f"config 4 n_swa={n_swa} out={'f16' if out_type else 'f32'} ({rows.size} rows, "
+                f"first and last of every 32-token tile)", got[rows], want[rows])
 
 
 def test_refusals(ctx):
