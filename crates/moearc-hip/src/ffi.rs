@@ -168,6 +168,30 @@ unsafe extern "C" {
         scale: c_float,
         kv_type: c_uint,
     ) -> c_int;
+    /// Allocation-free form of `moearc_attn_decode_batched` (no counterpart in the reference): for
+    /// callers that cannot allocate (HIP graph capture, serving loops); partial records go to a
+    /// fixed 8 MiB array of the code object, a call too large for it is refused with -2.
+    #[allow(clippy::too_many_arguments)]
+    pub fn moearc_attn_decode_batched_noalloc(
+        c: *mut MoearcCtx,
+        out: *mut c_void,
+        out_type: c_uint,
+        q: *const c_float,
+        k_pages: *const c_void,
+        v_pages: *const c_void,
+        block_tables: *const c_uint,
+        bt_stride: c_ulong,
+        kv_begin: *const c_uint,
+        n_kv: *const c_uint,
+        sinks: *const c_float,
+        n_seqs: c_ulong,
+        n_heads: c_ulong,
+        n_kv_heads: c_ulong,
+        head_dim: c_ulong,
+        page_tokens: c_ulong,
+        scale: c_float,
+        kv_type: c_uint,
+    ) -> c_int;
     #[allow(clippy::too_many_arguments)]
     pub fn moearc_attn_prefill(
         c: *mut MoearcCtx,

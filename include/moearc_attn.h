@@ -123,6 +123,26 @@ int moearc_attn_decode_batched(moearc_ctx *c, void *out, unsigned int out_type, 
                                unsigned long n_kv_heads, unsigned long head_dim,
                                unsigned long page_tokens, float scale, unsigned int kv_type);
 
+/* Allocation-free decode. No counterpart in the reference: for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. The
+ * arguments, refusals and results of moearc_attn_decode_batched (the same kernels, bit-identical
+ * outputs), but the partial records of split spans go to a fixed 8 MiB array inside the code
+ * object (MOEARC_DECODE_SCRATCH_FLOATS floats, one array per context on its device, held until the
+ * context is destroyed) instead of the context's workspace, and no profiling event is recorded, so
+ * the call makes no hipMalloc, hipFree, event or host allocation. Limit: n_heads x work items x 66
+ * floats must fit the array (64 heads: up to 496 work items; the default split plan uses at most
+ * 128); a larger call is refused with -2, checked for every launch of the call before anything is
+ * enqueued. Calls of one context reuse the array in stream order; calls that overlap in time on one
+ * context (e.g. graphs captured from it replayed on other streams concurrently) race. Nothing in the
+ * array needs clearing between calls. */
+int moearc_attn_decode_batched_noalloc(moearc_ctx *c, void *out, unsigned int out_type, const float *q,
+                                       const void *k_pages, const void *v_pages,
+                                       const unsigned int *block_tables, unsigned long bt_stride,
+                                       const unsigned int *kv_begin, const unsigned int *n_kv,
+                                       const float *sinks, unsigned long n_seqs, unsigned long n_heads,
+                                       unsigned long n_kv_heads, unsigned long head_dim,
+                                       unsigned long page_tokens, float scale, unsigned int kv_type);
+
 /* Chunked prefill over a paged f16 KV cache. The chunk's n_q tokens sit at absolute positions
  * pos0 .. pos0+n_q-1 and their K/V are already in the cache (logical keys 0 .. pos0+n_q-1 through
  * block_table). Row i is, exactly, moearc_attn_decode at n_kv = pos0+i+1 with

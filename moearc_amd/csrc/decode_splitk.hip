@@ -137,6 +137,15 @@ __device__ __forceinline__ void process_tile(SoftmaxState &st, const TileRegs &r
     }
 }
 
+// The fixed record array of the allocation-free entry point (moearc_attn_decode_batched_noalloc):
+// partial records live here instead of in the context's workspace. Each loaded instance of the code
+// object -- one per context, on that context's device -- holds its own array for the life of the
+// module; the host takes its device address from the module (hipModuleGetGlobal, the module form of
+// hipGetSymbolAddress) once, at context creation, and passes that address to the kernels like any
+// workspace. External linkage so the module can name it; nothing else refers to it. Nothing in it
+// needs clearing: a call's merge reads only records its own split kernel wrote.
+__device__ __align__(256) float moearc_decode_scratch[MOEARC_DECODE_SCRATCH_FLOATS];
+
 // Agent-scope relaxed atomic stores for the partial records: global_store with sc1, written
 // through to the device-coherent level, so the kernel-end release has no dirty L2 lines of them
 // to write back.

@@ -19,6 +19,10 @@
 //   rec_ml[(h * n_items + item) * 2 + 0/1] running max (log2 domain) / denominator (f32)
 #define MOEARC_MERGE_THREADS 256
 
+// Floats of the code object's fixed record array (moearc_decode_scratch, 8 MiB), which the
+// allocation-free decode entry point uses in place of the context's workspace: n_heads * work items
+// * 66 floats must fit (64 heads: up to 496 work items; the planner's default is at most 128).
+#define MOEARC_DECODE_SCRATCH_FLOATS (1u << 21)
 
 // Kernel arguments of the split-K decode that are not preloaded scalars (the leading kernel
 // arguments carry the KV and block-table bases, q, sequence 0's span, split and item count, and

@@ -102,6 +102,11 @@ struct moearc_ctx {
     uint32_t *err_word = nullptr;
     bool err_armed = false;
     bool deferred_error = false;
+    // The code object's fixed record array (moearc_decode_scratch): its device address in this
+    // context's module instance, read once at creation, and its size in floats.
+    float *scratch = nullptr;
+    size_t scratch_floats = 0;
+    int quiet = 0;  // > 0 during an allocation-free call: no profiling events are taken
     std::vector<Pending> pending;
     std::vector<KernelTime> totals;
     std::vector<hipEvent_t> event_pool;
@@ -175,7 +180,7 @@ void record_bracket(moearc_ctx *c, hipEvent_t start, const char *what, unsigned 
 // the reference does not track (what == nullptr), is recorded only with MOEARC_PROFILE_KERNELS=1,
 // under "kernel <what>" -- consumers that sum every key then still count each call once.
 bool tracks(const moearc_ctx *c, const char *what) {
-    if (!c->profiling) return false;
+    if (!c->profiling || c->quiet) return false;
     return c->profile_kernels || (what && c->scope_depth == 0);
 }
 
@@ -547,6 +552,17 @@ moearc_ctx *moearc_ctx_create(void) {
     if (hipMalloc((void **) &c->err_word, 256) != hipSuccess ||
         hipMemcpy(c->err_word, &zero, 4, hipMemcpyHostToDevice) != hipSuccess)
         return release(c);
+    // The fixed record array's address in this module instance (per context, on its device). The
+    // symbol's name on the host is not a device address; only this pointer is ever passed on.
+    hipDeviceptr_t scratch = nullptr;
+    size_t scratch_bytes = 0;
+    if (hipModuleGetGlobal(&scratch, &scratch_bytes, c->module, "moearc_decode_scratch") != hipSuccess ||
+        !scratch || scratch_bytes < (size_t) MOEARC_DECODE_SCRATCH_FLOATS * sizeof(float)) {
+        std::fprintf(stderr, "moearc: code object %s lacks the decode record array\n", co.c_str());
+        return release(c);
+    }
+    c->scratch = (float *) scratch;
+    c->scratch_floats = scratch_bytes / sizeof(float);
     struct {
         hipFunction_t *slot;
         const char *name;
@@ -1121,6 +1137,41 @@ int moearc_attn_decode_batched(moearc_ctx *c, void *out, unsigned int out_type, 
     spans.n = n_seqs;
     return decode_launch(c, out, out_type, q, k_pages, v_pages, block_tables, bt_stride, spans,
                          sinks, n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type);
+}
+
+int moearc_attn_decode_batched_noalloc(moearc_ctx *c, void *out, unsigned int out_type, const float *q,
+                                       const void *k_pages, const void *v_pages,
+                                       const unsigned int *block_tables, unsigned long bt_stride,
+                                       const unsigned int *kv_begin, const unsigned int *n_kv,
+                                       const float *sinks, unsigned long n_seqs, unsigned long n_heads,
+                                       unsigned long n_kv_heads, unsigned long head_dim,
+                                       unsigned long page_tokens, float scale, unsigned int kv_type) {
+    // The checks and kernels of moearc_attn_decode_batched; the split records go to the code
+    // object's fixed array (no hipMalloc, hipFree, event or host allocation), which a call must fit.
+    if (!c || !out || !q || !k_pages || !v_pages || !block_tables || !kv_begin || !n_kv) return ERR;
+    if (kv_type != 0u && kv_type != 1u) return ERR_ARG;
+    if (out_type != MOEARC_OUT_F32 && out_type != MOEARC_OUT_F16) return ERR_ARG;
+    if (n_seqs == 0 || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || page_tokens == 0)
+        return ERR_ARG;
+    if (n_heads % n_kv_heads != 0) return ERR_ARG;
+    if (head_dim > 1024) return ERR_ARG;
+    for (unsigned long b = 0; b < n_seqs; ++b) {
+        if (n_kv[b] == 0 || kv_begin[b] >= n_kv[b]) return ERR_ARG;
+        if ((n_kv[b] + page_tokens - 1) / page_tokens > bt_stride) return ERR_ARG;
+    }
+    if (!c->scratch) return ERR;
+    SpanList spans;
+    spans.kv_begin = kv_begin;
+    spans.n_kv = n_kv;
+    spans.n = n_seqs;
+    RecordSpace rs;
+    rs.fixed = c->scratch;
+    rs.cap = c->scratch_floats;
+    ++c->quiet;
+    const int rc = decode_launch(c, out, out_type, q, k_pages, v_pages, block_tables, bt_stride, spans,
+                                 sinks, n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type, rs);
+    --c->quiet;
+    return rc;
 }
 
 int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const void *q,

@@ -53,6 +53,9 @@ SIGNATURES = {
     "moearc_attn_decode_batched": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _c_ulong,
                                                   _vp, _vp, _vp, _c_ulong, _c_ulong, _c_ulong,
                                                   _c_ulong, _c_ulong, ctypes.c_float, _u32]),
+    "moearc_attn_decode_batched_noalloc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _c_ulong,
+                                                          _vp, _vp, _vp, _c_ulong, _c_ulong, _c_ulong,
+                                                          _c_ulong, _c_ulong, ctypes.c_float, _u32]),
     "moearc_attn_prefill": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _c_ulong,
                                            _c_ulong, _c_ulong, _c_ulong, _c_ulong, _c_ulong,
                                            _c_ulong, ctypes.c_float, _u32]),
