@@ -127,6 +127,16 @@ def decode_inputs(seed=0xC2):
     return kp.ravel(), vp.ravel(), bt, q, sinks
 
 
+def summary_value(path, key):
+    """A `key value` line of a committed rocprofv3 summary under profiles/, or None."""
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(key + " "):
+            return float(line.split()[1])
+    return None
+
+
 def pmc_traffic(path):
     """HBM bytes per decode call (split + merge) from the committed rocprofv3 summary."""
     if not os.path.exists(path):
@@ -627,13 +637,25 @@ def bench_configs(ctx, hip, steps, warmup):
 
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
-    decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
+    decode_graph (the main line's timed region: C2 steps in one graph, replayed), decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
     C4 chunk), matvec (the projection cases of MV_CASES, in order), matmul (MM_CASES, each as
     a graph of `steps` launches, replayed twice), or copy (a 256 MiB device-to-device copy, the
     reference size for scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
     from moearc_amd import Context, KvType, OUT_F16
     with Context() as ctx:
-        if what == "decode":
+        if what == "decode_graph":
+            # the timed region of the main line: C2 steps captured in one graph, replayed REPS times
+            kp, vp, bt, q, sinks = decode_inputs()
+            dks = [ctx.upload(kp) for _ in range(COPIES)]
+            dvs = [ctx.upload(vp) for _ in range(COPIES)]
+            dq, dbt, ds = ctx.upload(q), ctx.upload(bt), ctx.upload(sinks)
+            dout = ctx.alloc(H * D * 2)
+            kb, nk = np.zeros(1, np.uint32), np.full(1, N_KV, np.uint32)
+            reps = graph_timed(Hip(), ctx, lambda i: ctx.attn_decode_batched(
+                dout, dq, dks[i % COPIES], dvs[i % COPIES], dbt, N_KV // PT, kb, nk, ds, H, G, D, PT, 0.125,
+                KvType.F16, out_type=OUT_F16), steps, warmup)
+            print(f"graph replay: {rep_stats(reps)['median']:.2f} us per step", flush=True)
+        elif what == "decode":
             kp, vp, bt, q, sinks = decode_inputs()
             dks = [ctx.upload(kp) for _ in range(COPIES)]
             dvs = [ctx.upload(vp) for _ in range(COPIES)]
@@ -687,7 +709,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "rope_append", "matvec", "matmul", "copy"],
+    ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "rope_append", "matvec", "matmul",
+                                       "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
@@ -722,6 +745,7 @@ def main():
     want = oracle.attn_decode(q, kp, vp, bt, H, G, D, 0, N_KV, PT, 0.125, kv_type=1, sinks=sinks)
     err = float(np.max(np.abs(r["out"].ravel() - want)))
     traffic = pmc_traffic(os.path.join(ROOT, "profiles", "decode_c2_pmc.md"))
+    split_tr = summary_value(os.path.join(ROOT, "profiles", "decode_c2_kernel_trace.md"), "split_us_trace_graph")
     line = {
         "metric": "decode attn µs/layer + HBM GB/s (% peak) at B=1, 32K ctx; prefill MFMA util",
         "value": round(gbs, 1),
@@ -756,6 +780,11 @@ def main():
             "scope": "whole decode call (split-K launch + merge launch), graph-replay step time",
             "bytes_per_call": C2_BYTES,
             "frac_split": round(C2_BYTES / split_us / 1e3 / HBM_PEAK_GBS, 4) if split_us else None,
+            "frac_split_note": "split launch alone, HIP events around it in an eager run (they also "
+                               "bracket the dispatch gap); frac_split_trace: the committed rocprofv3 trace "
+                               "of the graph replay (profiles/decode_c2_kernel_trace.md)",
+            "frac_split_trace": round(C2_BYTES / split_tr / 1e3 / HBM_PEAK_GBS, 4) if split_tr else None,
+            "split_us_trace": split_tr,
             "split_us_events": round(split_us, 2) if split_us else None,
             "merge_us_events": round(merge_us, 2) if merge_us else None,
             "call_us_events": round(ev["attn_decode r64 m64"], 2) if "attn_decode r64 m64" in ev else None,
