@@ -14,7 +14,14 @@ N + 1 for `s_nop N`):
      between the load and the `s_waitcnt` that retires it (loads counted in program order);
   4. an inline-asm statement that writes m0 (the LDS base of the DMA copies; a register the compiler
      owns, so no asm may list it as clobbered) first saves it to an SGPR and ends by restoring it
-     from that SGPR, which nothing in between writes -- in every kernel of the code object.
+     from that SGPR, which nothing in between writes -- in every kernel of the code object;
+  5. every register the key loop (prefill_loop.inc) writes is an output ("+{...}") or a clobber of
+     the asm statement in prefill_fast.hip: the compiler keeps its own values in any other register
+     across the statement, and in an input-only operand it may reuse the value afterwards;
+  6. the VALU wait states hipcc itself inserts for gfx950 (seen in its output for plain HIP code):
+     a VALU result is not read by v_readfirstlane / v_readlane within 1 wait state, a transcendental
+     result (v_exp_f32 and the like) not by another VALU instruction within 1, and an SGPR written by
+     v_readfirstlane / v_readlane not read by a VALU instruction within 2.
 
 Usage: python check_asm_hazards.py [kernel-name-prefix ...]   (default: moearc_attn_prefill_g)
 Exit status 1 when a hazard is found.
@@ -157,6 +164,57 @@ def mfma_hazards(ins, labels):
     return out
 
 
+TRANS = ("v_exp_", "v_log_", "v_rcp_", "v_rsq_", "v_sqrt_", "v_sin_", "v_cos_")
+
+
+def sregs(tok):
+    """SGPR numbers named by one operand (sN or s[a:b])."""
+    tok = tok.split()[0] if tok else ""
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"s(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def valu_wait_hazards(ins, labels):
+    """Check 6 over the instructions of one kernel or asm statement."""
+    out = []
+    for i, t in enumerate(ins):
+        op, args = split_ops(t)
+        if not op.startswith("v_") or op.startswith("v_mfma"):
+            continue
+        if op.startswith(("v_readfirstlane", "v_readlane")):
+            sd = sregs(args[0]) if args else set()
+
+            def chk_s(u, sd=sd):
+                uop, ua = split_ops(u)
+                if uop.startswith("v_") and any(sd & sregs(a) for a in ua[1:]):
+                    return "VALU reads an SGPR that v_readfirstlane/v_readlane wrote"
+                return None
+            out += walk(ins, labels, i, 2, chk_s)
+            continue
+        w, _ = writes_reads(t)
+        if not w:
+            continue
+
+        def chk_r(u, w=w):
+            uop, ua = split_ops(u)
+            if uop.startswith(("v_readfirstlane", "v_readlane")) and len(ua) > 1 and w & regs(ua[1]):
+                return "v_readfirstlane/v_readlane reads a VALU result"
+            return None
+        out += walk(ins, labels, i, 1, chk_r)
+        if op.startswith(TRANS):
+            def chk_t(u, w=w):
+                uop, ua = split_ops(u)
+                if uop.startswith("v_") and not uop.startswith("v_mfma") and \
+                        w & set().union(*[regs(a) for a in ua[1:]] or [set()]):
+                    return "VALU reads a transcendental result"
+                return None
+            out += walk(ins, labels, i, 1, chk_t)
+    return out
+
+
 def load_hazards(ins):
     """Straight-line check of asm-issued load destinations against their retiring wait."""
     out = []
@@ -231,7 +289,98 @@ def _m0_region(ins):
     return []
 
 
+_NO_SDST = ("s_cmp", "s_bitcmp", "s_cbranch", "s_branch", "s_waitcnt", "s_barrier", "s_nop",
+            "s_setpc", "s_sleep", "s_endpgm", "s_dcache", "s_setprio", "s_sethalt", "s_trap")
+
+
+def sgpr_regs(tok):
+    tok = tok.split()[0] if tok else ""
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return {f"s{i}" for i in range(int(m.group(1)), int(m.group(2)) + 1)}
+    if re.fullmatch(r"s\d+|vcc|exec|m0|scc", tok):
+        return {tok}
+    return set()
+
+
+def scalar_writes(t):
+    """Scalar registers (sN, vcc, exec, m0, scc) an instruction writes."""
+    op, args = split_ops(t)
+    out = set()
+    if op.startswith("s_cmp") or op.startswith("s_bitcmp"):
+        return {"scc"}
+    if op.startswith("s_") and not op.startswith(_NO_SDST) and args:
+        out |= sgpr_regs(args[0])
+        if not op.startswith(("s_mov", "s_call", "s_getpc", "s_load", "s_memtime", "s_memrealtime",
+                              "s_readfirstlane")):
+            out.add("scc")
+    elif op.startswith("v_cmp") and args and "_e64" in op:
+        out |= sgpr_regs(args[0])
+    elif op.startswith("v_cmp"):
+        out.add("vcc")
+    elif op.startswith(("v_readfirstlane", "v_readlane")) and args:
+        out |= sgpr_regs(args[0])
+    elif op.startswith("v_") and len(args) > 1 and op.startswith(("v_add_co", "v_addc_co", "v_sub_co",
+                                                                    "v_subb_co", "v_mad_u64", "v_mad_i64")):
+        out |= sgpr_regs(args[1])
+    return out
+
+
+def asm_statement_registers(hip_text):
+    """Outputs, input-only operands and clobbers (register names) of the key-loop asm statement."""
+    start = hip_text.index('#include "prefill_loop.inc"')
+    end = hip_text.index("PFF_CLOBBERS);", start)
+    body = hip_text[start:end]
+    outs_txt, ins_txt = body.split("\n        : ", 2)[1:3] if body.count("\n        : ") >= 2 else (body, "")
+
+    def names(txt, plus):
+        found = set()
+        for m in re.finditer(r'"(\+?)\{(v\[(\d+):(\d+)\]|v(\d+))\}"', txt):
+            if bool(m.group(1)) != plus:
+                continue
+            if m.group(3):
+                found |= {f"v{i}" for i in range(int(m.group(3)), int(m.group(4)) + 1)}
+            else:
+                found.add(f"v{m.group(5)}")
+        return found
+    outputs = names(outs_txt, True)
+    inputs = names(ins_txt, False)
+    mac = hip_text.index("#define PFF_CLOBBERS")
+    mac_end = hip_text.index("\n\n", mac)
+    clobbers = set(re.findall(r'"(v\d+|s\d+|vcc|scc|exec)"', hip_text[mac:mac_end]))
+    return outputs, inputs, clobbers
+
+
+def loop_instructions(inc_text):
+    ins = []
+    for l in inc_text.split("\n"):
+        m = re.fullmatch(r'"(.*)\\n\\t"', l.strip())
+        if m and not m.group(1).endswith(":"):
+            ins.append(m.group(1))
+    return ins
+
+
+def undeclared_writes(inc_text, hip_text):
+    """Check 5: instructions of the key loop that write a register the statement does not declare
+    as written (m0 is covered by check 4)."""
+    outputs, _, clobbers = asm_statement_registers(hip_text)
+    declared = outputs | clobbers | {"m0"}
+    out = []
+    for t in loop_instructions(inc_text):
+        w, _ = writes_reads(t)
+        written = {f"v{i}" for i in w} | scalar_writes(t)
+        bad = sorted(written - declared)
+        if bad:
+            out.append(f"[{t}]: writes {', '.join(bad)}, not an output or clobber of the statement")
+    return out
+
+
 def main(prefixes):
+    undeclared = undeclared_writes(open(os.path.join(HERE, "prefill_loop.inc")).read(),
+                                   open(os.path.join(HERE, "prefill_fast.hip")).read())
+    print(f"key loop writes outside its outputs and clobbers: {len(undeclared)}")
+    for p in undeclared[:10]:
+        print("   ", p)
     lines = compile_asm()
     m0 = m0_hazards(lines)
     print(f"inline asm writing m0: {len(m0)} hazards")
@@ -243,7 +392,7 @@ def main(prefixes):
     bad = 0
     for name in names:
         ins, labels = kernel_body(lines, name)
-        probs = mfma_hazards(ins, labels) + load_hazards(ins)
+        probs = mfma_hazards(ins, labels) + load_hazards(ins) + valu_wait_hazards(ins, labels)
         print(f"{name}: {len(ins)} instructions, {len(probs)} hazards")
         for p in probs[:10]:
             print("   ", p)
@@ -251,7 +400,7 @@ def main(prefixes):
     if not names:
         print("no kernel matches", prefixes)
         return 1
-    return 1 if bad or m0 else 0
+    return 1 if bad or m0 or undeclared else 0
 
 
 if __name__ == "__main__":

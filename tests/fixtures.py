@@ -97,10 +97,11 @@ def reference_case(name: str) -> Case:
 
 def north_star_case(seed: int, n_kv: int, kv_begin: int = 0, H: int = 64, G: int = 8, D: int = 64,
                     pt: int = 256, sinks: bool = True, scatter: bool = True,
-                    spike_frac: float = 0.0, extra_pages: int = 0) -> Case:
+                    spike_frac: float = 0.0, extra_pages: int = 0, boost=None) -> Case:
     """gpt-oss-shaped decode input: q, K, V ~ N(0,1) (K/V stored f16), per-head f32 sinks ~ N(0,1),
     KV in pt-token pages through a seeded random page permutation. With spike_frac > 0 that
-    fraction of K rows is scaled by 8 (stresses the running max)."""
+    fraction of K rows is scaled by 8 (stresses the running max); boost, a list of (start, stop,
+    factor), scales K rows start..stop-1 by factor, in order (jumps in the scores where chosen)."""
     row = G * D
     n_pages = -(-n_kv // pt) + extra_pages
     kvals = synth.normal(seed, n_kv * row).reshape(n_kv, row)
@@ -108,6 +109,8 @@ def north_star_case(seed: int, n_kv: int, kv_begin: int = 0, H: int = 64, G: int
     if spike_frac > 0:
         pick = synth.splitmix64(seed + 2, n_kv) % np.uint64(10000) < np.uint64(int(spike_frac * 10000))
         kvals[pick] *= np.float32(8.0)
+    for start, stop, factor in boost or ():
+        kvals[start:stop] *= np.float32(factor)
     q = synth.normal(seed + 3, H * D)
     s = synth.normal(seed + 4, H) if sinks else None
     bt = synth.random_block_table(seed + 5, n_pages) if scatter else np.arange(n_pages, dtype=np.uint32)
@@ -160,8 +163,8 @@ def sdpa_reference(case: Case, kv_begin: int | None = None, sinks=None) -> np.nd
     return out.reshape(-1).numpy()
 
 
-def prefill_case(seed, n_q, pos0, pt=32, H=64, G=8, D=64):
-    case = north_star_case(seed, pos0 + n_q, pt=pt, H=H, G=G, D=D)
+def prefill_case(seed, n_q, pos0, pt=32, H=64, G=8, D=64, spike_frac=0.0, boost=None):
+    case = north_star_case(seed, pos0 + n_q, pt=pt, H=H, G=G, D=D, spike_frac=spike_frac, boost=boost)
     case.qp = synth.normal(seed + 7, n_q * H * D).astype(np.float16).reshape(n_q, H, D)
     case.n_q, case.pos0, case.seed = n_q, pos0, seed
     return case

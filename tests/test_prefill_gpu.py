@@ -63,6 +63,36 @@ def test_shapes_against_oracle(ctx, group, n_q, pos0, pt, n_swa):
     _report("  without sinks", nosink, want_ns)
 
 
+# K rows scaled by small factors early and larger ones later: the scores jump by more than 8 in
+# base-2 units (the rescale threshold) where a row first sees the scaled-up keys, with |scores| kept
+# within the default kernels' accuracy (they round the scaled Q to f16: an emulation of their
+# arithmetic puts these cases at 0.9e-3 to 1.5e-3 max-abs error; keys scaled by 6 reach 5e-3).
+JUMPS = {
+    "late": [(0, 600, 0.02), (600, 4096, 2.0)],
+    "early": [(0, 32, 0.02), (32, 128, 1.8), (128, 4096, 0.3)],
+    "bands": [(0, 4096, 0.02), (300, 320, 100.0), (470, 480, 100.0), (700, 716, 100.0)],
+}
+
+
+@pytest.mark.parametrize("group,n_q,pos0,n_swa,jumps", [
+    (8, 256, 512, 0, "late"), (8, 256, 512, 0, "early"), (8, 256, 512, 0, "bands"),
+    (8, 256, 512, 128, "bands"), (4, 256, 512, 0, "late"), (2, 200, 300, 100, "bands"),
+    (1, 300, 200, 64, "bands"),
+])
+def test_score_jumps_against_oracle(ctx, group, n_q, pos0, n_swa, jumps):
+    """Scores that rise far above everything a row saw first: the default kernels' lazy rescale
+    (a chunk whose exponents reach the threshold moves the row's reference before its weights are
+    formed) runs early in a row ("early"), late in it ("late"), and at several places ("bands")."""
+    G = 8 if group > 1 else 4
+    pc = fx.prefill_case(0x5C0 + n_q + group, n_q=n_q, pos0=pos0, pt=32, H=G * group, G=G,
+                         boost=JUMPS[jumps])
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, n_q, pos0, n_swa,
+                               pc.H, pc.G, pc.D, pc.pt, float(pc.scale), sinks=pc.sinks, n_threads=8)
+    got = _run(ctx, pc, n_swa)
+    assert np.isfinite(got).all()
+    _report(f"prefill jumps group={group} n_q={n_q} pos0={pos0} n_swa={n_swa} {jumps}", got, want)
+
+
 @pytest.mark.parametrize("precise", [False, True])
 def test_long_context_small_pages(monkeypatch, precise):
     # 40,024 keys in 16-token pages: 2,502 block-table entries per row's span (the kernels read
