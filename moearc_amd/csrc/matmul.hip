@@ -20,7 +20,7 @@ typedef _Float16 mm_half8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float mm_f16(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 
-template <uint32_t TY, int RT>
+template <uint32_t TY, int RT, int NST>
 __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     // The work-group's activation tile of one k-block (64 tokens x 32 k, hi and lo) is staged in
     // LDS once and read by all four waves: fragment (quarter q, token t) at 16-byte slot q*64 + t,
@@ -245,27 +245,37 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
             }
         }
     };
-    // Ping-pong: block b + 1's operands are requested (clamped at the end, so every iteration
-    // issues the same loads) before block b's products; they reach LDS after them, then the
-    // work-group meets once.
-    Ops p, q;
-    load(0, p);
-    stage(p, 0);
+    // NST operand sets in flight: k-block k lives in set k % NST, and block b + NST - 1 is
+    // requested (clamped at the end, so every step issues the same loads) before block b's
+    // products. Block b + 1's activation share reaches LDS after block b's products, then the
+    // work-group meets once (two LDS buffers: a buffer is refilled only after every wave has
+    // passed the barrier that follows the products that read it).
+    Ops ops[NST];
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) load(min((uint32_t) s, nb - 1u), ops[s]);
+    stage(ops[0], 0);
     __syncthreads();
     uint32_t b = 0;
-    for (; b + 1u < nb; b += 2u) {
-        load(b + 1u, q);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(p, 0, b);
-        stage(q, 1);
-        __syncthreads();
-        load(min(b + 2u, nb - 1u), p);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(q, 1, b + 1u);
-        stage(p, 0);
-        __syncthreads();
+    for (; b + NST <= nb; b += NST) {
+#pragma unroll
+        for (int s = 0; s < NST; ++s) {
+            load(min(b + (uint32_t) (s + NST - 1), nb - 1u), ops[(s + NST - 1) % NST]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ops[s], (b + s) & 1u, b + s);
+            stage(ops[(s + 1) % NST], (b + s + 1u) & 1u);
+            __syncthreads();
+        }
     }
-    if (b < nb) compute(p, 0, b);
+#pragma unroll
+    for (int s = 0; s < NST; ++s) {
+        if (b + s < nb) {
+            compute(ops[s], (b + s) & 1u, b + s);
+            if (b + s + 1u < nb) {
+                stage(ops[(s + 1) % NST], (b + s + 1u) & 1u);
+                __syncthreads();
+            }
+        }
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -286,19 +296,23 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
 
 }  // namespace
 
+#ifndef MM_STAGES
+#define MM_STAGES 2  // k-blocks of operands in flight per wave
+#endif
+
 // _r1: 16 rows per wave (more work-groups, for short chunks); _r2: 32 rows per wave.
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r1_k(MatmulArgs a) { matmul_body<12, 1>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r2_k(MatmulArgs a) { matmul_body<12, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r1_k(MatmulArgs a) { matmul_body<13, 1>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r2_k(MatmulArgs a) { matmul_body<13, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q6_k_r1_k(MatmulArgs a) { matmul_body<14, 1>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q6_k_r2_k(MatmulArgs a) { matmul_body<14, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r1_k(MatmulArgs a) { matmul_body<39, 1>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r2_k(MatmulArgs a) { matmul_body<39, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r1_k(MatmulArgs a) { matmul_body<8, 1>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r2_k(MatmulArgs a) { matmul_body<8, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r1_k(MatmulArgs a) { matmul_body<1, 1>(a); }
-extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r2_k(MatmulArgs a) { matmul_body<1, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r1_k(MatmulArgs a) { matmul_body<12, 1, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q4_k_r2_k(MatmulArgs a) { matmul_body<12, 2, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r1_k(MatmulArgs a) { matmul_body<13, 1, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q5_k_r2_k(MatmulArgs a) { matmul_body<13, 2, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q6_k_r1_k(MatmulArgs a) { matmul_body<14, 1, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q6_k_r2_k(MatmulArgs a) { matmul_body<14, 2, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r1_k(MatmulArgs a) { matmul_body<39, 1, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_mxfp4_r2_k(MatmulArgs a) { matmul_body<39, 2, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r1_k(MatmulArgs a) { matmul_body<8, 1, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_q8_0_r2_k(MatmulArgs a) { matmul_body<8, 2, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r1_k(MatmulArgs a) { matmul_body<1, 1, MM_STAGES>(a); }
+extern "C" __global__ void __launch_bounds__(256) moearc_matmul_f16_r2_k(MatmulArgs a) { matmul_body<1, 2, MM_STAGES>(a); }
 
 // x -> (hi, lo) f16 with hi = f16(x), lo = f16(x - hi), both round-to-nearest-even.
 extern "C" __global__ void moearc_split_f16_k(const float *x, uint16_t *hi, uint16_t *lo, uint64_t n) {

@@ -8,3 +8,4 @@
 #include "rope.hip"
 #include "matvec.hip"
 #include "matmul.hip"
+#include "matmul2.hip"

@@ -87,6 +87,7 @@ struct moearc_ctx {
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr;
     hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
+    hipFunction_t f_mm2[2] = {};  // Q8_0, F16: 128 x 128 tiles on the 32x32x16 MFMA
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
@@ -590,6 +591,8 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm[4][1], "moearc_matmul_mxfp4_r2_k"},
         {&c->f_mm[5][0], "moearc_matmul_q6_k_r1_k"},
         {&c->f_mm[5][1], "moearc_matmul_q6_k_r2_k"},
+        {&c->f_mm2[0], "moearc_matmul2_q8_0_k"},
+        {&c->f_mm2[1], "moearc_matmul2_f16_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
     };
@@ -1256,8 +1259,13 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     a.cols = (uint32_t) n_cols;
     a.n_tok = (uint32_t) n_tok;
     a.y_stride = (uint32_t) y_stride;
-    // 32 rows per wave halves the activation loads per MFMA, but only pays while the launch still
-    // has about two work-groups per CU; shorter chunks take 16 rows per wave.
+    // Q8_0 and F16 over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
+    // (matmul2.hip). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
+    // pays while the launch still has about two work-groups per CU; shorter chunks take 16.
+    if ((ty == 8u || ty == 1u) && n_tok >= 64) {
+        return launch2d(c, c->f_mm2[ty == 8u ? 0 : 1], (unsigned) ((n_rows + 127) / 128),
+                        (unsigned) ((n_tok + 127) / 128), 256, a, what, n_rows, n_tok);
+    }
     const unsigned long tok_groups = (n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS;
     const int r2 = ((n_rows + 127) / 128) * tok_groups >= 512 ? 1 : 0;
     const unsigned long rows_per_wg = r2 ? 128 : 64;
