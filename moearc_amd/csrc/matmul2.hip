@@ -27,6 +27,9 @@ constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group
 constexpr uint32_t MM2_HALF = MM2_TOK * 64u;  // bytes of one half (hi or lo) of an activation tile
 constexpr uint32_t MM2_BUF = 2u * MM2_HALF;   // one k-block's activation tile
 constexpr uint32_t MM2_NBUF = 3u;
+// fewest memory instructions one block's weight loads compile to (two row tiles x two k slices of
+// 8 int8 or 8 halves, which no load can merge: Q8_0 adds the scales)
+constexpr uint32_t MM2_WLOADS = 4u;
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
@@ -182,24 +185,26 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     };
 
     // k-block b's activations in buffer b % 3, its weights in set b % 3. Step b: wait for block b's
-    // DMA (the last four memory operations issued are block b + 1's DMA; its weight loads go out
-    // before it), meet the other waves (every wave has finished block b - 1, whose buffer is refilled
-    // next), request block b + 2, compute block b.
+    // DMA, meet the other waves (every wave has finished block b - 1, whose buffer is refilled
+    // next), request block b + 2 (its DMA first, then its weights), compute block b. Issued after
+    // block b's DMA are its weights and block b + 1's DMA and weights: at least 2 MM2_WLOADS + 4
+    // memory operations (the weight loads of one block are at least MM2_WLOADS instructions), so
+    // waiting until that many remain leaves both blocks' requests in flight.
     Mm2W<TY> ws[3];
-    wload(0, ws[0]);
     dma(0, 0);
-    wload(min(1u, nb - 1u), ws[1]);
+    wload(0, ws[0]);
     dma(min(1u, nb - 1u), 1);
+    wload(min(1u, nb - 1u), ws[1]);
     auto step = [&](uint32_t b, int s) {
-        // block b's DMA has landed (only block b + 1's four DMA operations may be in flight) and
-        // every LDS read of block b - 1 has returned, in this wave; then in every wave
+        // block b's DMA has landed and every LDS read of block b - 1 has returned, in this wave;
+        // then in every wave
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(4));
+        __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(2u * MM2_WLOADS + 4u));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t bn = min(b + 2u, nb - 1u);
-        wload(bn, ws[(s + 2) % 3]);
         dma(bn, (uint32_t) (s + 2) % 3u);
+        wload(bn, ws[(s + 2) % 3]);
         __builtin_amdgcn_sched_barrier(0);
         compute((uint32_t) s, ws[s]);
     };
