@@ -14,6 +14,9 @@ there is no model).
   beside it from the split launch alone (HIP events on the library stream, eager, with
   MOEARC_PROFILE_KERNELS=1). traffic = HBM bytes per call from the committed rocprofv3
   FETCH_SIZE/WRITE_SIZE summary (profiles/decode_c2_pmc.md), when present.
+* read_floor: a plain streaming read of the same 64 MiB (moearc_read_floor, every load of a lane
+  in flight, over the same rotating copies and graph replay): what reading the call's bytes alone
+  costs on this device; decode_frac_of_floor = its time over the decode call's.
 * configs: BASELINE configs 1, 3 (SWA-128 and full) and 5, timed the same way.
 * prefill: BASELINE config 4 (2048 new + 2048 cached tokens), full causal and SWA-128, MFMA
   utilisation = algorithmic flops / time / 2.5 PFLOP/s (dense f16); also as top-level keys.
@@ -205,6 +208,7 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
         result["graph_equals_eager"] = bool(np.array_equal(graph_out, eager_out))
         result["out"] = graph_out
         del dks, dvs
+        result["read_floor"] = bench_read_floor(ctx, hip, steps, warmup)
         result["configs"] = bench_configs(ctx, hip, steps, warmup)
         result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
         result["block_chunk"] = bench_block(ctx, hip)
@@ -238,6 +242,41 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
     if not skip_cpu:
         result["cpu"] = cpu_baseline(kp, vp, bt, q, sinks)
     return result
+
+
+def read_floor_inputs(ctx, copies=COPIES):
+    """COPIES buffers of C2's KV bytes (K then V of copy i), for the calibration read."""
+    from moearc_amd import DeviceView
+    kp, vp, _, _, _ = decode_inputs()
+    nbytes = kp.nbytes + vp.nbytes
+    bufs = []
+    for _ in range(copies):
+        b = ctx.alloc(nbytes)
+        ctx.upload_slice(DeviceView(b, 0, kp.nbytes), kp)
+        ctx.upload_slice(DeviceView(b, kp.nbytes, vp.nbytes), vp)
+        bufs.append(b)
+    out = ctx.alloc((nbytes + 65535) // 65536 * 4)
+    return bufs, out, nbytes
+
+
+def bench_read_floor(ctx, hip, steps, warmup):
+    """The plain read of C2's 64 MiB of KV (moearc_read_floor: every load of a lane in flight, 64 KiB
+    per work-group) over the same rotating copies and graph replay as the decode: what a streaming
+    read of those bytes costs on this device, the floor under the decode call's time."""
+    bufs, out, nbytes = read_floor_inputs(ctx)
+    ctx.read_floor(out, bufs[0], nbytes)
+    ctx.sync()
+    got = ctx.download(out, np.uint32, (nbytes + 65535) // 65536)
+    kp, vp = decode_inputs()[:2]
+    host = np.concatenate([kp.view(np.uint8).ravel(), vp.view(np.uint8).ravel()]).view(np.uint32)
+    want = np.bitwise_xor.reduce(host.reshape(-1, 16384), axis=1)
+    reps = graph_timed(hip, ctx, lambda i: ctx.read_floor(out, bufs[i % COPIES], nbytes), steps, warmup)
+    st = rep_stats(reps)
+    del bufs
+    return {"bytes": nbytes, "us": st["median"], "us_reps": st,
+            "gbs": round(nbytes / st["median"] / 1e3, 1),
+            "frac_of_peak": round(nbytes / st["median"] / 1e3 / HBM_PEAK_GBS, 4),
+            "checksums_match": bool(np.array_equal(got, want))}
 
 
 def launch_overhead():
@@ -639,8 +678,9 @@ def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
     decode_graph (the main line's timed region: C2 steps in one graph, replayed), decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
     C4 chunk), matvec (the projection cases of MV_CASES, in order), matmul (MM_CASES, each as
-    a graph of `steps` launches, replayed twice), or copy (a 256 MiB device-to-device copy, the
-    reference size for scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
+    a graph of `steps` launches, replayed twice), read_floor (the calibration read of C2's 64 MiB of
+    KV over the rotating copies), or copy (a 256 MiB device-to-device copy, the reference size for
+    scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
     from moearc_amd import Context, KvType, OUT_F16
     with Context() as ctx:
         if what == "decode_graph":
@@ -689,6 +729,10 @@ def only(what, steps, warmup):
         elif what == "matmul":
             hip = Hip()
             bench_matmul(ctx, hip, steps=steps)
+        elif what == "read_floor":
+            bufs, out, nbytes = read_floor_inputs(ctx)
+            for i in range(warmup + steps):
+                ctx.read_floor(out, bufs[i % COPIES], nbytes)
         elif what == "copy":
             hip = Hip()
             n = 256 << 20
@@ -710,7 +754,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "rope_append", "matvec", "matmul",
-                                       "copy"],
+                                       "read_floor", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
@@ -789,6 +833,10 @@ def main():
             "merge_us_events": round(merge_us, 2) if merge_us else None,
             "call_us_events": round(ev["attn_decode r64 m64"], 2) if "attn_decode r64 m64" in ev else None,
         },
+        "read_floor": dict(r["read_floor"], decode_frac_of_floor=round(r["read_floor"]["us"] / step_us, 4),
+                           note="moearc_read_floor over the same 64 MiB copies and graph replay: a plain "
+                                "streaming read of the call's KV bytes; decode_frac_of_floor = its time "
+                                "over the decode call's"),
         "device": r.get("device"),
         "commit": git_head(),
         "source_sha16": source_sha16(),

@@ -223,6 +223,14 @@ int moearc_matvec_f32(moearc_ctx *c, float *out, const float *w, const float *x,
  * Refusals: null pointer -> -1. n == 0 -> 0. */
 int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsigned long n);
 
+/* Calibration read. No counterpart in the reference: for measurements that set the attention
+ * kernels' HBM traffic beside what a plain streaming read reaches on the device. Reads `bytes`
+ * bytes at src (16-byte aligned, a multiple of 16 bytes) with every load of a lane in flight at
+ * once, 64 KiB per work-group, and writes out[g] = the xor of the 32-bit words of the g-th 64 KiB
+ * (ceil(bytes / 65536) words). Null pointer -> -1; bytes 0, not a multiple of 16 or a misaligned
+ * src -> -2. */
+int moearc_read_floor(moearc_ctx *c, unsigned int *out, const void *src, unsigned long bytes);
+
 /* Extension (no counterpart in the reference, which runs three moearc_matvec_q and up to three
  * moearc_add calls for attn.qkv, moe.rs:1942-1959): projection i (0 q, 1 k, 2 v) writes
  * out[i][r] = sum_c W_i[r][c] x[c] + bias[i][r] for r < rows[i] (bias[i] may be null), one launch

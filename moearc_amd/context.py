@@ -403,6 +403,12 @@ class Context:
                     "matvec f32")
 
 
+    def read_floor(self, out: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+        """Calibration read of nbytes at src; out[g] = xor of the 32-bit words of its g-th 64 KiB."""
+        src.require("source", nbytes)
+        out.require("checksums", (nbytes + 65535) // 65536 * 4)
+        self.finish(self._lib.moearc_read_floor(self.raw, out.ptr, src.ptr, nbytes), "read_floor")
+
     def add(self, out: DeviceBuffer, a: DeviceBuffer, b: DeviceBuffer, n: int) -> None:
         """out = a + b, element-wise (kernels.cpp:1676-1683)."""
         for buf, what in ((out, "output"), (a, "left operand"), (b, "right operand")):

@@ -70,3 +70,29 @@ extern "C" __global__ void moearc_kv_append_chunk_k(void *k_pages, void *v_pages
         ((float *) v_pages)[dst] = v[g];
     }
 }
+
+// Calibration read (moearc_read_floor): the HBM read rate a streaming kernel reaches on this device,
+// for comparison with the attention kernels' traffic. Work-group g reads the 64 KiB at
+// src + 64 KiB * g (16 KiB per wave: every load of a thread issued before any is used, 16 bytes per
+// lane, consecutive lanes on consecutive 16-byte pieces) and writes the xor of its 32-bit words to
+// out[g], so the loads cannot be dropped and the result can be checked.
+#define MOEARC_READ_FLOOR_LOADS 16u
+extern "C" __global__ void __launch_bounds__(256) moearc_read_floor_k(unsigned int *out, const u32x4_t *src,
+                                                                      uint64_t n16) {
+    __shared__ uint32_t part[4];
+    const uint64_t base = (uint64_t) blockIdx.x * (256u * MOEARC_READ_FLOOR_LOADS) + threadIdx.x;
+    u32x4_t v[MOEARC_READ_FLOOR_LOADS];
+#pragma unroll
+    for (uint32_t i = 0; i < MOEARC_READ_FLOOR_LOADS; ++i) {
+        const uint64_t p = base + 256u * i;
+        v[i] = p < n16 ? src[p] : (u32x4_t){0u, 0u, 0u, 0u};
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < MOEARC_READ_FLOOR_LOADS; ++i) x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+#pragma unroll
+    for (uint32_t m = 32; m >= 1; m >>= 1) x ^= (uint32_t) __shfl_xor((int) x, (int) m);
+    if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
