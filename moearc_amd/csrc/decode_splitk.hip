@@ -417,6 +417,9 @@ __device__ __forceinline__ void merge_body(const float *rec_o, const float *rec_
     }
     const uint32_t nsplit = ib1 - ib0;
     if (nsplit <= 1u) return;  // finished by the split kernel itself
+    // the sink, requested with the records and first used at the end (without sinks the load reads
+    // a record word, ignored)
+    const float sink_raw = *(sinks ? sinks + h : rec_ml);
     const uint32_t ch = 16u * part + 4u * c4;
     const uint64_t base = (uint64_t) h * n_items + ib0;
     float m_t = -INFINITY, l_t = 0.f;
@@ -430,6 +433,7 @@ __device__ __forceinline__ void merge_body(const float *rec_o, const float *rec_
             v[k] = *(const float4_t *) (rec_o + s * 64u + ch);
             ml[k] = *(const float2_t *) (rec_ml + 2u * s);
         }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the round leaves before any is used
         float mr = m_t;
 #pragma unroll
         for (int k = 0; k < MERGE_BATCH; ++k) mr = fmaxf(mr, ml[k][0]);  // duplicates are harmless
@@ -465,7 +469,7 @@ __device__ __forceinline__ void merge_body(const float *rec_o, const float *rec_
         for (int w = 1; w < 4; ++w)
             merge_partial4(m_t, l_t, o_t, red[w][0][c4], red[w][1][c4],
                            (float4_t){red[w][2][c4], red[w][3][c4], red[w][4][c4], red[w][5][c4]});
-        const float sink2 = sinks ? sinks[h] * MOEARC_LOG2E : -INFINITY;
+        const float sink2 = sinks ? sink_raw * MOEARC_LOG2E : -INFINITY;
         const uint64_t o = ((uint64_t) b * n_heads + h) * 64u + ch;
         float r4[4];
 #pragma unroll
