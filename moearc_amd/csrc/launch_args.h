@@ -189,4 +189,6 @@ struct MatmulArgs {
     uint64_t row_bytes;
     uint32_t rows, cols, n_tok, y_stride;
     uint32_t accumulate;       // 1: y[t][r] += the result (the residual add), else y[t][r] = it
+    uint32_t kb_per;           // k-blocks (of 32) per k-slice: work-group z takes blocks kb_per * z ..
+    float *part;               // split launches (grid z > 1): slice z's sums at part[(z n_tok + t) rows + r]
 };

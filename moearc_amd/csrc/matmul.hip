@@ -32,13 +32,18 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     const uint32_t lr = lane & 15u, lq = lane >> 4;
     const uint32_t r0 = blockIdx.x * (64u * RT) + 16u * RT * wave;  // RT 16-row tiles per wave
     const uint32_t t0 = blockIdx.y * MOEARC_MM_TOKENS;
-    const uint32_t nb = a.cols / 32u;
+    // this work-group's k-slice: blocks kb0 .. kb0 + nb (for the K-quants kb_per is a multiple of
+    // 8, so the sub-block index b & 7 is the same counted from the slice or from the row's start)
+    const uint32_t nb_all = a.cols / 32u, kb0 = blockIdx.z * a.kb_per;
+    const uint32_t nb = min(a.kb_per, nb_all - kb0);
+    const uint64_t kbyte0 = (uint64_t) kb0 * 32u / moearc_mv_be(TY) * moearc_mv_bb(TY);
     const uint8_t *wa[RT];  // this lane's A row (clamped: waves past the last row still stage)
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) wa[rt] = a.w + (uint64_t) min(r0 + 16u * rt + lr, a.rows - 1u) * a.row_bytes;
+    for (int rt = 0; rt < RT; ++rt)
+        wa[rt] = a.w + (uint64_t) min(r0 + 16u * rt + lr, a.rows - 1u) * a.row_bytes + kbyte0;
     const uint64_t ct = min(t0 + (tid & 63u), a.n_tok - 1u);
-    const uint16_t *cxh = a.xh + ct * a.cols + 8u * (tid >> 6);
-    const uint16_t *cxl = a.xl + ct * a.cols + 8u * (tid >> 6);
+    const uint16_t *cxh = a.xh + ct * a.cols + 32u * kb0 + 8u * (tid >> 6);
+    const uint16_t *cxl = a.xl + ct * a.cols + 32u * kb0 + 8u * (tid >> 6);
     float4_t acc[RT][4];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -111,7 +116,7 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
         o.xh = *(const u32x4_t *) (cxh + 32u * b);
         o.xl = *(const u32x4_t *) (cxl + 32u * b);
         if constexpr (TY == 12 || TY == 13)
-            o.xsum = a.xs[ct * nb + b];
+            o.xsum = a.xs[ct * nb_all + kb0 + b];
     };
     auto stage = [&](const Ops &o, uint32_t buf) {
         bsm[buf][0][(tid >> 6) * 64u + (tid & 63u)] = o.xh;
@@ -286,6 +291,10 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
             for (int k = 0; k < 4; ++k) {
                 const uint32_t r = r0 + 16u * rt + 4u * lq + k;
                 if (r < a.rows) {
+                    if (gridDim.z > 1) {  // one slice of a split launch: its sums, for the reduction
+                        a.part[((uint64_t) blockIdx.z * a.n_tok + t) * a.rows + r] = acc[rt][j][k];
+                        continue;
+                    }
                     float *yp = a.y + (uint64_t) t * a.y_stride + r;
                     const float v = a.bias ? acc[rt][j][k] + a.bias[r] : acc[rt][j][k];
                     *yp = a.accumulate ? *yp + v : v;
@@ -336,5 +345,30 @@ extern "C" __global__ void moearc_block_sums_k(const float *x, float *xs, uint64
 #pragma unroll
         for (int j = 0; j < 32; ++j) t += p[j];
         xs[i] = t;
+    }
+}
+
+// The reduction of a split launch: y[t][r] = the sum of the n_slices k-slices' sums (in slice
+// order) + bias[r], added to y[t][r] when a.accumulate -- the single launch's epilogue with the
+// sum taken over slices.
+extern "C" __global__ void moearc_matmul_reduce_k(MatmulArgs a, uint32_t n_slices) {
+    const uint64_t n = (uint64_t) a.n_tok * a.rows;
+    for (uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t) gridDim.x * blockDim.x) {
+        const uint32_t t = (uint32_t) (i / a.rows), r = (uint32_t) (i - (uint64_t) t * a.rows);
+        // eight slices' loads in flight at a time, added in slice order
+        float s = 0.f;
+        uint32_t z = 0;
+        for (; z + 8u <= n_slices; z += 8u) {
+            float v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) v[k] = a.part[(uint64_t) (z + k) * n + i];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) s = (z + k == 0u) ? v[k] : s + v[k];
+        }
+        for (; z < n_slices; ++z) s = z == 0u ? a.part[i] : s + a.part[(uint64_t) z * n + i];
+        float *yp = a.y + (uint64_t) t * a.y_stride + r;
+        const float v = a.bias ? s + a.bias[r] : s;
+        *yp = a.accumulate ? *yp + v : v;
     }
 }

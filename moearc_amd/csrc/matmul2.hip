@@ -77,7 +77,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31u, h = lane >> 5;
     const uint32_t t0 = blockIdx.y * MM2_TOK, r0 = blockIdx.x * MM2_ROWS;
-    const uint32_t nb = a.cols / 32u;
+    // this work-group's k-slice: blocks kb0 .. kb0 + nb
+    const uint32_t kb0 = blockIdx.z * a.kb_per, nb = min(a.kb_per, a.cols / 32u - kb0);
     const uint32_t lds0 = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles;
 
     // LDS DMA: instruction i of wave w fills region R = 4 w + i (1 KiB): half R >> 3, tokens
@@ -90,7 +91,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         const uint32_t tok = 16u * (R & 7u) + (lane >> 2);
         const uint32_t c = (lane & 3u) ^ mm2_swz(tok);
         const uint64_t tg = min(t0 + tok, a.n_tok - 1u);
-        dma_src[i] = ((R >> 3) ? a.xl : a.xh) + tg * a.cols + 8u * c;
+        dma_src[i] = ((R >> 3) ? a.xl : a.xh) + tg * a.cols + 32u * kb0 + 8u * c;
     }
     auto dma = [&](uint32_t b, uint32_t buf) {
 #pragma unroll
@@ -106,7 +107,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     const uint8_t *wrow[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
-        wrow[rt] = a.w + (uint64_t) min(r0 + 64u * (wave >> 1) + 32u * rt + n, a.rows - 1u) * a.row_bytes;
+        wrow[rt] = a.w + (uint64_t) min(r0 + 64u * (wave >> 1) + 32u * rt + n, a.rows - 1u) * a.row_bytes +
+                   (TY == 8 ? 34u : 64u) * (uint64_t) kb0;
     auto wload = [&](uint32_t b, Mm2W<TY> &o) {
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
@@ -224,6 +226,16 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     for (int rt = 0; rt < 2; ++rt) {
         const uint32_t r = r0 + 64u * (wave >> 1) + 32u * rt + n;
         if (r >= a.rows) continue;
+        if (gridDim.z > 1) {  // one slice of a split launch: its sums, for the reduction
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const uint32_t t = t0 + 64u * (wave & 1u) + 32u * tt + 8u * (j >> 2) + 4u * h + (j & 3);
+                    if (t < a.n_tok) a.part[((uint64_t) blockIdx.z * a.n_tok + t) * a.rows + r] = acc[tt][rt][j];
+                }
+            continue;
+        }
         const float bias = a.bias ? a.bias[r] : 0.f;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)

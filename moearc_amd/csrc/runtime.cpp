@@ -90,6 +90,9 @@ struct moearc_ctx {
     hipFunction_t f_mm2[2] = {};  // Q8_0, F16: 128 x 128 tiles on the 32x32x16 MFMA
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
+    float *mm_part = nullptr;   // the k-slices' sums of split chunk products
+    size_t mm_part_floats = 0;
+    hipFunction_t f_mm_reduce = nullptr;
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
     hipFunction_t f_prefill_precise[4] = {};  // the same with p split into f16 hi + lo
     bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
@@ -188,7 +191,7 @@ bool tracks(const moearc_ctx *c, const char *what) {
 // Launch `f` with one by-value argument block. With profiling on, a HIP event pair brackets the
 // launch under the key "<what> r<r> m<m>" (the reference's key format, kernels.cpp:1905-1916).
 template <typename Args>
-int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, unsigned block,
+int launch3d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, unsigned grid_z, unsigned block,
              const Args &args, const char *what, unsigned long r, unsigned long m,
              unsigned lds_bytes = 0, const char *kernel = nullptr) {
     if (!f) return ERR;
@@ -204,7 +207,7 @@ int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, uns
     void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *) &args, HIP_LAUNCH_PARAM_BUFFER_SIZE,
                       &size, HIP_LAUNCH_PARAM_END};
     const hipError_t err =
-        hipModuleLaunchKernel(f, grid, grid_y, 1, block, 1, 1, lds_bytes, c->stream, nullptr, config);
+        hipModuleLaunchKernel(f, grid, grid_y, grid_z, block, 1, 1, lds_bytes, c->stream, nullptr, config);
     if (e0) {
         if (own) {
             record_bracket(c, e0, what, r, m);
@@ -215,6 +218,13 @@ int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, uns
         }
     }
     return err == hipSuccess ? OK : ERR;
+}
+
+template <typename Args>
+int launch2d(moearc_ctx *c, hipFunction_t f, unsigned grid, unsigned grid_y, unsigned block,
+             const Args &args, const char *what, unsigned long r, unsigned long m,
+             unsigned lds_bytes = 0, const char *kernel = nullptr) {
+    return launch3d(c, f, grid, grid_y, 1, block, args, what, r, m, lds_bytes, kernel);
 }
 
 template <typename Args>
@@ -524,7 +534,8 @@ moearc_ctx *release(moearc_ctx *c) {
         (void) hipEventDestroy(p.stop);
     }
     for (auto e : c->event_pool) (void) hipEventDestroy(e);
-    for (void *p : {(void *) c->ws, (void *) c->blk_ws, (void *) c->mm_ws, (void *) c->err_word})
+    for (void *p : {(void *) c->ws, (void *) c->blk_ws, (void *) c->mm_ws, (void *) c->mm_part,
+                    (void *) c->err_word})
         if (p) (void) hipFree(p);
     if (c->module) (void) hipModuleUnload(c->module);
     if (c->stream) (void) hipStreamDestroy(c->stream);
@@ -596,6 +607,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm2[1], "moearc_matmul2_f16_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
+        {&c->f_mm_reduce, "moearc_matmul_reduce_k"},
     };
     for (auto &f : fns) {
         if (hipModuleGetFunction(f.slot, c->module, f.name) != hipSuccess) {
@@ -1243,6 +1255,16 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
 
 namespace {
 
+constexpr uint64_t kMmCUs = 256;  // compute units the chunk product's launch shapes are sized for
+
+// The reduction launch's arguments: the product's (y, bias, residual flag, slice sums) and the
+// slice count.
+struct MmReduceLaunch {
+    MatmulArgs a;
+    uint32_t n_slices;
+    uint32_t pad;
+};
+
 // Chunk-product formats: index into f_mm, or -1.
 int mm_index(unsigned ty) {
     return ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 39u ? 4 : ty == 14u ? 5 : -1;
@@ -1276,15 +1298,66 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     // Q8_0 and F16 over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
     // (matmul2.hip). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
     // pays while the launch still has about two work-groups per CU; shorter chunks take 16.
+    hipFunction_t f;
+    unsigned gx, gy;
     if ((ty == 8u || ty == 1u) && n_tok >= 64) {
-        return launch2d(c, c->f_mm2[ty == 8u ? 0 : 1], (unsigned) ((n_rows + 127) / 128),
-                        (unsigned) ((n_tok + 127) / 128), 256, a, what, n_rows, n_tok);
+        f = c->f_mm2[ty == 8u ? 0 : 1];
+        gx = (unsigned) ((n_rows + 127) / 128);
+        gy = (unsigned) ((n_tok + 127) / 128);
+    } else {
+        const unsigned long tok_groups = (n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS;
+        const int r2 = ((n_rows + 127) / 128) * tok_groups >= 512 ? 1 : 0;
+        const unsigned long rows_per_wg = r2 ? 128 : 64;
+        f = c->f_mm[mm_index(ty)][r2];
+        gx = (unsigned) ((n_rows + rows_per_wg - 1) / rows_per_wg);
+        gy = (unsigned) tok_groups;
     }
-    const unsigned long tok_groups = (n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS;
-    const int r2 = ((n_rows + 127) / 128) * tok_groups >= 512 ? 1 : 0;
-    const unsigned long rows_per_wg = r2 ? 128 : 64;
-    return launch2d(c, c->f_mm[mm_index(ty)][r2], (unsigned) ((n_rows + rows_per_wg - 1) / rows_per_wg),
-                    (unsigned) tok_groups, 256, a, what, n_rows, n_tok);
+    // Split-K. A tile grid of at most one work-group per CU leaves most of the device idle while
+    // each work-group walks the whole reduction (a 128-token chunk's k and v projections at gpt-oss
+    // shapes are 4 work-groups), so the reduction is cut into slices of at least 4 k-blocks over a
+    // third grid dimension -- up to about two work-groups per CU in all -- whose sums a second
+    // launch adds in slice order, with the bias and the residual. K-quant slices start on a
+    // 256-element super-block (a multiple of 8 k-blocks).
+    const uint64_t nb = n_cols / 32, tiles = (uint64_t) gx * gy;
+    const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : 1;
+    uint64_t slices = 1, kb_per = nb;
+    if (tiles <= kMmCUs && nb >= 8) {
+        const uint64_t want = std::min<uint64_t>(2 * kMmCUs / tiles, nb / 4);
+        kb_per = (nb + want - 1) / want;
+        kb_per = (kb_per + gran - 1) / gran * gran;
+        slices = (nb + kb_per - 1) / kb_per;
+    }
+    a.kb_per = (uint32_t) kb_per;
+    if (slices < 2) return launch2d(c, f, gx, gy, 256, a, what, n_rows, n_tok);
+    const size_t part = (size_t) slices * n_tok * n_rows;
+    if (part > c->mm_part_floats) {
+        if (c->mm_part) {
+            if (hipStreamSynchronize(c->stream) != hipSuccess || hipFree(c->mm_part) != hipSuccess) return ERR;
+            c->mm_part = nullptr;
+            c->mm_part_floats = 0;
+        }
+        if (hipMalloc((void **) &c->mm_part, part * sizeof(float)) != hipSuccess) return ERR;
+        c->mm_part_floats = part;
+    }
+    a.part = c->mm_part;
+    // one bracket for the call (the product and its reduction), as for a single launch
+    hipEvent_t call0 = nullptr;
+    if (what && tracks(c, what) && (call0 = take_event(c))) {
+        if (hipEventRecord(call0, c->stream) != hipSuccess) {
+            c->event_pool.push_back(call0);
+            call0 = nullptr;
+        }
+    }
+    ++c->scope_depth;
+    int rc = launch3d(c, f, gx, gy, (unsigned) slices, 256, a, what, n_rows, n_tok);
+    if (rc == OK) {
+        const uint64_t n = (uint64_t) n_tok * n_rows;
+        rc = launch2d(c, c->f_mm_reduce, (unsigned) std::min<uint64_t>((n + 255) / 256, 65536), 1, 256,
+                      MmReduceLaunch{a, (uint32_t) slices}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
+    }
+    --c->scope_depth;
+    if (call0) record_bracket(c, call0, what, n_rows, n_tok);
+    return rc;
 }
 
 // The f16 hi / lo split of x (n floats, n a multiple of 32) and its 32-element block sums into

@@ -217,7 +217,11 @@ def test_matvec_refusals_and_empty_shapes(ctx):
     # K-quants (sub-block scales and mins) and MXFP4, both launch shapes
     (QuantType.Q4_K, 37, 200, 1024), (QuantType.Q4_K, 512, 8192, 256), (QuantType.Q5_K, 67, 96, 2048),
     (QuantType.Q5_K, 512, 8192, 256), (QuantType.MXFP4, 37, 200, 1024), (QuantType.MXFP4, 512, 8192, 96),
-    (QuantType.Q6_K, 37, 200, 1024), (QuantType.Q6_K, 512, 8192, 256)],
+    (QuantType.Q6_K, 37, 200, 1024), (QuantType.Q6_K, 512, 8192, 256),
+    # grids of at most one work-group per CU split the reduction into k-slices (also above: every
+    # case with 16 or more k-blocks and a small grid, K-quant slices on super-block bounds, a ragged
+    # last slice) -- here a 128-token chunk's output projection at gpt-oss shapes, 16 slices
+    (QuantType.Q8_0, 128, 2880, 4096)],
     ids=str)
 def test_chunk_matmul_meets_the_matvec_bound(ctx, ty, n_tok, rows, cols):
     # the MFMA product of a chunk, token by token against the oracle's matvec. The bound is the
