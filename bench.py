@@ -678,7 +678,8 @@ def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
     decode_graph (the main line's timed region: C2 steps in one graph, replayed), decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
     C4 chunk), matvec (the projection cases of MV_CASES, in order), matmul (MM_CASES, each as
-    a graph of `steps` launches, replayed twice), read_floor (the calibration read of C2's 64 MiB of
+    a graph of `steps` launches, replayed twice), block (`steps` rounds of bench_block: the 128-token
+    attention block as one chunked call and as single-token calls), read_floor (the calibration read of C2's 64 MiB of
     KV over the rotating copies), or copy (a 256 MiB device-to-device copy, the reference size for
     scaling FETCH_SIZE/WRITE_SIZE readings to bytes)."""
     from moearc_amd import Context, KvType, OUT_F16
@@ -729,6 +730,10 @@ def only(what, steps, warmup):
         elif what == "matmul":
             hip = Hip()
             bench_matmul(ctx, hip, steps=steps)
+        elif what == "block":
+            hip = Hip()
+            for _ in range(max(1, steps)):
+                bench_block(ctx, hip)
         elif what == "read_floor":
             bufs, out, nbytes = read_floor_inputs(ctx)
             for i in range(warmup + steps):
@@ -754,7 +759,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "rope_append", "matvec", "matmul",
-                                       "read_floor", "copy"],
+                                       "block", "read_floor", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")

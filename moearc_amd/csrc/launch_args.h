@@ -176,19 +176,31 @@ struct MatvecArgs {
     uint32_t res_mask;     // bit s: out[s][r] += the result (the residual add), else out[s][r] = it
 };
 
-// Chunk-form projections (matmul.hip): Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the n_tok
-// tokens of a prompt chunk, W Q8_0 (8), F16 (1), Q4_K (12), Q5_K (13) or MXFP4 (39), X given as its
-// f16 hi + lo split.
+// Chunk-form projections (matmul.hip, matmul2.hip): Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for
+// the n_tok tokens of a prompt chunk, W Q8_0 (8), F16 (1), Q4_K (12), Q5_K (13), Q6_K (14) or
+// MXFP4 (39), X given as its f16 hi + lo split. One launch serves up to MOEARC_MM_MAX_SEG matrices
+// of one weight type over the same X (a block's q, k and v): its row tiles (grid x) run over the
+// segments in order.
 #define MOEARC_MM_TOKENS 64    // tokens per work-group
-struct MatmulArgs {
+#define MOEARC_MM_MAX_SEG 3
+struct MatmulSeg {
     const uint8_t *w;
-    const uint16_t *xh, *xl;   // [n_tok][cols] f16: x = hi + lo to within 2^-22 |x|
-    const float *xs;           // [n_tok][cols / 32] block sums of x (Q4_K, Q5_K), else null
     const float *bias;         // [rows] or null
     float *y;                  // [n_tok][y_stride]
     uint64_t row_bytes;
-    uint32_t rows, cols, n_tok, y_stride;
+    uint64_t part_off;         // split launches: this matrix's sums at part + z * part_stride + part_off
+    uint32_t rows, y_stride;
+    uint32_t tile_end;         // row tiles of the launch up to and including this matrix's
+    uint32_t pad;
+};
+struct MatmulArgs {
+    MatmulSeg seg[MOEARC_MM_MAX_SEG];
+    const uint16_t *xh, *xl;   // [n_tok][cols] f16: x = hi + lo to within 2^-22 |x|
+    const float *xs;           // [n_tok][cols / 32] block sums of x (Q4_K, Q5_K), else unread
+    float *part;               // split launches (grid z > 1): slice z's sums, [t][r] per matrix
+    uint64_t part_stride;      // floats per slice: the sum of n_tok * rows over the matrices
+    uint32_t n_seg, cols, n_tok;
     uint32_t accumulate;       // 1: y[t][r] += the result (the residual add), else y[t][r] = it
     uint32_t kb_per;           // k-blocks (of 32) per k-slice: work-group z takes blocks kb_per * z ..
-    float *part;               // split launches (grid z > 1): slice z's sums at part[(z n_tok + t) rows + r]
+    uint32_t pad;
 };

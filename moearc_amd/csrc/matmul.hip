@@ -20,6 +20,22 @@ typedef _Float16 mm_half8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float mm_f16(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 
+// The matrix of a launch that row tile x falls in (segments in order), and x's tile within it.
+struct MmSegView {
+    const uint8_t *w;
+    const float *bias;
+    float *y;
+    uint64_t row_bytes, part_off;
+    uint32_t rows, y_stride, tile;
+};
+__device__ __forceinline__ MmSegView mm_seg(const MatmulArgs &a, uint32_t x) {
+    uint32_t s = 0;
+    while (s + 1u < a.n_seg && x >= a.seg[s].tile_end) ++s;
+    const MatmulSeg &g = a.seg[s];
+    return MmSegView{g.w, g.bias, g.y, g.row_bytes, g.part_off, g.rows, g.y_stride,
+                     x - (s ? a.seg[s - 1u].tile_end : 0u)};
+}
+
 template <uint32_t TY, int RT, int NST>
 __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     // The work-group's activation tile of one k-block (64 tokens x 32 k, hi and lo) is staged in
@@ -30,7 +46,8 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     __shared__ float xsm[2][64];  // K-quants: the tile's per-token block sums
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t lr = lane & 15u, lq = lane >> 4;
-    const uint32_t r0 = blockIdx.x * (64u * RT) + 16u * RT * wave;  // RT 16-row tiles per wave
+    const MmSegView sg = mm_seg(a, blockIdx.x);
+    const uint32_t r0 = sg.tile * (64u * RT) + 16u * RT * wave;  // RT 16-row tiles per wave
     const uint32_t t0 = blockIdx.y * MOEARC_MM_TOKENS;
     // this work-group's k-slice: blocks kb0 .. kb0 + nb (for the K-quants kb_per is a multiple of
     // 8, so the sub-block index b & 7 is the same counted from the slice or from the row's start)
@@ -40,7 +57,7 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
     const uint8_t *wa[RT];  // this lane's A row (clamped: waves past the last row still stage)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-        wa[rt] = a.w + (uint64_t) min(r0 + 16u * rt + lr, a.rows - 1u) * a.row_bytes + kbyte0;
+        wa[rt] = sg.w + (uint64_t) min(r0 + 16u * rt + lr, sg.rows - 1u) * sg.row_bytes + kbyte0;
     const uint64_t ct = min(t0 + (tid & 63u), a.n_tok - 1u);
     const uint16_t *cxh = a.xh + ct * a.cols + 32u * kb0 + 8u * (tid >> 6);
     const uint16_t *cxl = a.xl + ct * a.cols + 32u * kb0 + 8u * (tid >> 6);
@@ -290,13 +307,13 @@ __device__ __forceinline__ void matmul_body(const MatmulArgs &a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint32_t r = r0 + 16u * rt + 4u * lq + k;
-                if (r < a.rows) {
+                if (r < sg.rows) {
                     if (gridDim.z > 1) {  // one slice of a split launch: its sums, for the reduction
-                        a.part[((uint64_t) blockIdx.z * a.n_tok + t) * a.rows + r] = acc[rt][j][k];
+                        a.part[blockIdx.z * a.part_stride + sg.part_off + (uint64_t) t * sg.rows + r] = acc[rt][j][k];
                         continue;
                     }
-                    float *yp = a.y + (uint64_t) t * a.y_stride + r;
-                    const float v = a.bias ? acc[rt][j][k] + a.bias[r] : acc[rt][j][k];
+                    float *yp = sg.y + (uint64_t) t * sg.y_stride + r;
+                    const float v = sg.bias ? acc[rt][j][k] + sg.bias[r] : acc[rt][j][k];
                     *yp = a.accumulate ? *yp + v : v;
                 }
             }
@@ -350,12 +367,16 @@ extern "C" __global__ void moearc_block_sums_k(const float *x, float *xs, uint64
 
 // The reduction of a split launch: y[t][r] = the sum of the n_slices k-slices' sums (in slice
 // order) + bias[r], added to y[t][r] when a.accumulate -- the single launch's epilogue with the
-// sum taken over slices.
+// sum taken over slices -- for every matrix of the launch.
 extern "C" __global__ void moearc_matmul_reduce_k(MatmulArgs a, uint32_t n_slices) {
-    const uint64_t n = (uint64_t) a.n_tok * a.rows;
+    const uint64_t n = a.part_stride;
     for (uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t) gridDim.x * blockDim.x) {
-        const uint32_t t = (uint32_t) (i / a.rows), r = (uint32_t) (i - (uint64_t) t * a.rows);
+        uint32_t g = 0;
+        while (g + 1u < a.n_seg && i >= a.seg[g + 1u].part_off) ++g;
+        const MatmulSeg &sg = a.seg[g];
+        const uint64_t e = i - sg.part_off;
+        const uint32_t t = (uint32_t) (e / sg.rows), r = (uint32_t) (e - (uint64_t) t * sg.rows);
         // eight slices' loads in flight at a time, added in slice order
         float s = 0.f;
         uint32_t z = 0;
@@ -367,8 +388,8 @@ extern "C" __global__ void moearc_matmul_reduce_k(MatmulArgs a, uint32_t n_slice
             for (uint32_t k = 0; k < 8u; ++k) s = (z + k == 0u) ? v[k] : s + v[k];
         }
         for (; z < n_slices; ++z) s = z == 0u ? a.part[i] : s + a.part[(uint64_t) z * n + i];
-        float *yp = a.y + (uint64_t) t * a.y_stride + r;
-        const float v = a.bias ? s + a.bias[r] : s;
+        float *yp = sg.y + (uint64_t) t * sg.y_stride + r;
+        const float v = sg.bias ? s + sg.bias[r] : s;
         *yp = a.accumulate ? *yp + v : v;
     }
 }

@@ -76,7 +76,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31u, h = lane >> 5;
-    const uint32_t t0 = blockIdx.y * MM2_TOK, r0 = blockIdx.x * MM2_ROWS;
+    const MmSegView sg = mm_seg(a, blockIdx.x);
+    const uint32_t t0 = blockIdx.y * MM2_TOK, r0 = sg.tile * MM2_ROWS;
     // this work-group's k-slice: blocks kb0 .. kb0 + nb
     const uint32_t kb0 = blockIdx.z * a.kb_per, nb = min(a.kb_per, a.cols / 32u - kb0);
     const uint32_t lds0 = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles;
@@ -107,7 +108,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     const uint8_t *wrow[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
-        wrow[rt] = a.w + (uint64_t) min(r0 + 64u * (wave >> 1) + 32u * rt + n, a.rows - 1u) * a.row_bytes +
+        wrow[rt] = sg.w + (uint64_t) min(r0 + 64u * (wave >> 1) + 32u * rt + n, sg.rows - 1u) * sg.row_bytes +
                    (TY == 8 ? 34u : 64u) * (uint64_t) kb0;
     auto wload = [&](uint32_t b, Mm2W<TY> &o) {
 #pragma unroll
@@ -225,25 +226,26 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
         const uint32_t r = r0 + 64u * (wave >> 1) + 32u * rt + n;
-        if (r >= a.rows) continue;
+        if (r >= sg.rows) continue;
         if (gridDim.z > 1) {  // one slice of a split launch: its sums, for the reduction
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const uint32_t t = t0 + 64u * (wave & 1u) + 32u * tt + 8u * (j >> 2) + 4u * h + (j & 3);
-                    if (t < a.n_tok) a.part[((uint64_t) blockIdx.z * a.n_tok + t) * a.rows + r] = acc[tt][rt][j];
+                    if (t < a.n_tok)
+                        a.part[blockIdx.z * a.part_stride + sg.part_off + (uint64_t) t * sg.rows + r] = acc[tt][rt][j];
                 }
             continue;
         }
-        const float bias = a.bias ? a.bias[r] : 0.f;
+        const float bias = sg.bias ? sg.bias[r] : 0.f;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const uint32_t t = t0 + 64u * (wave & 1u) + 32u * tt + 8u * (j >> 2) + 4u * h + (j & 3);
                 if (t < a.n_tok) {
-                    float *yp = a.y + (uint64_t) t * a.y_stride + r;
+                    float *yp = sg.y + (uint64_t) t * sg.y_stride + r;
                     const float v = acc[tt][rt][j] + bias;
                     *yp = a.accumulate ? *yp + v : v;
                 }

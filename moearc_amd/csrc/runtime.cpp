@@ -1278,40 +1278,66 @@ int mm_check(unsigned ty, const void *w, unsigned long n_tok, unsigned long n_ro
     return OK;
 }
 
-// y = W x over a chunk, x given as its f16 split (xh, xl) of n_tok x n_cols.
-int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, const void *w,
-              const uint16_t *xh, const uint16_t *xl, const float *xs, const float *bias, unsigned long n_tok,
-              unsigned long n_rows, unsigned long n_cols, const char *what, bool accumulate = false) {
+// One matrix of a chunk-product launch: y (row stride y_stride) = W x (+ bias), W rows x n_cols.
+struct MmMat {
+    const void *w;
+    const float *bias;
+    float *y;
+    unsigned long y_stride, rows;
+};
+
+// y = W x for n_mat matrices of one weight type over the same chunk x, given as its f16 split
+// (xh, xl) of n_tok x n_cols, in one launch (plus the split-K reduction).
+int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const uint16_t *xh, const uint16_t *xl,
+              const float *xs, unsigned long n_tok, unsigned long n_cols, const char *what,
+              bool accumulate = false) {
+    if (n_mat == 0 || n_mat > MOEARC_MM_MAX_SEG) return ERR;
     MatmulArgs a{};
     a.accumulate = accumulate ? 1u : 0u;
-    a.w = static_cast<const uint8_t *>(w);
     a.xh = xh;
     a.xl = xl;
     a.xs = xs;
-    a.bias = bias;
-    a.y = y;
-    a.row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
-    a.rows = (uint32_t) n_rows;
     a.cols = (uint32_t) n_cols;
     a.n_tok = (uint32_t) n_tok;
-    a.y_stride = (uint32_t) y_stride;
+    a.n_seg = n_mat;
+    unsigned long n_rows = 0, tiles128 = 0;
+    for (unsigned i = 0; i < n_mat; ++i) {
+        n_rows += m[i].rows;
+        tiles128 += (m[i].rows + 127) / 128;
+    }
     // Q8_0 and F16 over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
     // (matmul2.hip). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
     // pays while the launch still has about two work-groups per CU; shorter chunks take 16.
     hipFunction_t f;
-    unsigned gx, gy;
+    unsigned long rows_per_tile;
+    unsigned gy;
     if ((ty == 8u || ty == 1u) && n_tok >= 64) {
         f = c->f_mm2[ty == 8u ? 0 : 1];
-        gx = (unsigned) ((n_rows + 127) / 128);
+        rows_per_tile = 128;
         gy = (unsigned) ((n_tok + 127) / 128);
     } else {
         const unsigned long tok_groups = (n_tok + MOEARC_MM_TOKENS - 1) / MOEARC_MM_TOKENS;
-        const int r2 = ((n_rows + 127) / 128) * tok_groups >= 512 ? 1 : 0;
-        const unsigned long rows_per_wg = r2 ? 128 : 64;
+        const int r2 = tiles128 * tok_groups >= 512 ? 1 : 0;
         f = c->f_mm[mm_index(ty)][r2];
-        gx = (unsigned) ((n_rows + rows_per_wg - 1) / rows_per_wg);
+        rows_per_tile = r2 ? 128 : 64;
         gy = (unsigned) tok_groups;
     }
+    uint64_t tile_end = 0, part_off = 0;
+    for (unsigned i = 0; i < n_mat; ++i) {
+        MatmulSeg &g = a.seg[i];
+        g.w = static_cast<const uint8_t *>(m[i].w);
+        g.bias = m[i].bias;
+        g.y = m[i].y;
+        g.row_bytes = (uint64_t) n_cols / moearc_mv_be(ty) * moearc_mv_bb(ty);
+        g.rows = (uint32_t) m[i].rows;
+        g.y_stride = (uint32_t) m[i].y_stride;
+        g.part_off = part_off;
+        tile_end += (m[i].rows + rows_per_tile - 1) / rows_per_tile;
+        g.tile_end = (uint32_t) tile_end;
+        part_off += (uint64_t) n_tok * m[i].rows;
+    }
+    a.part_stride = part_off;
+    const unsigned gx = (unsigned) tile_end;
     // Split-K. A tile grid of at most one work-group per CU leaves most of the device idle while
     // each work-group walks the whole reduction (a 128-token chunk's k and v projections at gpt-oss
     // shapes are 4 work-groups), so the reduction is cut into slices of at least 4 k-blocks over a
@@ -1329,7 +1355,7 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     }
     a.kb_per = (uint32_t) kb_per;
     if (slices < 2) return launch2d(c, f, gx, gy, 256, a, what, n_rows, n_tok);
-    const size_t part = (size_t) slices * n_tok * n_rows;
+    const size_t part = (size_t) slices * a.part_stride;
     if (part > c->mm_part_floats) {
         if (c->mm_part) {
             if (hipStreamSynchronize(c->stream) != hipSuccess || hipFree(c->mm_part) != hipSuccess) return ERR;
@@ -1351,7 +1377,7 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     ++c->scope_depth;
     int rc = launch3d(c, f, gx, gy, (unsigned) slices, 256, a, what, n_rows, n_tok);
     if (rc == OK) {
-        const uint64_t n = (uint64_t) n_tok * n_rows;
+        const uint64_t n = a.part_stride;
         rc = launch2d(c, c->f_mm_reduce, (unsigned) std::min<uint64_t>((n + 255) / 256, 65536), 1, 256,
                       MmReduceLaunch{a, (uint32_t) slices}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
     }
@@ -1360,9 +1386,13 @@ int mm_launch(moearc_ctx *c, unsigned ty, float *y, unsigned long y_stride, cons
     return rc;
 }
 
-// The f16 hi / lo split of x (n floats, n a multiple of 32) and its 32-element block sums into
-// the context's buffer.
-int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl, float **xs) {
+// Whether a chunk product of this weight type reads the activation's block sums (the K-quants'
+// mins: Q4_K, Q5_K).
+bool mm_needs_sums(unsigned ty) { return ty == 12u || ty == 13u; }
+
+// The f16 hi / lo split of x (n floats, n a multiple of 32) into the context's buffer, and its
+// 32-element block sums when `sums` (else *xs points at space the products do not read).
+int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl, float **xs, bool sums) {
     const size_t halves = 2 * n + n / 16;  // hi, lo, then n / 32 floats
     if (halves > c->mm_ws_halves) {
         if (c->mm_ws) {
@@ -1381,9 +1411,10 @@ int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **
         float *xs;
         uint64_t n;
     } bs{x, *xs, n / 32};
-    if (const int rc = launch(c, c->f_bsums, (unsigned) std::min<size_t>((n / 32 + 255) / 256, 65536), 256, bs,
-                              "block_sums", n / 32, 0))
-        return rc;
+    if (sums)
+        if (const int rc = launch(c, c->f_bsums, (unsigned) std::min<size_t>((n / 32 + 255) / 256, 65536), 256,
+                                  bs, "block_sums", n / 32, 0))
+            return rc;
     struct {
         const float *x;
         uint16_t *hi, *lo;
@@ -1401,8 +1432,9 @@ int moearc_matmul_q(moearc_ctx *c, unsigned int type_id, float *y, const void *w
     if (n_rows == 0 || n_tok == 0) return OK;
     uint16_t *xh, *xl;
     float *xs;
-    if (const int rc = mm_split(c, x, n_tok * n_cols, &xh, &xl, &xs)) return rc;
-    return mm_launch(c, type_id, y, n_rows, w, xh, xl, xs, bias, n_tok, n_rows, n_cols, "matmul");
+    if (const int rc = mm_split(c, x, n_tok * n_cols, &xh, &xl, &xs, mm_needs_sums(type_id))) return rc;
+    const MmMat mat{w, bias, y, n_rows, n_rows};
+    return mm_launch(c, type_id, &mat, 1, xh, xl, xs, n_tok, n_cols, "matmul");
 }
 
 namespace {
@@ -1472,13 +1504,23 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     if (mm_qkv) {
         uint16_t *xh, *xl;
         float *xs;
-        if (const int rc = mm_split(c, x, n_tok * E, &xh, &xl, &xs)) return rc;
+        const bool sums = mm_needs_sums(b->w_type[0]) || mm_needs_sums(b->w_type[1]) || mm_needs_sums(b->w_type[2]);
+        if (const int rc = mm_split(c, x, n_tok * E, &xh, &xl, &xs, sums)) return rc;
         float *outs[3] = {q, k, v};
         const unsigned long rows[3] = {q_rows, kv_rows, kv_rows};
-        for (int i = 0; i < 3; ++i)
-            if (const int rc = mm_launch(c, b->w_type[i], outs[i], rows[i], b->w[i], xh, xl, xs, b->bias[i], n_tok,
-                                         rows[i], E, "attn_qkv_mm"))
-                return rc;
+        // the projections of one weight type in one launch (a block's q, k and v usually share it)
+        bool done[3] = {false, false, false};
+        for (int i = 0; i < 3; ++i) {
+            if (done[i]) continue;
+            MmMat mats[3];
+            unsigned n = 0;
+            for (int j = i; j < 3; ++j) {
+                if (done[j] || b->w_type[j] != b->w_type[i]) continue;
+                done[j] = true;
+                mats[n++] = MmMat{b->w[j], b->bias[j], outs[j], rows[j], rows[j]};
+            }
+            if (const int rc = mm_launch(c, b->w_type[i], mats, n, xh, xl, xs, n_tok, E, "attn_qkv_mm")) return rc;
+        }
     } else {
         float *outs[3] = {q, k, v};
         const unsigned long rows[3] = {q_rows, kv_rows, kv_rows};
@@ -1522,9 +1564,9 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     if (n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK) {
         uint16_t *xh, *xl;
         float *xs;
-        if (const int rc = mm_split(c, att, nq, &xh, &xl, &xs)) return rc;
-        return mm_launch(c, b->w_type[3], h, E, b->w[3], xh, xl, xs, b->bias[3], n_tok, E, q_rows, "attn_proj_mm",
-                         true);
+        if (const int rc = mm_split(c, att, nq, &xh, &xl, &xs, mm_needs_sums(b->w_type[3]))) return rc;
+        const MmMat mat{b->w[3], b->bias[3], h, E, E};
+        return mm_launch(c, b->w_type[3], &mat, 1, xh, xl, xs, n_tok, q_rows, "attn_proj_mm", true);
     }
     std::vector<MvJob> jobs;
     for (unsigned long t = 0; t < n_tok; ++t)
