@@ -54,11 +54,12 @@ __device__ __forceinline__ void pair_channels(const RopeParams &r, uint32_t j, u
 // shrinks by that factor, and the thread's 2*ROPE_HEADS independent loads (4*ROPE_HEADS when V
 // rides along) are all issued before the first store.
 
-// moearc_rope: src/dst f32 [n_tokens][n_heads][head_dim]; dst may equal src.
+// moearc_rope: src/dst f32 [n_tokens][n_heads][head_dim]; dst may equal src. F16: dst is written
+// as binary16 (f32_to_f16_bits of the f32 result, as moearc_quantize_f16 would narrow it).
 // Grid: x over (token, pair slot), y over groups of ROPE_HEADS heads.
-extern "C" __global__ void moearc_rope_k(float *dst, const float *src, const int *pos,
-                                         uint64_t n_tokens, uint32_t n_heads, uint32_t head_dim,
-                                         RopeParams r) {
+template <bool F16>
+__device__ __forceinline__ void rope_body(void *dst, const float *src, const int *pos, uint64_t n_tokens,
+                                          uint32_t n_heads, uint32_t head_dim, const RopeParams &r) {
     const uint32_t slots = (head_dim + 1u) >> 1;  // pair slots per head (head_dim may be odd)
     const uint64_t g = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= n_tokens * slots) return;
@@ -79,19 +80,32 @@ extern "C" __global__ void moearc_rope_k(float *dst, const float *src, const int
     }
     float2_t cs = {1.0f, 0.0f};
     if (rot) cs = rope_factors(r, pos[t], j);
+    auto put = [&](uint64_t at, float v) {
+        if constexpr (F16) ((uint16_t *) dst)[at] = f32_to_f16_bits(v);
+        else ((float *) dst)[at] = v;
+    };
 #pragma unroll
     for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
         if (h0 + i < n_heads) {
-            float *o = dst + (t * n_heads + h0 + i) * head_dim;
+            const uint64_t o = (t * n_heads + h0 + i) * head_dim;
             if (rot) {
-                o[lo] = x0[i] * cs[0] - x1[i] * cs[1];
-                o[hi] = x0[i] * cs[1] + x1[i] * cs[0];
+                put(o + lo, x0[i] * cs[0] - x1[i] * cs[1]);
+                put(o + hi, x0[i] * cs[1] + x1[i] * cs[0]);
             } else {
-                o[lo] = x0[i];
-                if (has_hi) o[hi] = x1[i];
+                put(o + lo, x0[i]);
+                if (has_hi) put(o + hi, x1[i]);
             }
         }
     }
+}
+
+extern "C" __global__ void moearc_rope_k(float *dst, const float *src, const int *pos, uint64_t n_tokens,
+                                         uint32_t n_heads, uint32_t head_dim, RopeParams r) {
+    rope_body<false>(dst, src, pos, n_tokens, n_heads, head_dim, r);
+}
+extern "C" __global__ void moearc_rope_f16_k(uint16_t *dst, const float *src, const int *pos, uint64_t n_tokens,
+                                             uint32_t n_heads, uint32_t head_dim, RopeParams r) {
+    rope_body<true>(dst, src, pos, n_tokens, n_heads, head_dim, r);
 }
 
 // A prefill chunk's K (rotated) and V to (page_ids[t], slots[t]); k, v f32 [n_tok][n_kv_heads][head_dim].

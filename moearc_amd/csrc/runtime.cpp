@@ -79,7 +79,7 @@ struct moearc_ctx {
     hipStream_t stream = nullptr;
     hipModule_t module = nullptr;
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
-    hipFunction_t f_rope = nullptr, f_rope_append_chunk = nullptr;
+    hipFunction_t f_rope = nullptr, f_rope_f16 = nullptr, f_rope_append_chunk = nullptr;
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[2] = {};  // split kernels (kDecodeVariants)
     hipFunction_t f_dec_merge = nullptr;
@@ -584,6 +584,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_append, "moearc_kv_append_k"},
         {&c->f_append_chunk, "moearc_kv_append_chunk_k"},
         {&c->f_rope, "moearc_rope_k"},
+        {&c->f_rope_f16, "moearc_rope_f16_k"},
         {&c->f_rope_append_chunk, "moearc_rope_kv_append_chunk_k"},
         {&c->f_dec_general, "moearc_attn_decode_general_k"},
         {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k4w2t4"},
@@ -682,7 +683,12 @@ static RopeParams rope_params(unsigned long n_dims, float freq_base, float freq_
     return r;
 }
 
-int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
+}  // extern "C"
+
+namespace {
+
+// moearc_rope's checks and launch, into f32 (f_rope) or binary16 (f_rope_f16) rows.
+int rope_launch(moearc_ctx *c, hipFunction_t f, void *dst, const float *src, const int *pos,
                 unsigned long n_tokens, unsigned long n_heads, unsigned long head_dim,
                 unsigned long n_dims, float freq_base, float freq_scale, float ext_factor,
                 float attn_factor, float corr_lo, float corr_hi, int neox) {
@@ -695,7 +701,7 @@ int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
     const uint64_t groups = (n_heads + ROPE_HEADS - 1) / ROPE_HEADS;
     if (threads / 256 >= 0xFFFFFFFFull || groups > 65535) return ERR_ARG;
     struct {
-        float *dst;
+        void *dst;
         const float *src;
         const int *pos;
         uint64_t n_tokens;
@@ -703,8 +709,21 @@ int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
         RopeParams r;
     } a{dst, src, pos, n_tokens, (uint32_t) n_heads, (uint32_t) head_dim,
         rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox)};
-    return launch2d(c, c->f_rope, (unsigned) ((threads + 255) / 256), (unsigned) groups, 256, a,
+    return launch2d(c, f, (unsigned) ((threads + 255) / 256), (unsigned) groups, 256, a,
                     nullptr, n_heads, head_dim, 0, "rope");
+}
+
+}  // namespace
+
+extern "C" {
+
+int moearc_rope(moearc_ctx *c, float *dst, const float *src, const int *pos,
+                unsigned long n_tokens, unsigned long n_heads, unsigned long head_dim,
+                unsigned long n_dims, float freq_base, float freq_scale, float ext_factor,
+                float attn_factor, float corr_lo, float corr_hi, int neox) {
+    if (!c) return ERR;
+    return rope_launch(c, c->f_rope, dst, src, pos, n_tokens, n_heads, head_dim, n_dims, freq_base, freq_scale,
+                       ext_factor, attn_factor, corr_lo, corr_hi, neox);
 }
 
 int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, const float *k,
@@ -1537,13 +1556,13 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
             if (const int rc = mv_launch_all(c, b->w_type[i], jobs, E, "attn_qkv_chunk")) return rc;
         }
     }
-    // RoPE of q (narrowed to f16 for the prefill kernel when there is a chunk); RoPE of K fused
-    // with the K/V append
-    if (const int rc = moearc_rope(c, qr, q, pos, n_tok, H, D, b->n_rot, b->freq_base, b->freq_scale,
-                                   b->ext_factor, b->attn_factor, b->corr_lo, b->corr_hi, 1))
+    // RoPE of q (written as f16 for the prefill kernel when there is a chunk: the values
+    // moearc_quantize_f16 would make of the f32 rotation); RoPE of K fused with the K/V append
+    const bool chunk = n_tok > 1;
+    if (const int rc = rope_launch(c, chunk ? c->f_rope_f16 : c->f_rope, chunk ? (void *) q16 : (void *) qr, q,
+                                   pos, n_tok, H, D, b->n_rot, b->freq_base, b->freq_scale, b->ext_factor,
+                                   b->attn_factor, b->corr_lo, b->corr_hi, 1))
         return rc;
-    if (n_tok > 1)
-        if (const int rc = moearc_quantize_f16(c, q16, qr, nq)) return rc;
     if (const int rc = moearc_rope_kv_append_chunk(c, b->k_pages, b->v_pages, k, v, pos, page_ids, slots,
                                                    n_tok, G, D, b->page_tokens, b->n_rot, b->freq_base,
                                                    b->freq_scale, b->ext_factor, b->attn_factor,
