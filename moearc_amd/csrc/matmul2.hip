@@ -94,13 +94,22 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         const uint64_t tg = min(t0 + tok, a.n_tok - 1u);
         dma_src[i] = ((R >> 3) ? a.xl : a.xh) + tg * a.cols + 32u * kb0 + 8u * c;
     }
+    // The copies are issued as asm (m0 saved and restored, memory clobbered), out of the compiler's
+    // wait bookkeeping: with LDS-DMA operations in flight it cannot count the weight loads' waits
+    // and drains every memory operation (vmcnt(0)) before each step's MFMAs -- the requests just
+    // made for two blocks ahead included. The step's leading wait covers the copies; the compiler
+    // counts its own weight loads (copies issued between them only make its waits longer).
     auto dma = [&](uint32_t b, uint32_t buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t R = 4u * wave + (uint32_t) i;
-            __builtin_amdgcn_global_load_lds(
-                (const void *) (dma_src[i] + 32u * b),
-                (__attribute__((address_space(3))) void *) (tiles + buf * MM2_BUF + R * 1024u), 16, 0, 0);
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(lds0 + buf * MM2_BUF + R * 1024u);
+            uint32_t m0_saved;
+            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                         "global_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                         : "=&s"(m0_saved)
+                         : "s"(lds), "v"(dma_src[i] + 32u * b)
+                         : "memory");
         }
     };
 
