@@ -1283,6 +1283,9 @@ struct MmReduceLaunch {
     uint32_t n_slices;
     uint32_t pad;
 };
+// moearc_matmul_reduce_k(MatmulArgs a, uint32_t n_slices): the count follows the struct directly
+static_assert(offsetof(MmReduceLaunch, n_slices) == sizeof(MatmulArgs), "reduce kernel argument layout");
+static_assert(sizeof(MatmulArgs) % 8 == 0, "MatmulArgs is passed by value as 8-byte aligned kernel arguments");
 
 // Chunk-product formats: index into f_mm, or -1.
 int mm_index(unsigned ty) {
