@@ -9,6 +9,10 @@
 // The product is computed transposed, D[token][row] = X . W^T, so that the weight rows are the MFMA's
 // N side: lane l holds D column l % 32 -- one weight row -- in all 16 of its accumulators, and a
 // Q8_0 block scale is one per-lane multiplier (it is also the lane that loaded that row's block).
+// Within a 32-wide k-block, lane (n, h) (h = l >> 5) feeds k 16h + 8s .. + 7 to the MFMA of k
+// slice s, for both operands: its weight bytes for the block are then one contiguous 16-byte
+// piece (a single load per row tile; the weight loads touch one cache line per row and lane pair
+// per instruction, and the fewer such instructions per step, the faster the step).
 //
 // Work-group: 4 waves over 128 tokens x 128 weight rows; wave w takes tokens 64 (w & 1) .. + 63 and
 // rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. Per 32-wide k-block the work-group's
@@ -27,8 +31,8 @@ constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group
 constexpr uint32_t MM2_HALF = MM2_TOK * 64u;  // bytes of one half (hi or lo) of an activation tile
 constexpr uint32_t MM2_BUF = 2u * MM2_HALF;   // one k-block's activation tile
 constexpr uint32_t MM2_NBUF = 3u;
-// fewest memory instructions one block's weight loads compile to (two row tiles x two k slices of
-// 8 int8 or 8 halves, which no load can merge: Q8_0 adds the scales)
+// fewest memory instructions one block's weight loads compile to (Q8_0: per row tile 16 int8 and
+// the scale; F16: per row tile two 16-byte pieces of 8 halves)
 constexpr uint32_t MM2_WLOADS = 4u;
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
@@ -61,8 +65,8 @@ __device__ __forceinline__ half8_t mm2_i8_to_f16(mm2_u32x2 q) {
 template <uint32_t TY>
 struct Mm2W;  // one k-block of this lane's weight operands, raw
 template <>
-struct Mm2W<8> {  // Q8_0: per row tile and k slice 8 int8; the block's d
-    mm2_u32x2 q[2][2];
+struct Mm2W<8> {  // Q8_0: per row tile this lane's 16 int8 (k 16h .. 16h + 15); the block's d
+    u32x4_t q[2];
     uint16_t d[2];
 };
 template <>
@@ -125,12 +129,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
             if constexpr (TY == 8) {
                 const uint8_t *blk = wrow[rt] + 34u * b;
                 o.d[rt] = *(const uint16_t *) blk;
-#pragma unroll
-                for (int s = 0; s < 2; ++s) __builtin_memcpy(&o.q[rt][s], blk + 2u + 16u * s + 8u * h, 8);
+                __builtin_memcpy(&o.q[rt], blk + 2u + 16u * h, 16);
             } else {
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
-                    o.h[rt][s] = *(const u32x4_t *) (wrow[rt] + 2u * (32u * b + 16u * s + 8u * h));
+                    o.h[rt][s] = *(const u32x4_t *) (wrow[rt] + 2u * (32u * b + 16u * h + 8u * s));
             }
         }
     };
@@ -143,14 +146,14 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) acc[tt][rt][j] = 0.f;
 
-    // A operand (activations) of token tile tt, k slice s: token 64 (w & 1) + 32 tt + n, chunk 2 s + h
+    // A operand (activations) of token tile tt, k slice s: token 64 (w & 1) + 32 tt + n, chunk 2 h + s
     uint32_t aoff[2][2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const uint32_t tok = 64u * (wave & 1u) + 32u * tt + n;
-            aoff[tt][s] = lds0 + tok * 64u + 16u * ((2u * s + h) ^ mm2_swz(tok));
+            aoff[tt][s] = lds0 + tok * 64u + 16u * ((2u * h + s) ^ mm2_swz(tok));
         }
     auto compute = [&](uint32_t buf, const Mm2W<TY> &o) {
         half8_t ah[2][2], al[2][2];
@@ -168,7 +171,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
             half8_t bw[2];
             if constexpr (TY == 8) {
 #pragma unroll
-                for (int s = 0; s < 2; ++s) bw[s] = mm2_i8_to_f16(o.q[rt][s]);
+                for (int s = 0; s < 2; ++s) bw[s] = mm2_i8_to_f16(mm2_u32x2{o.q[rt][2 * s], o.q[rt][2 * s + 1]});
             } else {
 #pragma unroll
                 for (int s = 0; s < 2; ++s) bw[s] = __builtin_bit_cast(half8_t, o.h[rt][s]);
