@@ -8,32 +8,42 @@
 //
 // The product is computed transposed, D[token][row] = X . W^T, so that the weight rows are the MFMA's
 // N side: lane l holds D column l % 32 -- one weight row -- in all 16 of its accumulators, and a
-// Q8_0 block scale is one per-lane multiplier (it is also the lane that loaded that row's block).
-// Within a 32-wide k-block, lane (n, h) (h = l >> 5) feeds k 16h + 8s .. + 7 to the MFMA of k
-// slice s, for both operands: its weight bytes for the block are then one contiguous 16-byte
-// piece (a single load per row tile; the weight loads touch one cache line per row and lane pair
-// per instruction, and the fewer such instructions per step, the faster the step).
+// Q8_0 block scale is one per-lane multiplier. Within a 32-wide k-block, lane (n, h) (h = l >> 5)
+// feeds k 16h + 8s .. + 7 to the MFMA of k slice s, for both operands.
 //
 // Work-group: 4 waves over 128 tokens x 128 weight rows; wave w takes tokens 64 (w & 1) .. + 63 and
-// rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. Per 32-wide k-block the work-group's
-// activation tile (128 tokens x 32 k, hi and lo: 16 KiB) arrives in LDS by LDS DMA
-// (global_load_lds_dwordx4, 16 bytes per lane at the wave's base + 16 lane), three buffers, two
-// k-blocks ahead; each wave loads its own weight rows into registers, also two k-blocks ahead. One
-// barrier per k-block. LDS layout per half: token t's 64-byte row holds 16-byte chunk c (k 8c..8c+7)
-// at position c ^ swz(t), swz(t) = ((t >> 2) + 2 (t >> 4)) & 3, so that every 16-lane group of an
-// operand read (tokens t..t+15, or t..t+7 and t+16..t+23, one chunk) touches 64 distinct banks.
+// rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. Both operands reach LDS by LDS DMA
+// (global_load_lds_dwordx4: 16 bytes per lane, written at the instruction's LDS base + 16 lane),
+// two k-blocks ahead, and are read from there in operand layout; one barrier per k-block. Every
+// copy reads 64-byte row pieces, four lanes per row: a memory instruction costs in proportion to
+// the cache lines it touches, and loading weights straight into operand layout touches one line
+// per row for 16 useful bytes (measured: that form spends a third of the product's time there).
+// - Activations: per k-block 128 tokens x 32 k, hi and lo (16 KiB); three buffers. Token t's
+//   64-byte row holds 16-byte chunk c (k 8c .. 8c + 7) at position c ^ swz(t), swz(t) = ((t >> 2)
+//   + 2 (t >> 4)) & 3, so that every 16-lane group of an operand read (16 tokens, one chunk)
+//   touches 64 distinct banks.
+// - F16 weights: per k-block 128 rows x 64 bytes in the same layout, beside each activation tile.
+// - Q8_0 weights, per pair of k-blocks: a row's 68 bytes (d0, q0[32], d1, q1[32]) as four 16-byte
+//   chunks (bytes 0 .. 63, same layout) plus a 4-byte tail array (bytes 64 .. 67); three pair
+//   buffers. Lane (n, h) takes its 16 payload bytes of block 0 from chunk h and the first dword of
+//   chunk h + 1 (window bytes 2 + 16h ..: one v_alignbyte per dword), those of block 1 from chunk
+//   h + 2 and the first dword of chunk 3 or the tail (dword-aligned), and the scales from the first
+//   dwords of chunks 0 and 2. So a slice of the reduction starts on an even k-block and the rows
+//   hold an even number of blocks (the host sends other Q8_0 shapes to matmul.hip).
 #include "common.h"
 
 namespace {
 
 constexpr uint32_t MM2_TOK = 128;   // tokens per work-group
 constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group
-constexpr uint32_t MM2_HALF = MM2_TOK * 64u;  // bytes of one half (hi or lo) of an activation tile
-constexpr uint32_t MM2_BUF = 2u * MM2_HALF;   // one k-block's activation tile
+constexpr uint32_t MM2_HALF = MM2_TOK * 64u;    // bytes of one half (hi or lo) of an activation tile
+constexpr uint32_t MM2_ACT = 2u * MM2_HALF;     // one k-block's activation tile
 constexpr uint32_t MM2_NBUF = 3u;
-// fewest memory instructions one block's weight loads compile to (Q8_0: per row tile 16 int8 and
-// the scale; F16: per row tile two 16-byte pieces of 8 halves)
-constexpr uint32_t MM2_WLOADS = 4u;
+// Q8_0 pair buffer: the rows' 64-byte pieces, their tails (rows 0 .. 63 from wave 0, 64 .. 127 from
+// wave 1), and 512 bytes that waves 2 and 3 fill with the same tails (so every wave issues the same
+// copies; nothing reads them)
+constexpr uint32_t MM2_QTAIL = MM2_ROWS * 64u;
+constexpr uint32_t MM2_QPAIR = MM2_QTAIL + 4u * 256u;
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
@@ -62,80 +72,98 @@ __device__ __forceinline__ half8_t mm2_i8_to_f16(mm2_u32x2 q) {
     return r;
 }
 
-template <uint32_t TY>
-struct Mm2W;  // one k-block of this lane's weight operands, raw
-template <>
-struct Mm2W<8> {  // Q8_0: per row tile this lane's 16 int8 (k 16h .. 16h + 15); the block's d
-    u32x4_t q[2];
-    uint16_t d[2];
-};
-template <>
-struct Mm2W<1> {  // F16: per row tile and k slice 8 halves
-    u32x4_t h[2][2];
-};
+// LDS-DMA copies of 16 (or 4) bytes per lane from src to LDS byte lds + 16 lane (4 lane). Issued as
+// asm (m0 saved and restored, memory clobbered), out of the compiler's wait bookkeeping: with such
+// copies in flight it would drain every memory operation (vmcnt(0)) before each step's LDS reads,
+// the copies just requested for two blocks ahead included. The step's leading wait covers them.
+__device__ __forceinline__ void mm2_copy16(uint32_t lds, const void *src) {
+    uint32_t m0_saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(m0_saved)
+                 : "s"(lds), "v"(src)
+                 : "memory");
+}
+__device__ __forceinline__ void mm2_copy4(uint32_t lds, const void *src) {
+    uint32_t m0_saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(m0_saved)
+                 : "s"(lds), "v"(src)
+                 : "memory");
+}
+
+__device__ __forceinline__ u32x4_t mm2_lds16(uint32_t off) {
+    return *(const __attribute__((address_space(3))) u32x4_t *) (uintptr_t) off;
+}
+__device__ __forceinline__ uint32_t mm2_lds4(uint32_t off) {
+    return *(const __attribute__((address_space(3))) uint32_t *) (uintptr_t) off;
+}
 
 template <uint32_t TY>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t tiles[MM2_NBUF * MM2_BUF];
+    constexpr bool Q8 = TY == 8;
+    // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair buffers
+    constexpr uint32_t BUF = MM2_ACT + (Q8 ? 0u : MM2_ROWS * 64u);
+    constexpr uint32_t QBASE = MM2_NBUF * BUF;
+    __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + (Q8 ? MM2_NBUF * MM2_QPAIR : 0u)];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31u, h = lane >> 5;
     const MmSegView sg = mm_seg(a, blockIdx.x);
     const uint32_t t0 = blockIdx.y * MM2_TOK, r0 = sg.tile * MM2_ROWS;
-    // this work-group's k-slice: blocks kb0 .. kb0 + nb
+    // this work-group's k-slice: blocks kb0 .. kb0 + nb (Q8_0: both even)
     const uint32_t kb0 = blockIdx.z * a.kb_per, nb = min(a.kb_per, a.cols / 32u - kb0);
-    const uint32_t lds0 = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles;
+    const uint32_t lds0 =
+        __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles);
 
-    // LDS DMA: instruction i of wave w fills region R = 4 w + i (1 KiB): half R >> 3, tokens
-    // 16 (R & 7) .. + 15; lane L writes slot L of the region = chunk position L & 3 of token L >> 2,
-    // which holds chunk (L & 3) ^ swz(token).
-    const uint16_t *dma_src[4];
+    // Activation copies: instruction i of wave w fills region R = 4 w + i (1 KiB): half R >> 3,
+    // tokens 16 (R & 7) .. + 15; lane L writes slot L of the region = chunk position L & 3 of token
+    // L >> 2, which holds chunk (L & 3) ^ swz(token).
+    const uint16_t *xsrc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t R = 4u * wave + (uint32_t) i;
         const uint32_t tok = 16u * (R & 7u) + (lane >> 2);
         const uint32_t c = (lane & 3u) ^ mm2_swz(tok);
         const uint64_t tg = min(t0 + tok, a.n_tok - 1u);
-        dma_src[i] = ((R >> 3) ? a.xl : a.xh) + tg * a.cols + 32u * kb0 + 8u * c;
+        xsrc[i] = ((R >> 3) ? a.xl : a.xh) + tg * a.cols + 32u * kb0 + 8u * c;
     }
-    // The copies are issued as asm (m0 saved and restored, memory clobbered), out of the compiler's
-    // wait bookkeeping: with LDS-DMA operations in flight it cannot count the weight loads' waits
-    // and drains every memory operation (vmcnt(0)) before each step's MFMAs -- the requests just
-    // made for two blocks ahead included. The step's leading wait covers the copies; the compiler
-    // counts its own weight loads (copies issued between them only make its waits longer).
-    auto dma = [&](uint32_t b, uint32_t buf) {
+    // Weight copies: instruction i of wave w fills rows 16 (2 w + i) .. + 15 of the 64-byte pieces
+    // (F16: one k-block; Q8_0: bytes 0 .. 63 of a pair), lane L row 16 (2 w + i) + (L >> 2), whose
+    // position L & 3 holds chunk (L & 3) ^ swz(row); Q8_0: wave w also copies the tails of rows
+    // 64 (w & 1) .. + 63 (lane L: row 64 (w & 1) + L). Rows past the last copy the last row (not stored).
+    constexpr uint32_t wbb = Q8 ? 34u : 64u;  // bytes of a row per k-block
+    const uint8_t *wsrc[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t R = 4u * wave + (uint32_t) i;
-            const uint32_t lds = __builtin_amdgcn_readfirstlane(lds0 + buf * MM2_BUF + R * 1024u);
-            uint32_t m0_saved;
-            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
-                         "global_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
-                         : "=&s"(m0_saved)
-                         : "s"(lds), "v"(dma_src[i] + 32u * b)
-                         : "memory");
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t rl = 16u * (2u * wave + (uint32_t) i) + (lane >> 2);
+        wsrc[i] = sg.w + (uint64_t) min(r0 + rl, sg.rows - 1u) * sg.row_bytes + wbb * (uint64_t) kb0 +
+                  16u * ((lane & 3u) ^ mm2_swz(rl));
+    }
+    const uint8_t *wtail =
+        sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes + 34u * (uint64_t) kb0 + 64u;
+
+    // block b's activations (F16: and weights) into buffer buf
+    auto copy = [&](uint32_t b, uint32_t buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + buf * BUF + (4u * wave + (uint32_t) i) * 1024u),
+                       xsrc[i] + 32u * b);
+        if constexpr (!Q8) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + buf * BUF + MM2_ACT + (2u * wave + (uint32_t) i) * 1024u),
+                           wsrc[i] + 64u * b);
         }
     };
-
-    // this lane's weight rows (clamped: lanes past the last row load row rows - 1 and store nothing)
-    const uint8_t *wrow[2];
+    // Q8_0: the weights of blocks b, b + 1 (b even) into pair buffer qb
+    auto qcopy = [&](uint32_t b, uint32_t qb) {
+        const uint32_t base = lds0 + QBASE + qb * MM2_QPAIR;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-        wrow[rt] = sg.w + (uint64_t) min(r0 + 64u * (wave >> 1) + 32u * rt + n, sg.rows - 1u) * sg.row_bytes +
-                   (TY == 8 ? 34u : 64u) * (uint64_t) kb0;
-    auto wload = [&](uint32_t b, Mm2W<TY> &o) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            if constexpr (TY == 8) {
-                const uint8_t *blk = wrow[rt] + 34u * b;
-                o.d[rt] = *(const uint16_t *) blk;
-                __builtin_memcpy(&o.q[rt], blk + 2u + 16u * h, 16);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    o.h[rt][s] = *(const u32x4_t *) (wrow[rt] + 2u * (32u * b + 16u * h + 8u * s));
-            }
-        }
+        for (int i = 0; i < 2; ++i)
+            mm2_copy16(__builtin_amdgcn_readfirstlane(base + (2u * wave + (uint32_t) i) * 1024u), wsrc[i] + 34u * b);
+        mm2_copy4(__builtin_amdgcn_readfirstlane(base + MM2_QTAIL + wave * 256u), wtail + 34u * b);
     };
 
     mm2_f32x16 acc[2][2];
@@ -155,83 +183,132 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
             const uint32_t tok = 64u * (wave & 1u) + 32u * tt + n;
             aoff[tt][s] = lds0 + tok * 64u + 16u * ((2u * h + s) ^ mm2_swz(tok));
         }
-    auto compute = [&](uint32_t buf, const Mm2W<TY> &o) {
-        half8_t ah[2][2], al[2][2];
+    // B operand (weights) of row tile rt: row 64 (w >> 1) + 32 rt + n. F16 slice s: chunk 2 h + s.
+    // Q8_0 (pair buffer 0): [0] chunk h, [1] chunk h + 1, [2] chunk h + 2, [3] chunk 3 (h = 0) or the
+    // tail (h = 1), [4] chunk 0, [5] chunk 2.
+    uint32_t woff[2][Q8 ? 6 : 2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
+        const uint32_t sw = mm2_swz(rl);
+        if constexpr (Q8) {
+            const uint32_t base = lds0 + QBASE + rl * 64u;
+            woff[rt][0] = base + 16u * (h ^ sw);
+            woff[rt][1] = base + 16u * ((h + 1u) ^ sw);
+            woff[rt][2] = base + 16u * ((h + 2u) ^ sw);
+            woff[rt][3] = h ? lds0 + QBASE + MM2_QTAIL + rl * 4u : base + 16u * (3u ^ sw);
+            woff[rt][4] = base + 16u * sw;
+            woff[rt][5] = base + 16u * (2u ^ sw);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) woff[rt][s] = lds0 + MM2_ACT + rl * 64u + 16u * ((2u * h + s) ^ sw);
+        }
+    }
+
+    // block b from activation buffer buf and (Q8_0) pair buffer qb, b odd: the pair's second block
+    auto compute = [&](uint32_t buf, uint32_t qb, bool odd) {
+        half8_t ah[2][2], al[2][2], bw[2][2];
+        float d[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const uint32_t off = aoff[tt][s] + buf * MM2_BUF;
-                ah[tt][s] = __builtin_bit_cast(half8_t, *(const __attribute__((address_space(3))) u32x4_t *) (uintptr_t) off);
-                al[tt][s] = __builtin_bit_cast(half8_t,
-                                               *(const __attribute__((address_space(3))) u32x4_t *) (uintptr_t) (off + MM2_HALF));
+                const uint32_t off = aoff[tt][s] + buf * BUF;
+                ah[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off));
+                al[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off + MM2_HALF));
             }
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-            half8_t bw[2];
-            if constexpr (TY == 8) {
+            if constexpr (Q8) {
+                const uint32_t qo = qb * MM2_QPAIR;
+                u32x4_t q;
+                uint32_t dd;
+                if (!odd) {  // window bytes 2 + 16h .. 17 + 16h
+                    const u32x4_t c = mm2_lds16(woff[rt][0] + qo);
+                    const uint32_t nx = mm2_lds4(woff[rt][1] + qo);
+                    q = (u32x4_t){__builtin_amdgcn_alignbyte(c[1], c[0], 2u), __builtin_amdgcn_alignbyte(c[2], c[1], 2u),
+                                  __builtin_amdgcn_alignbyte(c[3], c[2], 2u), __builtin_amdgcn_alignbyte(nx, c[3], 2u)};
+                    dd = mm2_lds4(woff[rt][4] + qo) & 0xFFFFu;
+                } else {  // window bytes 36 + 16h .. 51 + 16h
+                    const u32x4_t c = mm2_lds16(woff[rt][2] + qo);
+                    q = (u32x4_t){c[1], c[2], c[3], mm2_lds4(woff[rt][3] + qo)};
+                    dd = mm2_lds4(woff[rt][5] + qo) >> 16;
+                }
+                d[rt] = (float) __builtin_bit_cast(_Float16, (uint16_t) dd);
 #pragma unroll
-                for (int s = 0; s < 2; ++s) bw[s] = mm2_i8_to_f16(mm2_u32x2{o.q[rt][2 * s], o.q[rt][2 * s + 1]});
+                for (int s = 0; s < 2; ++s) bw[rt][s] = mm2_i8_to_f16(mm2_u32x2{q[2 * s], q[2 * s + 1]});
             } else {
 #pragma unroll
-                for (int s = 0; s < 2; ++s) bw[s] = __builtin_bit_cast(half8_t, o.h[rt][s]);
+                for (int s = 0; s < 2; ++s) bw[rt][s] = __builtin_bit_cast(half8_t, mm2_lds16(woff[rt][s] + buf * BUF));
             }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                if constexpr (TY == 8) {
+                if constexpr (Q8) {
                     mm2_f32x16 sblk = {};
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
-                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][s], bw[s], sblk, 0, 0, 0);
-                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][s], bw[s], sblk, 0, 0, 0);
+                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][s], bw[rt][s], sblk, 0, 0, 0);
+                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][s], bw[rt][s], sblk, 0, 0, 0);
                     }
-                    const float d = (float) __builtin_bit_cast(_Float16, o.d[rt]);
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[tt][rt][j] = fmaf(d, sblk[j], acc[tt][rt][j]);
+                    for (int j = 0; j < 16; ++j) acc[tt][rt][j] = fmaf(d[rt], sblk[j], acc[tt][rt][j]);
                 } else {
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
-                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][s], bw[s], acc[tt][rt], 0, 0, 0);
-                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][s], bw[s], acc[tt][rt], 0, 0, 0);
+                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][s], bw[rt][s], acc[tt][rt], 0, 0, 0);
+                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][s], bw[rt][s], acc[tt][rt], 0, 0, 0);
                     }
                 }
             }
-        }
     };
 
-    // k-block b's activations in buffer b % 3, its weights in set b % 3. Step b: wait for block b's
-    // DMA, meet the other waves (every wave has finished block b - 1, whose buffer is refilled
-    // next), request block b + 2 (its DMA first, then its weights), compute block b. Issued after
-    // block b's DMA are its weights and block b + 1's DMA and weights: at least 2 MM2_WLOADS + 4
-    // memory operations (the weight loads of one block are at least MM2_WLOADS instructions), so
-    // waiting until that many remain leaves both blocks' requests in flight.
-    Mm2W<TY> ws[3];
-    dma(0, 0);
-    wload(0, ws[0]);
-    dma(min(1u, nb - 1u), 1);
-    wload(min(1u, nb - 1u), ws[1]);
-    auto step = [&](uint32_t b, int s) {
-        // block b's DMA has landed and every LDS read of block b - 1 has returned, in this wave;
+    // k-block b's activations in buffer b % 3 (F16: its weights beside them); Q8_0: pair b / 2 in
+    // pair buffer (b / 2) % 3. Step b: wait for block b's copies (b even, Q8_0: and its pair's), meet
+    // the other waves (every wave has finished block b - 1, whose buffers are refilled next),
+    // request block b + 2 (Q8_0, b even: and pair b + 2, b + 3), compute block b. Copies issued after
+    // block b's activations, which may stay in flight: F16, block b + 1's (6); Q8_0, b even: pair b's
+    // weights, then block b + 1's activations (4); b odd: block b + 1's activations and pair b + 1's
+    // weights (7). Past the end, the requests repeat the last block and pair into the buffers next
+    // in line, which nothing reads, so every step issues the same copies.
+    copy(0, 0);
+    if constexpr (Q8) qcopy(0, 0);
+    copy(min(1u, nb - 1u), 1);
+    auto step = [&](uint32_t b, uint32_t buf, uint32_t qb, bool odd) {
+        // block b's copies have landed and every LDS read of block b - 1 has returned, in this wave;
         // then in every wave
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(2u * MM2_WLOADS + 4u));
+        if (!Q8)
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(6u));
+        else if (odd)
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
+        else
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(4u));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t bn = min(b + 2u, nb - 1u);
-        dma(bn, (uint32_t) (s + 2) % 3u);
-        wload(bn, ws[(s + 2) % 3]);
+        copy(min(b + 2u, nb - 1u), (buf + 2u) % 3u);
+        if constexpr (Q8)
+            if (!odd) qcopy(min(b + 2u, nb - 2u), (qb + 1u) % 3u);
         __builtin_amdgcn_sched_barrier(0);
-        compute((uint32_t) s, ws[s]);
+        compute(buf, qb, odd);
     };
     uint32_t b = 0;
-    for (; b + 3u <= nb; b += 3u) {
-        step(b, 0);
-        step(b + 1u, 1);
-        step(b + 2u, 2);
+    for (; b + 6u <= nb; b += 6u) {
+        step(b, 0, 0, false);
+        step(b + 1u, 1, 0, true);
+        step(b + 2u, 2, 1, false);
+        step(b + 3u, 0, 1, true);
+        step(b + 4u, 1, 2, false);
+        step(b + 5u, 2, 2, true);
     }
-    if (b < nb) step(b, 0);
-    if (b + 1u < nb) step(b + 1u, 1);
-    __builtin_amdgcn_s_waitcnt(mm2_vmcnt(0));  // no DMA outlives the work-group
+    if (b < nb) step(b, 0, 0, false);
+    if (b + 1u < nb) step(b + 1u, 1, 0, true);
+    if (b + 2u < nb) step(b + 2u, 2, 1, false);
+    if (b + 3u < nb) step(b + 3u, 0, 1, true);
+    if (b + 4u < nb) step(b + 4u, 1, 2, false);
+    __builtin_amdgcn_s_waitcnt(mm2_vmcnt(0));  // no copy outlives the work-group
 
     // D[token][row]: lane l holds row r0 + 64 (w >> 1) + 32 rt + n, tokens 8 (j / 4) + 4 h + j % 4 of
     // tile tt -- 32 consecutive rows per store instruction

@@ -1328,12 +1328,14 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
         tiles128 += (m[i].rows + 127) / 128;
     }
     // Q8_0 and F16 over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
-    // (matmul2.hip). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
+    // (matmul2.hip; Q8_0 weights arrive there in pairs of k-blocks, so its rows must hold an even
+    // number of them). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
     // pays while the launch still has about two work-groups per CU; shorter chunks take 16.
     hipFunction_t f;
     unsigned long rows_per_tile;
     unsigned gy;
-    if ((ty == 8u || ty == 1u) && n_tok >= 64) {
+    const bool mm2 = (ty == 1u || (ty == 8u && (n_cols / 32) % 2 == 0)) && n_tok >= 64;
+    if (mm2) {
         f = c->f_mm2[ty == 8u ? 0 : 1];
         rows_per_tile = 128;
         gy = (unsigned) ((n_tok + 127) / 128);
@@ -1365,9 +1367,9 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     // shapes are 4 work-groups), so the reduction is cut into slices of at least 4 k-blocks over a
     // third grid dimension -- up to about two work-groups per CU in all -- whose sums a second
     // launch adds in slice order, with the bias and the residual. K-quant slices start on a
-    // 256-element super-block (a multiple of 8 k-blocks).
+    // 256-element super-block (a multiple of 8 k-blocks), matmul2.hip's Q8_0 slices on a pair.
     const uint64_t nb = n_cols / 32, tiles = (uint64_t) gx * gy;
-    const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : 1;
+    const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : (mm2 && ty == 8u) ? 2 : 1;
     uint64_t slices = 1, kb_per = nb;
     if (tiles <= kMmCUs && nb >= 8) {
         const uint64_t want = std::min<uint64_t>(2 * kMmCUs / tiles, nb / 4);

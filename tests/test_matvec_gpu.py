@@ -210,10 +210,13 @@ def test_matvec_refusals_and_empty_shapes(ctx):
     (QuantType.Q8_0, 2, 4096, 2880), (QuantType.F16, 129, 2880, 4096),
     # enough work-groups for the 32-rows-per-wave kernels
     (QuantType.Q8_0, 512, 8192, 256), (QuantType.F16, 256, 16384, 128),
-    # the 128 x 128-tile kernels (Q8_0 and F16 from 64 tokens): ragged tiles, k-block counts 1 to 7
-    # around the three-deep pipeline
+    # the 128 x 128-tile kernels (Q8_0 and F16 from 64 tokens): ragged tiles, k-block counts around
+    # the three-deep pipeline and its six-block unroll (Q8_0 there only with an even count: its
+    # weights travel in pairs of blocks; odd counts, as 224 and 96 columns, take the 16x16 kernels)
     (QuantType.Q8_0, 200, 300, 64), (QuantType.Q8_0, 64, 128, 224), (QuantType.F16, 100, 200, 32),
     (QuantType.Q8_0, 300, 129, 96), (QuantType.F16, 190, 257, 160),
+    (QuantType.Q8_0, 64, 128, 128), (QuantType.Q8_0, 100, 200, 192), (QuantType.Q8_0, 70, 130, 320),
+    (QuantType.Q8_0, 96, 160, 448), (QuantType.F16, 65, 136, 224), (QuantType.F16, 80, 128, 352),
     # K-quants (sub-block scales and mins) and MXFP4, both launch shapes
     (QuantType.Q4_K, 37, 200, 1024), (QuantType.Q4_K, 512, 8192, 256), (QuantType.Q5_K, 67, 96, 2048),
     (QuantType.Q5_K, 512, 8192, 256), (QuantType.MXFP4, 37, 200, 1024), (QuantType.MXFP4, 512, 8192, 96),
