@@ -19,9 +19,9 @@
 // the cache lines it touches, and loading weights straight into operand layout touches one line
 // per row for 16 useful bytes (measured: that form spends a third of the product's time there).
 // - Activations: per k-block 128 tokens x 32 k, hi and lo (16 KiB); three buffers. Token t's
-//   64-byte row holds 16-byte chunk c (k 8c .. 8c + 7) at position c ^ swz(t), swz(t) = ((t >> 2)
-//   + 2 (t >> 4)) & 3, so that every 16-lane group of an operand read (16 tokens, one chunk)
-//   touches 64 distinct banks.
+//   64-byte row holds 16-byte chunk c (k 8c .. 8c + 7) at position c ^ swz(t), swz(t) = (t >> 2)
+//   & 3: the 16-byte operand reads then measure free of bank conflicts (SQ_LDS_BANK_CONFLICT 0 in
+//   the F16 kernel; 4 cycles per read with 2 (t >> 4) added to swz, 12 with no swizzle).
 // - F16 weights: per k-block 128 rows x 64 bytes in the same layout, beside each activation tile.
 // - Q8_0 weights, per pair of k-blocks: a row's 68 bytes (d0, q0[32], d1, q1[32]) as four 16-byte
 //   chunks (bytes 0 .. 63, same layout) plus a 4-byte tail array (bytes 64 .. 67); three pair
@@ -48,7 +48,7 @@ constexpr uint32_t MM2_QPAIR = MM2_QTAIL + 4u * 256u;
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t mm2_swz(uint32_t t) { return ((t >> 2) + ((t >> 4) << 1)) & 3u; }
+__device__ __forceinline__ uint32_t mm2_swz(uint32_t t) { return (t >> 2) & 3u; }
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt <= n and nothing else; vmcnt <= n and lgkmcnt 0
 constexpr uint32_t mm2_vmcnt(uint32_t n) { return (n & 0xFu) | ((n >> 4) << 14) | (0x7u << 4) | (0xFu << 8); }
