@@ -372,24 +372,33 @@ extern "C" __global__ void moearc_matmul_reduce_k(MatmulArgs a, uint32_t n_slice
     const uint64_t n = a.part_stride;
     for (uint64_t i = (uint64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t) gridDim.x * blockDim.x) {
-        uint32_t g = 0;
-        while (g + 1u < a.n_seg && i >= a.seg[g + 1u].part_off) ++g;
-        const MatmulSeg &sg = a.seg[g];
-        const uint64_t e = i - sg.part_off;
-        const uint32_t t = (uint32_t) (e / sg.rows), r = (uint32_t) (e - (uint64_t) t * sg.rows);
-        // eight slices' loads in flight at a time, added in slice order
+        // this element's matrix, chosen by selects between the (uniform) segment fields: indexing
+        // the argument block with a per-lane value would cost a memory round trip first
+        const bool s1 = a.n_seg > 1u && i >= a.seg[1].part_off, s2 = a.n_seg > 2u && i >= a.seg[2].part_off;
+        auto pick = [&](auto f0, auto f1, auto f2) { return s2 ? f2 : s1 ? f1 : f0; };
+        const uint64_t part_off = pick(a.seg[0].part_off, a.seg[1].part_off, a.seg[2].part_off);
+        const uint32_t rows = pick(a.seg[0].rows, a.seg[1].rows, a.seg[2].rows);
+        const uint32_t y_stride = pick(a.seg[0].y_stride, a.seg[1].y_stride, a.seg[2].y_stride);
+        float *const y = pick(a.seg[0].y, a.seg[1].y, a.seg[2].y);
+        const float *const bias = pick(a.seg[0].bias, a.seg[1].bias, a.seg[2].bias);
+        const uint64_t e = i - part_off;
+        const uint32_t t = (uint32_t) (e / rows), r = (uint32_t) (e - (uint64_t) t * rows);
+        float *yp = y + (uint64_t) t * y_stride + r;
+        // the residual (when accumulating), the bias and eight slices' loads in flight at a time, added in
+        // slice order; a last group short of eight reads slice n_slices - 1 in the missing places
+        // and leaves those values out, so that every group's loads leave before its first add
+        const float prev = a.accumulate ? *yp : 0.f;
+        const float bv = bias ? bias[r] : 0.f;
         float s = 0.f;
-        uint32_t z = 0;
-        for (; z + 8u <= n_slices; z += 8u) {
+        for (uint32_t z = 0; z < n_slices; z += 8u) {
             float v[8];
 #pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) v[k] = a.part[(uint64_t) (z + k) * n + i];
+            for (uint32_t k = 0; k < 8u; ++k) v[k] = a.part[(uint64_t) min(z + k, n_slices - 1u) * n + i];
 #pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) s = (z + k == 0u) ? v[k] : s + v[k];
+            for (uint32_t k = 0; k < 8u; ++k)
+                s = z + k == 0u ? v[k] : z + k < n_slices ? s + v[k] : s;
         }
-        for (; z < n_slices; ++z) s = z == 0u ? a.part[i] : s + a.part[(uint64_t) z * n + i];
-        float *yp = sg.y + (uint64_t) t * sg.y_stride + r;
-        const float v = sg.bias ? s + sg.bias[r] : s;
-        *yp = a.accumulate ? *yp + v : v;
+        const float v = bias ? s + bv : s;
+        *yp = a.accumulate ? prev + v : v;
     }
 }

@@ -123,6 +123,7 @@ struct moearc_ctx {
     size_t blk_ws_bytes = 0;
     unsigned long mv_rpw_override = 0;  // MOEARC_MATVEC_RPW: rows per wave of the matvec launches
     unsigned mv_waves_override = 0;     // MOEARC_MATVEC_WAVES: 4 or 8 waves per work-group
+    int mm_split_wg = -1;  // MOEARC_MM_SPLIT_WG: work-groups per CU the chunk product's split-K aims at (0: none; -1: by chunk)
 };
 
 namespace {
@@ -659,6 +660,7 @@ moearc_ctx *moearc_ctx_create(void) {
             if (std::strcmp(w, kDecodeVariants[i].name) == 0) c->decode_variant_override = i;
     }
     if (const char *s = std::getenv("MOEARC_DECODE_SPLIT")) c->split_override = std::strtoul(s, nullptr, 10);
+    if (const char *s = std::getenv("MOEARC_MM_SPLIT_WG")) c->mm_split_wg = (int) std::min(8ul, std::strtoul(s, nullptr, 10));
     return c;
 }
 
@@ -1365,14 +1367,19 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     // Split-K. A tile grid of at most one work-group per CU leaves most of the device idle while
     // each work-group walks the whole reduction (a 128-token chunk's k and v projections at gpt-oss
     // shapes are 4 work-groups), so the reduction is cut into slices of at least 4 k-blocks over a
-    // third grid dimension -- up to about two work-groups per CU in all -- whose sums a second
-    // launch adds in slice order, with the bias and the residual. K-quant slices start on a
+    // third grid dimension, whose sums a second launch adds in slice order, with the bias and the
+    // residual. The slice count fills every CU at least once, aiming at one work-group per CU for
+    // chunks of one or two 128-token tiles and two above (measured on gpt-oss blocks: at 128 and 256
+    // tokens the reduction's traffic, which grows with the slices, outweighs a second work-group per
+    // CU; at 512 the reverse); MOEARC_MM_SPLIT_WG sets the aim. K-quant slices start on a
     // 256-element super-block (a multiple of 8 k-blocks), matmul2.hip's Q8_0 slices on a pair.
     const uint64_t nb = n_cols / 32, tiles = (uint64_t) gx * gy;
     const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : (mm2 && ty == 8u) ? 2 : 1;
     uint64_t slices = 1, kb_per = nb;
-    if (tiles <= kMmCUs && nb >= 8) {
-        const uint64_t want = std::min<uint64_t>(2 * kMmCUs / tiles, nb / 4);
+    const uint64_t aim = c->mm_split_wg >= 0 ? (uint64_t) c->mm_split_wg : gy <= 2 ? 1 : 2;
+    if (tiles <= kMmCUs && nb >= 8 && aim) {
+        const uint64_t fill = (kMmCUs + tiles - 1) / tiles;  // slices for one work-group on every CU
+        const uint64_t want = std::max<uint64_t>(1, std::min<uint64_t>(std::max(fill, aim * kMmCUs / tiles), nb / 4));
         kb_per = (nb + want - 1) / want;
         kb_per = (kb_per + gran - 1) / gran * gran;
         slices = (nb + kb_per - 1) / kb_per;

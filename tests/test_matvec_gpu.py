@@ -223,7 +223,7 @@ def test_matvec_refusals_and_empty_shapes(ctx):
     (QuantType.Q6_K, 37, 200, 1024), (QuantType.Q6_K, 512, 8192, 256),
     # grids of at most one work-group per CU split the reduction into k-slices (also above: every
     # case with 16 or more k-blocks and a small grid, K-quant slices on super-block bounds, a ragged
-    # last slice) -- here a 128-token chunk's output projection at gpt-oss shapes, 16 slices
+    # last slice) -- here a 128-token chunk's output projection at gpt-oss shapes (11 slices)
     (QuantType.Q8_0, 128, 2880, 4096)],
     ids=str)
 def test_chunk_matmul_meets_the_matvec_bound(ctx, ty, n_tok, rows, cols):
