@@ -16,3 +16,12 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // log2(e) in f32: exp(x) = exp2(x * log2(e)).
 #define MOEARC_LOG2E 1.4426950408889634f
+
+// A 16-byte store written through to the device-coherent level (sc1, as an agent-scope store): a
+// kernel's end then has no dirty L2 lines of it to write back, which for outputs of tens of MB is
+// microseconds of the dispatch. It pays for whole-line writes (the prefill's output rows); 4-byte
+// pieces written this way measured slower (the chunk product's epilogue: +7%), the L2 no longer
+// merging them into lines.
+__device__ __forceinline__ void store_through16(void *p, u32x4_t v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
