@@ -36,6 +36,14 @@ __device__ __forceinline__ float2_t rope_factors(const RopeParams &r, int pos, u
     return (float2_t){c * mscale, s * mscale};
 }
 
+// The rotation of one pair, (x0, x1) -> (x0 cos - x1 sin, x0 sin + x1 cos), with the roundings
+// fixed by explicit fmas: every kernel here uses this one expression, so that the fused append and
+// the separate rope + append paths agree to the bit whatever the compiler would contract.
+__device__ __forceinline__ void rope_rotate(float x0, float x1, float2_t cs, float &o0, float &o1) {
+    o0 = fmaf(x0, cs[0], -(x1 * cs[1]));
+    o1 = fmaf(x0, cs[1], x1 * cs[0]);
+}
+
 // Channels (lo, hi) handled by pair slot j of a head_dim-wide row: rotated pairs first, then the
 // pass-through channels two at a time.
 __device__ __forceinline__ void pair_channels(const RopeParams &r, uint32_t j, uint32_t &lo, uint32_t &hi) {
@@ -89,8 +97,10 @@ __device__ __forceinline__ void rope_body(void *dst, const float *src, const int
         if (h0 + i < n_heads) {
             const uint64_t o = (t * n_heads + h0 + i) * head_dim;
             if (rot) {
-                put(o + lo, x0[i] * cs[0] - x1[i] * cs[1]);
-                put(o + hi, x0[i] * cs[1] + x1[i] * cs[0]);
+                float o0, o1;
+                rope_rotate(x0[i], x1[i], cs, o0, o1);
+                put(o + lo, o0);
+                put(o + hi, o1);
             } else {
                 put(o + lo, x0[i]);
                 if (has_hi) put(o + hi, x1[i]);
@@ -149,11 +159,7 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
     if (rot) {
         const float2_t cs = rope_factors(r, p, j);
 #pragma unroll
-        for (uint32_t i = 0; i < ROPE_HEADS; ++i) {
-            const float x0 = k0[i], x1 = k1[i];
-            k0[i] = x0 * cs[0] - x1 * cs[1];
-            k1[i] = x0 * cs[1] + x1 * cs[0];
-        }
+        for (uint32_t i = 0; i < ROPE_HEADS; ++i) rope_rotate(k0[i], k1[i], cs, k0[i], k1[i]);
     }
     const uint64_t base = ((uint64_t) page * page_tokens + slot) * n_kv_heads;
 #pragma unroll
@@ -179,4 +185,61 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
             }
         }
     }
+}
+
+// The fused append for the common geometry -- NeoX pairs over all 64 channels (n_dims = head_dim =
+// 64), f16 pools, n_kv_heads dividing 16. A work-group covers 16 (token, KV head) rows, 16 /
+// n_kv_heads whole tokens; lane c of a row's 16 holds channels 4c .. 4c + 3 of K and of V (one
+// 16-byte load each: whole rows per load instruction). Pair p = 4 (c & 7) + i has its halves in
+// lanes c and c ^ 8, which trade their K values (__shfl_xor by 8; a DPP row rotation built with
+// __builtin_amdgcn_update_dpp here read element 0's register for all four elements); the cos and sin
+// of each (token, pair) are computed once per work-group into LDS (the generic kernel computes
+// them once per 4 heads). Each lane stores 8 bytes of K and of V -- a row is one 128-byte line --
+// written through to the device-coherent level. Same results as moearc_rope_kv_append_chunk_k.
+extern "C" __global__ void __launch_bounds__(256) moearc_rope_kv_append_chunk64_k(
+    uint16_t *k_pages, uint16_t *v_pages, const float *k, const float *v, const int *pos,
+    const uint32_t *page_ids, const uint32_t *slots, uint64_t n_tok, uint32_t n_kv_heads,
+    uint64_t page_tokens, RopeParams r, uint32_t *err) {
+    __shared__ float2_t cs_tab[16 * 32];
+    const uint32_t tid = threadIdx.x, c = tid & 15u;
+    const uint32_t T = 16u / n_kv_heads;  // tokens per work-group
+    const uint64_t t_first = (uint64_t) blockIdx.x * T;
+    const uint64_t row = (uint64_t) blockIdx.x * 16u + (tid >> 4);
+    const uint64_t t = row / n_kv_heads;
+    const bool live = t < n_tok;
+    // this lane's pieces and its row's destination leave before anything waits on them
+    float4_t kx = {}, vx = {};
+    uint32_t slot = 0, page = 0;
+    if (live) {
+        kx = *(const float4_t *) (k + row * 64u + 4u * c);
+        vx = *(const float4_t *) (v + row * 64u + 4u * c);
+        slot = slots[t];
+        page = page_ids[t];
+    }
+    for (uint32_t i = tid; i < T * 32u; i += 256u) {
+        const uint64_t tt = t_first + (i >> 5);
+        if (tt < n_tok) cs_tab[i] = rope_factors(r, pos[tt], i & 31u);
+    }
+    __syncthreads();
+    if (!live) return;  // whole rows leave together: the row exchange below stays within live rows
+    if (slot >= page_tokens) {
+        if (c == 0) *(volatile uint32_t *) err = 1u;
+        return;
+    }
+    const bool hi = c >= 8u;
+    const uint32_t tl = (uint32_t) (t - t_first);
+    uint32_t ko[2], vo[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float kq = __shfl_xor(kx[i], 8);  // lane c ^ 8 of the same row
+        const float2_t cs = cs_tab[tl * 32u + 4u * (c & 7u) + (uint32_t) i];
+        float o0, o1;
+        rope_rotate(hi ? kq : kx[i], hi ? kx[i] : kq, cs, o0, o1);
+        const uint32_t kb = f32_to_f16_bits(hi ? o1 : o0), vb = f32_to_f16_bits(vx[i]);
+        ko[i >> 1] = (i & 1) ? (ko[i >> 1] | (kb << 16)) : kb;
+        vo[i >> 1] = (i & 1) ? (vo[i >> 1] | (vb << 16)) : vb;
+    }
+    const uint64_t dst = (((uint64_t) page * page_tokens + slot) * n_kv_heads + (row - t * n_kv_heads)) * 64u + 4u * c;
+    store_through8(k_pages + dst, u32x2_t{ko[0], ko[1]});
+    store_through8(v_pages + dst, u32x2_t{vo[0], vo[1]});
 }

@@ -79,7 +79,7 @@ struct moearc_ctx {
     hipStream_t stream = nullptr;
     hipModule_t module = nullptr;
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
-    hipFunction_t f_rope = nullptr, f_rope_f16 = nullptr, f_rope_append_chunk = nullptr;
+    hipFunction_t f_rope = nullptr, f_rope_f16 = nullptr, f_rope_append_chunk = nullptr, f_rope_append64 = nullptr;
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[2] = {};  // split kernels (kDecodeVariants)
     hipFunction_t f_dec_merge = nullptr;
@@ -587,6 +587,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_rope, "moearc_rope_k"},
         {&c->f_rope_f16, "moearc_rope_f16_k"},
         {&c->f_rope_append_chunk, "moearc_rope_kv_append_chunk_k"},
+        {&c->f_rope_append64, "moearc_rope_kv_append_chunk64_k"},
         {&c->f_dec_general, "moearc_attn_decode_general_k"},
         {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k4w2t4"},
         {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w4t1"},
@@ -741,6 +742,27 @@ int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, con
     if (page_tokens == 0 || n_kv_heads == 0 || head_dim == 0) return ERR_ARG;
     if (n_tok == 0) return OK;
     if (head_dim > 0xFFFFFFFFul || n_kv_heads > 0xFFFFFFFFul) return ERR_ARG;
+    const RopeParams rp = rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox);
+    // NeoX over all 64 channels into f16 pools, KV heads dividing 16, rows 16-byte aligned: whole
+    // rows per lane group (moearc_rope_kv_append_chunk64_k)
+    if (kv_type == 1u && neox && head_dim == 64 && n_dims == 64 && 16 % n_kv_heads == 0 &&
+        ((uintptr_t) k | (uintptr_t) v) % 16 == 0 && ((uintptr_t) k_pages | (uintptr_t) v_pages) % 8 == 0) {
+        const uint64_t wgs = (n_tok * n_kv_heads + 15) / 16;
+        if (wgs >= 0xFFFFFFFFull) return ERR_ARG;
+        struct {
+            void *kp, *vp;
+            const float *k, *v;
+            const int *pos;
+            const uint32_t *pages, *slots;
+            uint64_t n_tok;
+            uint32_t n_kv_heads;
+            uint64_t pt;
+            RopeParams r;
+            uint32_t *err;
+        } a{k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, (uint32_t) n_kv_heads, page_tokens, rp, c->err_word};
+        c->err_armed = true;
+        return launch2d(c, c->f_rope_append64, (unsigned) wgs, 1, 256, a, "rope_kv_append_chunk", n_kv_heads, head_dim);
+    }
     const uint64_t threads = (uint64_t) n_tok * ((head_dim + 1) / 2);
     const uint64_t groups = (n_kv_heads + ROPE_HEADS - 1) / ROPE_HEADS;
     if (threads / 256 >= 0xFFFFFFFFull || groups > 65535) return ERR_ARG;
@@ -756,9 +778,7 @@ int moearc_rope_kv_append_chunk(moearc_ctx *c, void *k_pages, void *v_pages, con
         RopeParams r;
         uint32_t *err;
     } a{k_pages, v_pages, k, v, pos, page_ids, slots, n_tok, (uint32_t) n_kv_heads,
-        (uint32_t) head_dim, page_tokens, kv_type,
-        rope_params(n_dims, freq_base, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi, neox),
-        c->err_word};
+        (uint32_t) head_dim, page_tokens, kv_type, rp, c->err_word};
     c->err_armed = true;
     return launch2d(c, c->f_rope_append_chunk, (unsigned) ((threads + 255) / 256), (unsigned) groups,
                     256, a, "rope_kv_append_chunk", n_kv_heads, head_dim);

@@ -96,9 +96,14 @@ def _chunk(n_tok, G, D, pt, seed):
     return k, v, pos, pages, slots, n_pages
 
 
-@pytest.mark.parametrize("pt,kv", [(256, KvType.F16), (16, KvType.F16), (32, KvType.F32)])
-def test_fused_append_equals_rope_then_append(ctx, pt, kv):
-    n_tok, G, D = 300, 8, 64
+# f16 pools with NeoX over all 64 channels and KV heads dividing 16 take the whole-row kernel
+# (moearc_rope_kv_append_chunk64_k: 16 / G tokens per work-group, G = 1 and 16 its extremes, 300
+# tokens leaving the last work-group part empty for G = 1); G = 3 and f32 pools the general one
+@pytest.mark.parametrize("pt,kv,G", [(256, KvType.F16, 8), (16, KvType.F16, 8), (32, KvType.F32, 8),
+                                     (16, KvType.F16, 1), (256, KvType.F16, 16), (16, KvType.F16, 3)],
+                         ids=str)
+def test_fused_append_equals_rope_then_append(ctx, pt, kv, G):
+    n_tok, D = 300, 64
     k, v, pos, pages, slots, n_pages = _chunk(n_tok, G, D, pt, 0x40 + pt)
     el = 2 if kv == KvType.F16 else 4
     nbytes = n_pages * pt * G * D * el
