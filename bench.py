@@ -18,9 +18,13 @@ there is no model).
   in flight, over the same rotating copies and graph replay): what reading the call's bytes alone
   costs on this device; decode_frac_of_floor = its time over the decode call's.
 * configs: BASELINE configs 1, 3 (SWA-128 and full) and 5, timed the same way.
-* prefill: BASELINE config 4 (2048 new + 2048 cached tokens), full causal and SWA-128, MFMA
-  utilisation = algorithmic flops / time / 2.5 PFLOP/s (dense f16); also as top-level keys.
-* rope_kv_append_chunk: the fused RoPE-K + f16 K/V append of the same config-4 chunk.
+* prefill: BASELINE config 4 (2048 new + 2048 cached tokens), full causal and SWA-128, timed as
+  the decode (8 calls in one graph, replayed REPS times, the median per call); MFMA utilisation =
+  algorithmic flops / time / 2.5 PFLOP/s (dense f16), SWA-128 also against max(bytes / 8 TB/s,
+  flops / 2.5 PF); also as top-level keys. Beside it: per-call HIP-event timing (us_events) and
+  the committed trace's kernel duration (us_trace, profiles/prefill_c4_kernel_trace.md).
+* rope_kv_append_chunk: the fused RoPE-K + f16 K/V append of the same config-4 chunk, timed by
+  graph replay (24 calls over 24 input sets), with event timing and the committed trace beside it.
 * launch_overhead: moearc_amd/launch_overhead (examples/launch_overhead.rs:21-125 over the C ABI).
 * cpu_baseline: the CPU oracle (a C restatement of the reference's f64 CPU twin,
   reference.rs:821-873, plus the sink) timed on this host on a bounded sample of the same decode,
@@ -209,6 +213,11 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
         result["out"] = graph_out
         del dks, dvs
         result["read_floor"] = bench_read_floor(ctx, hip, steps, warmup)
+        # the prefill before the MFMA-heavy chunk products: its full-causal kernel is power-limited,
+        # and right after them it measures ~15% slower
+        if not skip_prefill:
+            result["prefill_graph"] = bench_prefill_graph(ctx, hip)
+            result["rope_graph"] = bench_rope_append_graph(ctx, hip)
         result["configs"] = bench_configs(ctx, hip, steps, warmup)
         result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
         result["block_chunk"] = bench_block(ctx, hip)
@@ -234,7 +243,9 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
             result["events"] = {k: v[0] / v[1] / 1e3 for k, v in rep.items()}
             del dks, dvs
             if not skip_prefill:
-                result["prefill"] = bench_prefill(ctx, steps=max(5, steps // 5), warmup=3)
+                result["prefill"] = bench_prefill(ctx, steps=max(5, steps // 5), warmup=3,
+                                                  graph=result.get("prefill_graph"),
+                                                  rope_graph=result.get("rope_graph"))
     finally:
         os.environ.pop("MOEARC_PROFILE_KERNELS", None)
 
@@ -290,16 +301,40 @@ def launch_overhead():
     return json.loads(res.stdout.strip().splitlines()[-1])
 
 
-def bench_prefill(ctx, steps, warmup):
-    import fixtures as fx  # tests/fixtures.py: the same seeded prefill inputs the parity tests use
-    from moearc_amd import KvType, OUT_F16
+def prefill_inputs(ctx, copies=4):
+    """Config-4 prefill inputs (tests/fixtures.py: the same seeded case the parity tests use), in
+    `copies` independent sets of q, K and V."""
+    import fixtures as fx
     pc = fx.prefill_case(0xC4, n_q=PF_NQ, pos0=PF_POS0, pt=PT)
-    copies = 4
     dks = [ctx.upload(pc.k_raw) for _ in range(copies)]
     dvs = [ctx.upload(pc.v_raw) for _ in range(copies)]
     dqs = [ctx.upload(np.ascontiguousarray(pc.qp).view(np.uint16)) for _ in range(copies)]
-    dbt, ds = ctx.upload(pc.bt), ctx.upload(pc.sinks)
-    dout = ctx.alloc(PF_NQ * H * D * 2)
+    return dks, dvs, dqs, ctx.upload(pc.bt), ctx.upload(pc.sinks), ctx.alloc(PF_NQ * H * D * 2)
+
+
+def bench_prefill_graph(ctx, hip, calls=8, warmup=3):
+    """Both config-4 layers timed as the decode is: `calls` calls (rotating over 4 input sets)
+    captured in one graph and replayed REPS times; per-call µs statistics, the first replay
+    discarded. Close to the kernel's own duration (one dispatch gap per call)."""
+    from moearc_amd import KvType, OUT_F16
+    dks, dvs, dqs, dbt, ds, dout = prefill_inputs(ctx)
+    out = {}
+    for name, n_swa in (("full", 0), ("swa128", 128)):
+        def call(i, n_swa=n_swa):
+            ctx.attn_prefill(dout, dqs[i % 4], dks[i % 4], dvs[i % 4], dbt, ds, PF_NQ, PF_POS0, n_swa,
+                             H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+        out[name] = rep_stats(graph_timed(hip, ctx, call, calls, warmup))
+    return out
+
+
+def bench_prefill(ctx, steps, warmup, graph=None, rope_graph=None):
+    """Config-4 prefill: per-call HIP-event timing (eager, under the reference's key), and -- when
+    `graph` holds bench_prefill_graph's statistics -- the headline from the graph replay, with the
+    committed trace's kernel duration under the same replay beside it (us_trace)."""
+    from moearc_amd import KvType, OUT_F16
+    dks, dvs, dqs, dbt, ds, dout = prefill_inputs(ctx)
+    copies = len(dks)
+    trace_path = os.path.join(ROOT, "profiles", "prefill_c4_kernel_trace.md")
     out = {}
     for name, n_swa in (("full", 0), ("swa128", 128)):
         for i in range(warmup + steps):
@@ -310,18 +345,30 @@ def bench_prefill(ctx, steps, warmup):
                              PF_POS0, n_swa, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
         ctx.sync()
         rep = ctx.profile_events_report()
-        us = rep["attn_prefill r64 m64"][0] / rep["attn_prefill r64 m64"][1] / 1e3
+        us_events = rep["attn_prefill r64 m64"][0] / rep["attn_prefill r64 m64"][1] / 1e3
+        us = graph[name]["median"] if graph else us_events
         flops = PF_FLOPS_FULL if n_swa == 0 else PF_FLOPS_SWA
+        bound_us = max(PF_BYTES_SWA / (HBM_PEAK_GBS * 1e3), flops / (MFMA_F16_PEAK_TFLOPS * 1e6))
+
+        def fracs(t):
+            f = {"mfma_util": round(flops / t / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
+            if n_swa:
+                f["roofline_frac"] = round(bound_us / t, 4)
+            return f
         tflops = flops / us / 1e6
-        entry = {"us": round(us, 2), "tflops": round(tflops, 1),
-                 "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                 "tokens_per_s": round(PF_NQ * 1e6 / us, 0)}
+        entry = {"us": round(us, 2), "timing": "graph replay, median per call" if graph else "HIP events",
+                 "tflops": round(tflops, 1), **fracs(us), "tokens_per_s": round(PF_NQ * 1e6 / us, 0),
+                 "us_events": round(us_events, 2)}
+        if graph:
+            entry["us_reps"] = graph[name]
         if n_swa:
-            gbs = PF_BYTES_SWA / us / 1e3
-            bound_us = max(PF_BYTES_SWA / (HBM_PEAK_GBS * 1e3), flops / (MFMA_F16_PEAK_TFLOPS * 1e6))
-            entry.update({"hbm_gbs": round(gbs, 0), "roofline_frac": round(bound_us / us, 4)})
+            entry["hbm_gbs"] = round(PF_BYTES_SWA / us / 1e3, 0)
+        tr = summary_value(trace_path, f"{name}_us_trace_graph")
+        if tr:
+            entry["us_trace"] = tr
+            entry.update({k + "_trace": v for k, v in fracs(tr).items()})
         out[name] = entry
-    out["rope_kv_append_chunk"] = bench_rope_append(ctx, steps, warmup)
+    out["rope_kv_append_chunk"] = bench_rope_append(ctx, steps, warmup, rope_graph)
     return out
 
 
@@ -356,8 +403,17 @@ def rope_append_launch(ctx, sets, meta, i):
 RA_BYTES = PF_NQ * G * D * (4 + 4 + 2 + 2) + PF_NQ * 12
 
 
-def bench_rope_append(ctx, steps, warmup):
-    """The fused RoPE-K + f16 K/V append (HBM-bound) timed with the library's events."""
+def bench_rope_append_graph(ctx, hip):
+    """The fused RoPE-K + f16 K/V append: 24 calls over 24 input sets in one graph, replayed REPS
+    times; per-call µs statistics, the first replay discarded."""
+    sets, meta = rope_append_inputs(ctx, 24)
+    return rep_stats(graph_timed(hip, ctx, lambda i: rope_append_launch(ctx, sets, meta, i), 24, 3))
+
+
+def bench_rope_append(ctx, steps, warmup, graph=None):
+    """The fused RoPE-K + f16 K/V append (HBM-bound): the library's per-call event timing and, when
+    `graph` holds bench_rope_append_graph's statistics, the headline from the graph replay; the
+    committed trace's kernel duration beside them."""
     sets, meta = rope_append_inputs(ctx, 24)
     for i in range(warmup + steps):
         if i == warmup:
@@ -367,10 +423,20 @@ def bench_rope_append(ctx, steps, warmup):
     ctx.sync()
     rep = ctx.profile_events_report()
     key = [k2 for k2 in rep if k2.startswith("rope_kv_append_chunk")][0]
-    us = rep[key][0] / rep[key][1] / 1e3
+    us_events = rep[key][0] / rep[key][1] / 1e3
+    out = {"bytes": RA_BYTES, "us_events": round(us_events, 2)}
+    us = us_events
+    if graph:
+        us = graph["median"]
+        out["us_reps"] = graph
     gbs = RA_BYTES / us / 1e3
-    return {"us": round(us, 2), "bytes": RA_BYTES, "hbm_gbs": round(gbs, 0),
-            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    out.update({"us": round(us, 2), "timing": "graph replay, median per call" if graph else "HIP events",
+                "hbm_gbs": round(gbs, 0), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)})
+    tr = summary_value(os.path.join(ROOT, "profiles", "rope_append_c4_kernel_trace.md"), "rope_append_us_trace")
+    if tr:
+        out["us_trace"] = tr
+        out["roofline_frac_trace"] = round(RA_BYTES / tr / 1e3 / HBM_PEAK_GBS, 4)
+    return out
 
 
 # The attention projections either side of the path, at gpt-oss-20b's shapes (2880-wide residual,
@@ -676,7 +742,8 @@ def bench_configs(ctx, hip, steps, warmup):
 
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
-    decode_graph (the main line's timed region: C2 steps in one graph, replayed), decode (C2), prefill (C4 full then SWA-128), rope_append (the fused RoPE-K + K/V append of one
+    decode_graph (the main line's timed region: C2 steps in one graph, replayed), decode (C2), prefill (C4 full then SWA-128),
+    prefill_graph (the main line's prefill timing: each layer 8 calls per graph, replayed), rope_append (the fused RoPE-K + K/V append of one
     C4 chunk), matvec (the projection cases of MV_CASES, in order), matmul (MM_CASES, each as
     a graph of `steps` launches, replayed twice), block (`steps` rounds of bench_block: the 128-token
     attention block as one chunked call and as single-token calls), read_floor (the calibration read of C2's 64 MiB of
@@ -706,6 +773,10 @@ def only(what, steps, warmup):
             for i in range(warmup + steps):
                 ctx.attn_decode_batched(dout, dq, dks[i % COPIES], dvs[i % COPIES], dbt, N_KV // PT,
                                         kb, nk, ds, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+        elif what == "prefill_graph":
+            # the prefill's timed region in the main line: both layers, 8 calls per graph, replayed
+            r = bench_prefill_graph(ctx, Hip())
+            print("graph replay: " + ", ".join(f"{k} {v['median']:.2f} us" for k, v in r.items()), flush=True)
         elif what == "prefill":
             import fixtures as fx
             pc = fx.prefill_case(0xC4, n_q=PF_NQ, pos0=PF_POS0, pt=PT)
@@ -758,7 +829,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "rope_append", "matvec", "matmul",
+    ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "prefill_graph", "rope_append", "matvec", "matmul",
                                        "block", "read_floor", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
