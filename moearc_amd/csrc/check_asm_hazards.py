@@ -21,7 +21,12 @@ N + 1 for `s_nop N`):
   6. the VALU wait states hipcc itself inserts for gfx950 (seen in its output for plain HIP code):
      a VALU result is not read by v_readfirstlane / v_readlane within 1 wait state, a transcendental
      result (v_exp_f32 and the like) not by another VALU instruction within 1, and an SGPR written by
-     v_readfirstlane / v_readlane not read by a VALU instruction within 2.
+     v_readfirstlane / v_readlane not read by a VALU instruction within 2;
+  7. the data registers of a vector-memory store of more than 8 bytes (dwordx3 / dwordx4) are not
+     written by the next instruction: the store reads them after issue and needs 1 wait state
+     (hipcc inserts it after its own stores, not after an inline-asm store -- a 16-byte asm store
+     followed at once by a VALU write of its data stored the new value) -- in every kernel of the
+     code object.
 
 Usage: python check_asm_hazards.py [kernel-name-prefix ...]   (default: moearc_attn_prefill_g)
 Exit status 1 when a hazard is found.
@@ -247,6 +252,24 @@ def load_hazards(ins):
     return out
 
 
+STORE_WAIT = 1  # VALU write of a >64-bit store's data VGPRs after the store
+
+
+def store_data_hazards(ins, labels):
+    out = []
+    for i, t in enumerate(ins):
+        op, args = split_ops(t)
+        if not re.match(r"(global|flat|scratch|buffer)_store_dwordx[34]$", op) or len(args) < 2:
+            continue
+        data = regs(args[0] if op.startswith("buffer") else args[1])
+
+        def check(u, data=data):
+            w, _ = writes_reads(u)
+            return "writes the store's data" if w & data else None
+        out += walk(ins, labels, i, STORE_WAIT, check)
+    return out
+
+
 def m0_hazards(lines):
     """Check 4 over the raw assembly: every ;;#ASMSTART .. ;;#ASMEND region that writes m0 saves
     it first (s_mov_b32 sN, m0) and restores it last (s_mov_b32 m0, sN), sN untouched between."""
@@ -387,6 +410,14 @@ def main(prefixes):
     for p in m0[:10]:
         print("   ", p)
     heads = [l.split(";")[0].rstrip() for l in lines]
+    kernels = sorted({h[:-1] for h in heads if re.match(r"^moearc_\w*_k\w*:$", h) or re.match(r"^moearc_attn_prefill_g\d+:$", h)})
+    store = []
+    for name in kernels:
+        ins, labels = kernel_body(lines, name)
+        store += [f"{name}: {p}" for p in store_data_hazards(ins, labels)]
+    print(f"stores of more than 8 bytes with their data overwritten too soon, {len(kernels)} kernels: {len(store)}")
+    for p in store[:10]:
+        print("   ", p)
     names = sorted({h[:-1] for h in heads if re.match(r"^[A-Za-z_]\w*:$", h)
                     and any(h.startswith(p) for p in prefixes)})
     bad = 0
@@ -400,7 +431,7 @@ def main(prefixes):
     if not names:
         print("no kernel matches", prefixes)
         return 1
-    return 1 if bad or m0 or undeclared else 0
+    return 1 if bad or m0 or undeclared or store else 0
 
 
 if __name__ == "__main__":

@@ -86,7 +86,7 @@ struct moearc_ctx {
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr, f_read_floor = nullptr;
-    hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
+    hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_split8 = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
     hipFunction_t f_mm2[2] = {};  // Q8_0, F16: 128 x 128 tiles on the 32x32x16 MFMA
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
@@ -610,6 +610,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm2[1], "moearc_matmul2_f16_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
+        {&c->f_split8, "moearc_split_f16_v8_k"},
         {&c->f_mm_reduce, "moearc_matmul_reduce_k"},
     };
     for (auto &f : fns) {
@@ -1471,6 +1472,12 @@ int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **
         uint16_t *hi, *lo;
         uint64_t n;
     } a{x, *xh, *xl, n};
+    // eight elements per thread when x allows 16-byte loads (hi and lo are: n is a multiple of 32)
+    if ((uintptr_t) x % 16 == 0) {
+        a.n = n / 8;
+        return launch(c, c->f_split8, (unsigned) std::min<size_t>((n / 8 + 255) / 256, 65536), 256, a, "split_f16",
+                      n, 0);
+    }
     return launch(c, c->f_split, (unsigned) std::min<size_t>((n + 255) / 256, 65536), 256, a, "split_f16", n, 0);
 }
 

@@ -248,6 +248,25 @@ def test_chunk_matmul_meets_the_matvec_bound(ctx, ty, n_tok, rows, cols):
     assert worst <= 1.0
 
 
+def test_chunk_matmul_activation_alignment(ctx):
+    # the activation's f16 split runs eight elements per thread from a 16-byte aligned x and one
+    # element per thread otherwise: the same arithmetic, so the products agree to the bit
+    ty, n_tok, rows, cols = QuantType.Q8_0, 96, 200, 320
+    w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x7A1)
+    x = fx.synth.unit(0x7A2, n_tok * cols).reshape(n_tok, cols)
+    dw = ctx.upload(w)
+    outs = []
+    for off in (0, 4):
+        buf = ctx.alloc(x.nbytes + 16)
+        xv = DeviceView(buf, off, x.nbytes)
+        ctx.upload_slice(xv, x)
+        y = ctx.alloc(n_tok * rows * 4)
+        ctx.matmul_q(ty, y, dw, xv, None, n_tok, rows, cols)
+        outs.append(ctx.download(y, np.float32, (n_tok, rows)))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.any(outs[0] != 0)
+
+
 def test_chunk_matmul_refusals(ctx):
     lib = ctx._lib
     buf = ctx.alloc(1 << 16)
