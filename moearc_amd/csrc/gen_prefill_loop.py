@@ -151,20 +151,21 @@ def pid_load(slot, tile_sgpr, label):
 
 def copy_tile(slot, tile_sgpr, buf, label):
     """LDS-DMA copy of tile s[tile_sgpr] (clamped) into buffer `buf` with the entries in `slot`:
-    wave-uniform scalar-base form when the tile lies in one page (pages >= 64 keys) wholly below
-    the last query position, per-lane addresses otherwise (out of line). Four memory operations
-    either way."""
+    wave-uniform scalar-base form when the tile's 64 keys lie in one page (tiles start on a 32-key
+    boundary, so a tile may straddle two pages) wholly below the last query position, per-lane
+    addresses otherwise (out of line). Four memory operations either way."""
     ins(f"s_min_u32 s71, s{tile_sgpr}, %[ntm1]")
     ins("s_lshl_b32 s70, s71, 6")
     ins("s_add_u32 s70, s70, %[kb0]")          # first key of the tile
-    ins("s_cmp_lt_u32 %[sh], 6")
-    ins(f"s_cbranch_scc1 {label}_lane")
     ins("s_add_u32 s73, s70, 63")
     ins("s_cmp_gt_u32 s73, %[plast]")
     ins(f"s_cbranch_scc1 {label}_lane")
+    ins("s_and_b32 s73, s70, %[pmask]")        # the tile's first key within its page
+    ins("s_add_u32 s79, s73, 63")
+    ins("s_cmp_gt_u32 s79, %[pmask]")          # last key past the page's end (always for pages < 64)
+    ins(f"s_cbranch_scc1 {label}_lane")
     ins(f"v_readfirstlane_b32 s72, v{222 + 2 * slot}")
     ins("s_lshl_b32 s72, s72, %[sh]")
-    ins("s_and_b32 s73, s70, %[pmask]")
     ins("s_or_b32 s72, s72, s73")               # row of the tile's first key
     ins("s_mul_i32 s74, s72, %[rowb]")
     ins("s_mul_hi_u32 s75, s72, %[rowb]")       # byte offset of the row (64-bit)
@@ -346,12 +347,13 @@ def generate():
     for x in max_ops(64, 82):
         ins(x)
     # ---- main loop: four tiles (eight chunks) per pass; buffers and entry slots fixed ----
+    # (the chunk count may be odd: the loop can end after a tile's first chunk)
     ins("pff_loop:")
     for k in range(NBUF):
         for ci in range(2):
             chunk(k, ci, f"c{k}{ci}")
-        ins("s_cmp_ge_u32 s64, %[nc]")
-        ins("s_cbranch_scc1 pff_end")
+            ins("s_cmp_ge_u32 s64, %[nc]")
+            ins("s_cbranch_scc1 pff_end")
     ins("s_branch pff_loop")
     out.extend(ool)
     # ---- rare paths (called with s_call_b64 s[66:67], return with s_setpc_b64) ----
