@@ -196,25 +196,34 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
 // of each (token, pair) are computed once per work-group into LDS (the generic kernel computes
 // them once per 4 heads). Each lane stores 8 bytes of K and of V -- a row is one 128-byte line --
 // written through to the device-coherent level. Same results as moearc_rope_kv_append_chunk_k.
-extern "C" __global__ void __launch_bounds__(256) moearc_rope_kv_append_chunk64_k(
-    uint16_t *k_pages, uint16_t *v_pages, const float *k, const float *v, const int *pos,
-    const uint32_t *page_ids, const uint32_t *slots, uint64_t n_tok, uint32_t n_kv_heads,
-    uint64_t page_tokens, RopeParams r, uint32_t *err) {
-    __shared__ float2_t cs_tab[16 * 32];
+//
+// Rows of 64 channels, 16 per work-group (row = (token, head) of n_heads rows per token, with
+// n_heads dividing 16 or a multiple of 16, so the work-group's rows cover T <= 16 whole or
+// partial tokens). KV: the rows are K (rotated) and V, appended at (page_ids[t], slots[t]); else
+// the rows are q, rotated into q_out (binary16 when q_f16, f32 otherwise).
+template <bool KV>
+__device__ __forceinline__ void rope64_rows(uint32_t b, uint32_t nh, const float *x, const float *v,
+                                            void *q_out, uint32_t q_f16, uint16_t *k_pages,
+                                            uint16_t *v_pages, const int *pos, const uint32_t *page_ids,
+                                            const uint32_t *slots, uint64_t n_tok, uint64_t page_tokens,
+                                            const RopeParams &r, uint32_t *err, float2_t *cs_tab) {
     const uint32_t tid = threadIdx.x, c = tid & 15u;
-    const uint32_t T = 16u / n_kv_heads;  // tokens per work-group
-    const uint64_t t_first = (uint64_t) blockIdx.x * T;
-    const uint64_t row = (uint64_t) blockIdx.x * 16u + (tid >> 4);
-    const uint64_t t = row / n_kv_heads;
+    const uint64_t row0 = (uint64_t) b * 16u;
+    const uint64_t t_first = row0 / nh;
+    const uint32_t T = (uint32_t) ((row0 + 15u) / nh - t_first) + 1u;  // tokens the 16 rows touch
+    const uint64_t row = row0 + (tid >> 4);
+    const uint64_t t = row / nh;
     const bool live = t < n_tok;
     // this lane's pieces and its row's destination leave before anything waits on them
     float4_t kx = {}, vx = {};
     uint32_t slot = 0, page = 0;
     if (live) {
-        kx = *(const float4_t *) (k + row * 64u + 4u * c);
-        vx = *(const float4_t *) (v + row * 64u + 4u * c);
-        slot = slots[t];
-        page = page_ids[t];
+        kx = *(const float4_t *) (x + row * 64u + 4u * c);
+        if constexpr (KV) {
+            vx = *(const float4_t *) (v + row * 64u + 4u * c);
+            slot = slots[t];
+            page = page_ids[t];
+        }
     }
     for (uint32_t i = tid; i < T * 32u; i += 256u) {
         const uint64_t tt = t_first + (i >> 5);
@@ -222,12 +231,13 @@ extern "C" __global__ void __launch_bounds__(256) moearc_rope_kv_append_chunk64_
     }
     __syncthreads();
     if (!live) return;  // whole rows leave together: the row exchange below stays within live rows
-    if (slot >= page_tokens) {
+    if (KV && slot >= page_tokens) {
         if (c == 0) *(volatile uint32_t *) err = 1u;
         return;
     }
     const bool hi = c >= 8u;
     const uint32_t tl = (uint32_t) (t - t_first);
+    float o[4];
     uint32_t ko[2], vo[2];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -235,11 +245,45 @@ extern "C" __global__ void __launch_bounds__(256) moearc_rope_kv_append_chunk64_
         const float2_t cs = cs_tab[tl * 32u + 4u * (c & 7u) + (uint32_t) i];
         float o0, o1;
         rope_rotate(hi ? kq : kx[i], hi ? kx[i] : kq, cs, o0, o1);
-        const uint32_t kb = f32_to_f16_bits(hi ? o1 : o0), vb = f32_to_f16_bits(vx[i]);
+        o[i] = hi ? o1 : o0;
+        const uint32_t kb = f32_to_f16_bits(o[i]), vb = f32_to_f16_bits(vx[i]);
         ko[i >> 1] = (i & 1) ? (ko[i >> 1] | (kb << 16)) : kb;
         vo[i >> 1] = (i & 1) ? (vo[i >> 1] | (vb << 16)) : vb;
     }
-    const uint64_t dst = (((uint64_t) page * page_tokens + slot) * n_kv_heads + (row - t * n_kv_heads)) * 64u + 4u * c;
-    store_through8(k_pages + dst, u32x2_t{ko[0], ko[1]});
-    store_through8(v_pages + dst, u32x2_t{vo[0], vo[1]});
+    if constexpr (KV) {
+        const uint64_t dst = (((uint64_t) page * page_tokens + slot) * nh + (row - t * nh)) * 64u + 4u * c;
+        store_through8(k_pages + dst, u32x2_t{ko[0], ko[1]});
+        store_through8(v_pages + dst, u32x2_t{vo[0], vo[1]});
+    } else if (q_f16) {
+        store_through8((uint16_t *) q_out + row * 64u + 4u * c, u32x2_t{ko[0], ko[1]});
+    } else {
+        *(float4_t *) ((float *) q_out + row * 64u + 4u * c) = float4_t{o[0], o[1], o[2], o[3]};
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) moearc_rope_kv_append_chunk64_k(
+    uint16_t *k_pages, uint16_t *v_pages, const float *k, const float *v, const int *pos,
+    const uint32_t *page_ids, const uint32_t *slots, uint64_t n_tok, uint32_t n_kv_heads,
+    uint64_t page_tokens, RopeParams r, uint32_t *err) {
+    __shared__ float2_t cs_tab[16 * 32];
+    rope64_rows<true>(blockIdx.x, n_kv_heads, k, v, nullptr, 0u, k_pages, v_pages, pos, page_ids, slots,
+                      n_tok, page_tokens, r, err, cs_tab);
+}
+
+// RoPE of a chunk's q and the fused K/V append in one launch (the attention block's two steps
+// between its projections and its attention, independent of each other): work-groups [0, nb_q)
+// take q's rows, the rest K/V's, each as in rope64_rows. q f32 [n_tok][n_heads][64] -> q_out;
+// results equal moearc_rope_f16_k (q_f16) or moearc_rope_k, and moearc_rope_kv_append_chunk64_k.
+extern "C" __global__ void __launch_bounds__(256) moearc_rope_qkv_chunk64_k(
+    void *q_out, const float *q, uint32_t n_heads, uint32_t q_f16, uint32_t nb_q,
+    uint16_t *k_pages, uint16_t *v_pages, const float *k, const float *v, const int *pos,
+    const uint32_t *page_ids, const uint32_t *slots, uint64_t n_tok, uint32_t n_kv_heads,
+    uint64_t page_tokens, RopeParams r, uint32_t *err) {
+    __shared__ float2_t cs_tab[16 * 32];
+    if (blockIdx.x < nb_q)
+        rope64_rows<false>(blockIdx.x, n_heads, q, nullptr, q_out, q_f16, nullptr, nullptr, pos, nullptr,
+                           nullptr, n_tok, 0u, r, err, cs_tab);
+    else
+        rope64_rows<true>(blockIdx.x - nb_q, n_kv_heads, k, v, nullptr, 0u, k_pages, v_pages, pos, page_ids,
+                          slots, n_tok, page_tokens, r, err, cs_tab);
 }

@@ -80,6 +80,8 @@ struct moearc_ctx {
     hipModule_t module = nullptr;
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
     hipFunction_t f_rope = nullptr, f_rope_f16 = nullptr, f_rope_append_chunk = nullptr, f_rope_append64 = nullptr;
+    hipFunction_t f_rope_qkv64 = nullptr;  // RoPE of q and the fused K/V append in one launch
+    bool rope_qkv_fused = true;            // MOEARC_ROPE_QKV_FUSED=0: the block makes them as two launches
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[2] = {};  // split kernels (kDecodeVariants)
     hipFunction_t f_dec_merge = nullptr;
@@ -588,6 +590,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_rope_f16, "moearc_rope_f16_k"},
         {&c->f_rope_append_chunk, "moearc_rope_kv_append_chunk_k"},
         {&c->f_rope_append64, "moearc_rope_kv_append_chunk64_k"},
+        {&c->f_rope_qkv64, "moearc_rope_qkv_chunk64_k"},
         {&c->f_dec_general, "moearc_attn_decode_general_k"},
         {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k4w2t4"},
         {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w4t1"},
@@ -627,6 +630,7 @@ moearc_ctx *moearc_ctx_create(void) {
     }
     c->merge_threads = (unsigned) merge_threads;
     if (const char *pp = std::getenv("MOEARC_PREFILL_PRECISE")) c->prefill_precise = pp[0] == '1';
+    if (const char *rf = std::getenv("MOEARC_ROPE_QKV_FUSED")) c->rope_qkv_fused = rf[0] != '0';
     for (int i = 0; i < 8; ++i) {
         const bool precise = i >= 4;
         char name[64];
@@ -1596,17 +1600,48 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
         }
     }
     // RoPE of q (written as f16 for the prefill kernel when there is a chunk: the values
-    // moearc_quantize_f16 would make of the f32 rotation); RoPE of K fused with the K/V append
+    // moearc_quantize_f16 would make of the f32 rotation); RoPE of K fused with the K/V append.
+    // With NeoX over all 64 channels and head counts that divide 16 or are multiples of it, both
+    // go out as one launch (moearc_rope_qkv_chunk64_k), with the same results.
     const bool chunk = n_tok > 1;
-    if (const int rc = rope_launch(c, chunk ? c->f_rope_f16 : c->f_rope, chunk ? (void *) q16 : (void *) qr, q,
-                                   pos, n_tok, H, D, b->n_rot, b->freq_base, b->freq_scale, b->ext_factor,
-                                   b->attn_factor, b->corr_lo, b->corr_hi, 1))
-        return rc;
-    if (const int rc = moearc_rope_kv_append_chunk(c, b->k_pages, b->v_pages, k, v, pos, page_ids, slots,
-                                                   n_tok, G, D, b->page_tokens, b->n_rot, b->freq_base,
-                                                   b->freq_scale, b->ext_factor, b->attn_factor,
-                                                   b->corr_lo, b->corr_hi, 1, 1u))
-        return rc;
+    auto rows16 = [](unsigned long nh) { return nh != 0 && (16 % nh == 0 || nh % 16 == 0); };
+    void *qdst = chunk ? (void *) q16 : (void *) qr;
+    if (c->rope_qkv_fused && D == 64 && b->n_rot == 64 && rows16(H) && rows16(G) && H <= 0xFFFFFFFFul &&
+        ((uintptr_t) q | (uintptr_t) qdst | (uintptr_t) k | (uintptr_t) v) % 16 == 0 &&
+        ((uintptr_t) b->k_pages | (uintptr_t) b->v_pages) % 8 == 0 && (n_tok * (H + G) + 15) / 16 < 0xFFFFFFFFull) {
+        const uint64_t nb_q = (n_tok * H + 15) / 16, nb_kv = (n_tok * G + 15) / 16;
+        struct {
+            void *q_out;
+            const float *q;
+            uint32_t n_heads, q_f16, nb_q;
+            void *kp, *vp;
+            const float *k, *v;
+            const int *pos;
+            const uint32_t *pages, *slots;
+            uint64_t n_tok;
+            uint32_t n_kv_heads;
+            uint64_t pt;
+            RopeParams r;
+            uint32_t *err;
+        } a{qdst, q, (uint32_t) H, chunk ? 1u : 0u, (uint32_t) nb_q, b->k_pages, b->v_pages, k, v, pos,
+            page_ids, slots, n_tok, (uint32_t) G, b->page_tokens,
+            rope_params(b->n_rot, b->freq_base, b->freq_scale, b->ext_factor, b->attn_factor, b->corr_lo,
+                        b->corr_hi, 1),
+            c->err_word};
+        c->err_armed = true;
+        if (const int rc = launch2d(c, c->f_rope_qkv64, (unsigned) (nb_q + nb_kv), 1, 256, a, "rope_qkv_chunk", H, D))
+            return rc;
+    } else {
+        if (const int rc = rope_launch(c, chunk ? c->f_rope_f16 : c->f_rope, qdst, q, pos, n_tok, H, D, b->n_rot,
+                                       b->freq_base, b->freq_scale, b->ext_factor, b->attn_factor, b->corr_lo,
+                                       b->corr_hi, 1))
+            return rc;
+        if (const int rc = moearc_rope_kv_append_chunk(c, b->k_pages, b->v_pages, k, v, pos, page_ids, slots,
+                                                       n_tok, G, D, b->page_tokens, b->n_rot, b->freq_base,
+                                                       b->freq_scale, b->ext_factor, b->attn_factor,
+                                                       b->corr_lo, b->corr_hi, 1, 1u))
+            return rc;
+    }
     if (n_tok == 1) {  // one decode step: the split-K decode kernel, f32 q (moe.rs:2044-2060)
         const unsigned long n_kv = pos0 + 1, kv_begin = b->n_swa && n_kv > b->n_swa ? n_kv - b->n_swa : 0;
         if (const int rc = moearc_attn_decode(c, att, qr, b->k_pages, b->v_pages, b->block_table, b->sinks, H, G,
