@@ -100,6 +100,8 @@ struct PrefillArgs {
     uint32_t out_f16;
     float scale_log2e;
     uint32_t n_qtiles;            // query tiles per KV head
+    uint16_t *out_lo;             // with f16 output: also f16(o - hi) here, the low half of the
+                                  // chunk product's activation split (default kernels; else null)
 };
 
 // RoPE parameters (moearc_rope, moearc_rope_kv_append_chunk): theta_scale = freq_base^(-2/n_dims),

@@ -81,7 +81,7 @@ struct moearc_ctx {
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
     hipFunction_t f_rope = nullptr, f_rope_f16 = nullptr, f_rope_append_chunk = nullptr, f_rope_append64 = nullptr;
     hipFunction_t f_rope_qkv64 = nullptr;  // RoPE of q and the fused K/V append in one launch
-    bool rope_qkv_fused = true;            // MOEARC_ROPE_QKV_FUSED=0: the block makes them as two launches
+    bool block_fused = true;  // MOEARC_BLOCK_FUSED=0: the attention block's fused steps as separate launches
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[2] = {};  // split kernels (kDecodeVariants)
     hipFunction_t f_dec_merge = nullptr;
@@ -630,7 +630,7 @@ moearc_ctx *moearc_ctx_create(void) {
     }
     c->merge_threads = (unsigned) merge_threads;
     if (const char *pp = std::getenv("MOEARC_PREFILL_PRECISE")) c->prefill_precise = pp[0] == '1';
-    if (const char *rf = std::getenv("MOEARC_ROPE_QKV_FUSED")) c->rope_qkv_fused = rf[0] != '0';
+    if (const char *bf = std::getenv("MOEARC_BLOCK_FUSED")) c->block_fused = bf[0] != '0';
     for (int i = 0; i < 8; ++i) {
         const bool precise = i >= 4;
         char name[64];
@@ -1249,12 +1249,24 @@ int moearc_attn_decode_batched_noalloc(moearc_ctx *c, void *out, unsigned int ou
     return rc;
 }
 
-int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const void *q,
-                        const void *k_pages, const void *v_pages, const unsigned int *block_table,
-                        const float *sinks, unsigned long n_q, unsigned long pos0,
-                        unsigned long n_swa, unsigned long n_heads, unsigned long n_kv_heads,
-                        unsigned long head_dim, unsigned long page_tokens, float scale,
-                        unsigned int kv_type) {
+}  // extern "C"
+
+namespace {
+
+// The single-f16 kernels pre-scale Q by scale*log2(e) in f16, which stays in range for
+// |scale*log2(e)| <= 1 (every softmax scale up to 0.69); larger scales take the precise kernels.
+bool prefill_is_fast(const moearc_ctx *c, float scale) {
+    return !c->prefill_precise && std::fabs(scale * 1.4426950408889634f) <= 1.0f;
+}
+
+// moearc_attn_prefill's checks and launch; out_lo (f16 output, default kernels only) also takes
+// the low halves of the chunk product's activation split.
+int prefill_launch(moearc_ctx *c, void *out, unsigned int out_type, uint16_t *out_lo, const void *q,
+                   const void *k_pages, const void *v_pages, const unsigned int *block_table,
+                   const float *sinks, unsigned long n_q, unsigned long pos0,
+                   unsigned long n_swa, unsigned long n_heads, unsigned long n_kv_heads,
+                   unsigned long head_dim, unsigned long page_tokens, float scale,
+                   unsigned int kv_type) {
     if (!c || !out || !q || !k_pages || !v_pages || !block_table) return ERR;
     if (kv_type != 1u) return ERR_ARG;
     if (out_type != MOEARC_OUT_F32 && out_type != MOEARC_OUT_F16) return ERR_ARG;
@@ -1265,10 +1277,9 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     if (group != 1 && group != 2 && group != 4 && group != 8) return ERR_ARG;
     if (pos0 + n_q > 0xFFFFFFFFul) return ERR_ARG;
     const int gi = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : 3;
-    // The single-f16 kernels pre-scale Q by scale*log2(e) in f16, which stays in range for
-    // |scale*log2(e)| <= 1 (every softmax scale up to 0.69); larger scales take the precise kernels.
     const float scale_log2e = scale * 1.4426950408889634f;
-    const bool precise = c->prefill_precise || !(std::fabs(scale_log2e) <= 1.0f);
+    const bool precise = !prefill_is_fast(c, scale);
+    if (out_lo && (precise || out_type != MOEARC_OUT_F16)) return ERR_ARG;
     hipFunction_t f = precise ? c->f_prefill_precise[gi] : c->f_prefill[gi];
     if (!f) return ERR;
     PrefillArgs a{};
@@ -1291,11 +1302,27 @@ int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const v
     const uint32_t rows_per_tile = precise ? MOEARC_PREFILL_ROWS : MOEARC_PREFILL_FAST_ROWS;
     const uint64_t rows = (uint64_t) n_q * group;
     a.n_qtiles = (uint32_t) ((rows + rows_per_tile - 1) / rows_per_tile);
+    a.out_lo = out_lo;
     const uint64_t wgs = (uint64_t) a.n_qtiles * n_kv_heads;
     if (wgs > 0x7FFFFFFFull) return ERR_ARG;
     return launch(c, f, (unsigned) wgs, MOEARC_PREFILL_THREADS, a, "attn_prefill",
                   n_heads, head_dim);
 }
+
+}  // namespace
+
+extern "C" {
+
+int moearc_attn_prefill(moearc_ctx *c, void *out, unsigned int out_type, const void *q,
+                        const void *k_pages, const void *v_pages, const unsigned int *block_table,
+                        const float *sinks, unsigned long n_q, unsigned long pos0,
+                        unsigned long n_swa, unsigned long n_heads, unsigned long n_kv_heads,
+                        unsigned long head_dim, unsigned long page_tokens, float scale,
+                        unsigned int kv_type) {
+    return prefill_launch(c, out, out_type, nullptr, q, k_pages, v_pages, block_table, sinks, n_q, pos0, n_swa,
+                          n_heads, n_kv_heads, head_dim, page_tokens, scale, kv_type);
+}
+
 
 }  // extern "C"
 
@@ -1448,7 +1475,8 @@ bool mm_needs_sums(unsigned ty) { return ty == 12u || ty == 13u; }
 
 // The f16 hi / lo split of x (n floats, n a multiple of 32) into the context's buffer, and its
 // 32-element block sums when `sums` (else *xs points at space the products do not read).
-int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl, float **xs, bool sums) {
+// The split's buffers in the context's workspace (grown on demand): hi, lo, then n / 32 floats.
+int mm_split_space(moearc_ctx *c, size_t n, uint16_t **xh, uint16_t **xl, float **xs) {
     const size_t halves = 2 * n + n / 16;  // hi, lo, then n / 32 floats
     if (halves > c->mm_ws_halves) {
         if (c->mm_ws) {
@@ -1462,6 +1490,11 @@ int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **
     *xh = c->mm_ws;
     *xl = c->mm_ws + n;
     *xs = (float *) (c->mm_ws + 2 * n);  // 4-byte aligned: n is a multiple of 32
+    return OK;
+}
+
+int mm_split(moearc_ctx *c, const float *x, size_t n, uint16_t **xh, uint16_t **xl, float **xs, bool sums) {
+    if (const int rc = mm_split_space(c, n, xh, xl, xs)) return rc;
     struct {
         const float *x;
         float *xs;
@@ -1606,7 +1639,7 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     const bool chunk = n_tok > 1;
     auto rows16 = [](unsigned long nh) { return nh != 0 && (16 % nh == 0 || nh % 16 == 0); };
     void *qdst = chunk ? (void *) q16 : (void *) qr;
-    if (c->rope_qkv_fused && D == 64 && b->n_rot == 64 && rows16(H) && rows16(G) && H <= 0xFFFFFFFFul &&
+    if (c->block_fused && D == 64 && b->n_rot == 64 && rows16(H) && rows16(G) && H <= 0xFFFFFFFFul &&
         ((uintptr_t) q | (uintptr_t) qdst | (uintptr_t) k | (uintptr_t) v) % 16 == 0 &&
         ((uintptr_t) b->k_pages | (uintptr_t) b->v_pages) % 8 == 0 && (n_tok * (H + G) + 15) / 16 < 0xFFFFFFFFull) {
         const uint64_t nb_q = (n_tok * H + 15) / 16, nb_kv = (n_tok * G + 15) / 16;
@@ -1642,22 +1675,33 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
                                                        b->corr_lo, b->corr_hi, 1, 1u))
             return rc;
     }
+    // With the output projection on the MFMA product (a format without block sums) and the
+    // default prefill kernels, the prefill writes the product's f16 hi + lo activation split
+    // itself, in place of an f32 output and a split launch (the same halves).
+    const bool proj_mm = n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK;
+    const bool att_split = c->block_fused && proj_mm && !mm_needs_sums(b->w_type[3]) && prefill_is_fast(c, b->scale);
+    uint16_t *axh = nullptr, *axl = nullptr;
+    float *axs = nullptr;
+    if (att_split)
+        if (const int rc = mm_split_space(c, nq, &axh, &axl, &axs)) return rc;
     if (n_tok == 1) {  // one decode step: the split-K decode kernel, f32 q (moe.rs:2044-2060)
         const unsigned long n_kv = pos0 + 1, kv_begin = b->n_swa && n_kv > b->n_swa ? n_kv - b->n_swa : 0;
         if (const int rc = moearc_attn_decode(c, att, qr, b->k_pages, b->v_pages, b->block_table, b->sinks, H, G,
                                               D, kv_begin, n_kv, b->page_tokens, b->scale, 1u))
             return rc;
-    } else if (const int rc = moearc_attn_prefill(c, att, MOEARC_OUT_F32, q16, b->k_pages, b->v_pages,
-                                                  b->block_table, b->sinks, n_tok, pos0, b->n_swa, H, G, D,
-                                                  b->page_tokens, b->scale, 1u)) {
+    } else if (const int rc = prefill_launch(c, att_split ? (void *) axh : (void *) att,
+                                             att_split ? MOEARC_OUT_F16 : MOEARC_OUT_F32, axl, q16, b->k_pages,
+                                             b->v_pages, b->block_table, b->sinks, n_tok, pos0, b->n_swa, H, G,
+                                             D, b->page_tokens, b->scale, 1u)) {
         return rc;
     }
     // h += W_o attn (+ bias_o), the residual add folded into the product's store
     (void) proj;
-    if (n_tok >= 2 && mm_check(b->w_type[3], b->w[3], n_tok, E, q_rows) == OK) {
-        uint16_t *xh, *xl;
-        float *xs;
-        if (const int rc = mm_split(c, att, nq, &xh, &xl, &xs, mm_needs_sums(b->w_type[3]))) return rc;
+    if (proj_mm) {
+        uint16_t *xh = axh, *xl = axl;
+        float *xs = axs;
+        if (!att_split)
+            if (const int rc = mm_split(c, att, nq, &xh, &xl, &xs, mm_needs_sums(b->w_type[3]))) return rc;
         const MmMat mat{b->w[3], b->bias[3], h, E, E};
         return mm_launch(c, b->w_type[3], &mat, 1, xh, xl, xs, n_tok, q_rows, "attn_proj_mm", true);
     }

@@ -182,15 +182,16 @@ def test_chunk_equals_token_by_token(ctx):
 
 
 @pytest.mark.parametrize("dims", ["toy", "gpt_oss"])
-def test_fused_rope_launch_equals_two_launches(monkeypatch, dims):
-    # RoPE of q and the K/V append as one launch (moearc_rope_qkv_chunk64_k, the default for NeoX
-    # over 64 channels) against the two launches it replaces (MOEARC_ROPE_QKV_FUSED=0): the
-    # residual after a chunk and after a decode step, and both pools, bit-identical
+def test_fused_launches_equal_separate_ones(monkeypatch, dims):
+    # The block's fused steps (the default) against the launches they replace (MOEARC_BLOCK_FUSED=0):
+    # the RoPE of q and the K/V append as one launch (moearc_rope_qkv_chunk64_k), and the prefill
+    # writing the output projection's f16 hi + lo split instead of f32 rows and a split launch. The
+    # residual after a chunk and after a decode step, and both pools, bit-identical.
     from moearc_amd import Context
     d = TOY if dims == "toy" else GPT_OSS
     got = {}
     for fused in ("1", "0"):
-        monkeypatch.setenv("MOEARC_ROPE_QKV_FUSED", fused)
+        monkeypatch.setenv("MOEARC_BLOCK_FUSED", fused)
         with Context() as cx:
             blk = Block(cx, (8, 8, 8, 8), 0xB60C, n_ctx=256, chunk=64, dims=d, x_scale=0.03,
                         scaling=RopeScaling.yarn(64, 4096, 150000.0, 32.0), freq_base=150000.0)
@@ -205,7 +206,7 @@ def test_fused_rope_launch_equals_two_launches(monkeypatch, dims):
             outs.append(cx.download(blk.d_vp, np.uint16, blk.vp.shape))
         got[fused] = outs
     for name, a, b in zip(("chunk", "decode step", "K pool", "V pool"), got["1"], got["0"]):
-        print(f"fused RoPE launch, {dims}, {name}: {int(np.sum(a.view(np.uint8) != b.view(np.uint8)))} bytes differ",
+        print(f"fused block launches, {dims}, {name}: {int(np.sum(a.view(np.uint8) != b.view(np.uint8)))} bytes differ",
               flush=True)
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
 
