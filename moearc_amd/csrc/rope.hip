@@ -208,11 +208,12 @@ __device__ __forceinline__ void rope64_rows(uint32_t b, uint32_t nh, const float
                                             const uint32_t *slots, uint64_t n_tok, uint64_t page_tokens,
                                             const RopeParams &r, uint32_t *err, float2_t *cs_tab) {
     const uint32_t tid = threadIdx.x, c = tid & 15u;
-    const uint64_t row0 = (uint64_t) b * 16u;
-    const uint64_t t_first = row0 / nh;
-    const uint32_t T = (uint32_t) ((row0 + 15u) / nh - t_first) + 1u;  // tokens the 16 rows touch
-    const uint64_t row = row0 + (tid >> 4);
-    const uint64_t t = row / nh;
+    // tokens the 16 rows touch: 16 / nh whole ones, or one (32-bit divisions only)
+    const bool few = nh <= 16u;
+    const uint32_t T = few ? 16u / nh : 1u;
+    const uint64_t t_first = few ? (uint64_t) b * T : (uint64_t) (b / (nh >> 4));
+    const uint64_t row = (uint64_t) b * 16u + (tid >> 4);
+    const uint64_t t = few ? t_first + (tid >> 4) / nh : t_first;
     const bool live = t < n_tok;
     // this lane's pieces and its row's destination leave before anything waits on them
     float4_t kx = {}, vx = {};
