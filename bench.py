@@ -301,7 +301,12 @@ def launch_overhead():
     return json.loads(res.stdout.strip().splitlines()[-1])
 
 
-def prefill_inputs(ctx, copies=4):
+# independent config-4 input sets the prefill timings rotate over: 12 x (16 MiB q + 2 x 4 MiB K/V)
+# = 288 MiB, more than the 256 MB Infinity Cache, so no call is served its inputs from that cache
+PF_SETS = 12
+
+
+def prefill_inputs(ctx, copies=PF_SETS):
     """Config-4 prefill inputs (tests/fixtures.py: the same seeded case the parity tests use), in
     `copies` independent sets of q, K and V."""
     import fixtures as fx
@@ -312,17 +317,18 @@ def prefill_inputs(ctx, copies=4):
     return dks, dvs, dqs, ctx.upload(pc.bt), ctx.upload(pc.sinks), ctx.alloc(PF_NQ * H * D * 2)
 
 
-def bench_prefill_graph(ctx, hip, calls=8, warmup=3):
-    """Both config-4 layers timed as the decode is: `calls` calls (rotating over 4 input sets)
-    captured in one graph and replayed REPS times; per-call µs statistics, the first replay
-    discarded. Close to the kernel's own duration (one dispatch gap per call)."""
+def bench_prefill_graph(ctx, hip, calls=PF_SETS, warmup=3):
+    """Both config-4 layers timed as the decode is: `calls` calls (each on its own input set,
+    PF_SETS of them) captured in one graph and replayed REPS times; per-call µs statistics, the
+    first replay discarded. Close to the kernel's own duration (one dispatch gap per call)."""
     from moearc_amd import KvType, OUT_F16
     dks, dvs, dqs, dbt, ds, dout = prefill_inputs(ctx)
+    n_sets = len(dks)
     out = {}
     for name, n_swa in (("full", 0), ("swa128", 128)):
         def call(i, n_swa=n_swa):
-            ctx.attn_prefill(dout, dqs[i % 4], dks[i % 4], dvs[i % 4], dbt, ds, PF_NQ, PF_POS0, n_swa,
-                             H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
+            ctx.attn_prefill(dout, dqs[i % n_sets], dks[i % n_sets], dvs[i % n_sets], dbt, ds, PF_NQ,
+                             PF_POS0, n_swa, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
         out[name] = rep_stats(graph_timed(hip, ctx, call, calls, warmup))
     return out
 

@@ -1,8 +1,8 @@
 """Generates prefill_loop.inc: the key loop of the default prefill kernels (prefill_fast.hip) as one
 gfx950 inline-asm statement.
 
-Why asm: the loop keeps ~210 VGPRs of state (four 16-register O accumulators, two score tuples,
-two bias tuples, Q, K and V^T operands). Written in C++, the compiler's allocator copies whole
+Why asm: the loop keeps ~180 VGPRs of state (four 16-register O accumulators, two score tuples,
+Q, K and V^T operands). Written in C++, the compiler's allocator copies whole
 accumulator tuples at every join and spills; and register constraints on separate asm statements
 do not pin a value between them. One asm statement over a fixed register map does.
 
@@ -13,7 +13,8 @@ Register map (VGPRs):
   v0-v15 v16-v31     O of block A, channel blocks 0 and 1      v128-v143  Q of block A (4 x half8)
   v32-v47 v48-v63    O of block B                              v144-v159  Q of block B
   v64-v79 v80-v95    S of blocks A and B (exponents, weights)  v160-v175  K operands of a chunk
-  v96-v111 v112-v127 bias of blocks A and B (the QK^T init)    v176-v191  V^T operands of a chunk
+  v96 v112           bias 7 - m of blocks A and B (per row)    v176-v191  V^T operands of a chunk
+                     (v97-v111 and v113-v127 are not used)
   v192-v199          P operands (one block at a time)          v200-v207  temporaries
   v208 v209          reference m of A, B                       v210 v211  row sums l of A, B
   v212-v215          LDS addresses of the K operand reads (buffer 0, chunk 0)
@@ -58,25 +59,41 @@ def mfma(d, a, b, c):
 K_OPS = ["160:163", "164:167", "168:171", "172:175"]
 
 
-def qk_exp(sd, q0, bias, e):
-    """S_D = K . Q^T + bias (4 chained MFMAs) beside the 16 exponentials of the weights in
-    v[e..e+15] (in place), four after each MFMA."""
+def qk_exp(sd, q0, e):
+    """S_D = K . Q^T, the raw scores (4 chained MFMAs from zero), beside the 16 exponentials of the
+    weights in v[e..e+15] (in place), four after each MFMA."""
     qs = [f"{q0 + 4 * t}:{q0 + 4 * t + 3}" for t in range(4)]
     for t in range(4):
-        mfma(sd, K_OPS[t], qs[t], f"v[{bias}]" if t == 0 else f"v[{sd}]")
+        mfma(sd, K_OPS[t], qs[t], "0" if t == 0 else f"v[{sd}]")
         for i in range(4 * t, 4 * t + 4):
             ins(f"v_exp_f32 v{e + i}, v{e + i}")
 
 
-def sum_ops(e, l):
-    """Row-sum tree of the weights v[e..e+15] into l (temporaries v200-v207), in an order that
-    keeps dependent adds apart."""
-    E = list(range(e, e + 16))
+def fma_ops(e, bias):
+    """Exponent inputs of the raw scores v[e..e+15], in place: x = s * c + bias, c = scale * log2(e)
+    in f32 (Q enters the MFMA as the caller's exact f16 values) and bias = 7 - m of the lane's row."""
+    return [f"v_fma_f32 v{e + i}, v{e + i}, %[cs], v{bias}" for i in range(16)]
+
+
+def mix(d, p):
+    """v[d] = lo + hi of the f16 pair in v[p], in f32 (exact: two f16 values)."""
+    return f"v_fma_mix_f32 v{d}, v{p}, 1.0, v{p} op_sel:[0,0,1] op_sel_hi:[1,0,1]"
+
+
+def sum_head():
+    """Row sum of a block's weights as the P.V product sees them (the f16 P operands in v192-v199,
+    so that the normalisation divides by the sum of the very weights the output was formed with):
+    pair sums of v192-v197, each placed after the conversion that writes its pair (extras 1-4 after
+    v192-v195, extras 5-6 after v196-v197)."""
+    return [mix(200 + k, 192 + k) for k in range(6)]
+
+
+def sum_tail(l):
+    """The rest of the row sum: pair sums of v198, v199 (converted before the third MFMA), the tree
+    over v200-v207, and l += the chunk's sum."""
     a = lambda d, x, y: f"v_add_f32 v{d}, v{x}, v{y}"
-    return [a(200, E[0], E[1]), a(201, E[2], E[3]), a(202, E[4], E[5]), a(203, E[6], E[7]),
-            a(200, 200, 201), a(204, E[8], E[9]), a(205, E[10], E[11]), a(202, 202, 203),
-            a(206, E[12], E[13]), a(207, E[14], E[15]), a(204, 204, 205), a(206, 206, 207),
-            a(200, 200, 202), a(204, 204, 206), a(200, 200, 204), a(l, l, 200)]
+    return [mix(206, 198), mix(207, 199), a(200, 200, 201), a(202, 202, 203), a(204, 204, 205),
+            a(206, 206, 207), a(200, 200, 202), a(204, 204, 206), a(200, 200, 204), a(l, l, 200)]
 
 
 def max_ops(e, flag):
@@ -93,28 +110,29 @@ def max_ops(e, flag):
 
 def pv(o0, o1, e, extra):
     """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7], with
-    the VALU instructions `extra` (independent of P and of the V^T operands) spread between the
-    MFMAs: 4 before the first (they cover the VALU-write -> MFMA-read wait), then 6, 6, 6, rest.
-    The chunk places its rescale test (a max3 tree and a compare) from the seventh on: after the
-    first MFMA, at least 20 wait states after the MFMAs that wrote the scores, and two MFMAs before
-    the branch that reads the compare."""
+    the VALU instructions `extra` (not writing P or the V^T operands) spread between the MFMAs: 4
+    before the first (they cover the VALU-write -> MFMA-read wait), then the rest in three equal
+    groups after the first three and a smaller one after the last. The chunk places the other
+    block's exponent inputs and rescale test (16 FMAs, a max3 tree and a compare) from the seventh
+    on: after the first MFMA, at least 20 wait states after the MFMAs that wrote the scores."""
     cvt = lambda d, a, b: ins(f"v_cvt_pk_f16_f32 v{d}, v{e + a}, v{e + b}")
     extra = list(extra)
     take = lambda n: [ins(extra.pop(0)) for _ in range(min(n, len(extra)))]
+    group = max(6, -(-(len(extra) - 4) // 4) + 1)
     cvt(192, 0, 1); cvt(193, 2, 3); cvt(194, 4, 5); cvt(195, 6, 7)
     if len(extra) < 2:
         ins("s_nop 2")  # VALU write -> MFMA read
     take(4)
     mfma(o0, "176:179", "192:195", f"v[{o0}]")
     cvt(196, 8, 9); cvt(197, 10, 11)
-    take(6)
+    take(group)
     mfma(o1, "184:187", "192:195", f"v[{o1}]")
     cvt(198, 12, 13); cvt(199, 14, 15)
     if len(extra) < 2:
         ins("s_nop 2")
-    take(6)
+    take(group)
     mfma(o0, "180:183", "196:199", f"v[{o0}]")
-    take(6)
+    take(group)
     mfma(o1, "188:191", "196:199", f"v[{o1}]")
     take(len(extra))
 
@@ -228,7 +246,7 @@ def chunk(bi, ci, label):
     ins(f"s_cbranch_scc1 {label}_ra")
     ins(f"{label}_a_ok:")
     ool_block(f"{label}_ra", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_rescale_a"], f"{label}_a_ok")
-    qk_exp("80:95", 144, "112:127", 64)
+    qk_exp("80:95", 144, 64)
     read_k(offn)
     # R2: mask of S_B(j); O_A += V(j)^T . P_A(j) | row sum of A(j), rescale test of S_B(j)
     ins("s_waitcnt lgkmcnt(4)")
@@ -237,7 +255,7 @@ def chunk(bi, ci, label):
     ins(f"s_cbranch_scc1 {label}_mb")
     ins(f"{label}_mb_ok:")
     ool_block(f"{label}_mb", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_mask_b"], f"{label}_mb_ok")
-    pv("0:15", "16:31", 64, sum_ops(64, 210)[:6] + max_ops(80, 84) + sum_ops(64, 210)[6:])
+    pv("0:15", "16:31", 64, sum_head() + fma_ops(80, 112) + max_ops(80, 84) + sum_tail(210))
     # R3: S_A(j + 1) | weights of B(j)
     ins("s_cmp_lg_u64 s[84:85], 0")
     ins(f"s_cbranch_scc1 {label}_rb")
@@ -245,14 +263,14 @@ def chunk(bi, ci, label):
     ool_block(f"{label}_rb", ["s_mov_b32 s78, s64", f"s_mov_b32 s76, {off}", f"s_mov_b32 s77, {offn}",
                               "s_call_b64 s[66:67], pff_rescale_b"], f"{label}_b_ok")
     ins("s_waitcnt lgkmcnt(0)")
-    qk_exp("64:79", 128, "96:111", 80)
+    qk_exp("64:79", 128, 80)
     # R4: mask of S_A(j + 1); O_B += V(j)^T . P_B(j) | row sum of B(j), rescale test of S_A(j + 1)
     ins("s_sub_u32 s79, s64, %[jloa1]")           # (j + 1) - jlo_A
     ins("s_cmp_ge_u32 s79, %[jna]")
     ins(f"s_cbranch_scc1 {label}_ma")
     ins(f"{label}_ma_ok:")
     ool_block(f"{label}_ma", ["s_add_u32 s78, s64, 1", "s_call_b64 s[66:67], pff_mask_a"], f"{label}_ma_ok")
-    pv("32:47", "48:63", 80, sum_ops(80, 211)[:6] + max_ops(64, 82) + sum_ops(80, 211)[6:])
+    pv("32:47", "48:63", 80, sum_head() + fma_ops(64, 96) + max_ops(64, 82) + sum_tail(211))
     read_v(offn)
     ins("s_add_u32 s64, s64, 1")
 
@@ -287,6 +305,8 @@ def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jn, l
     ins(f"s_cbranch_scc1 {label}_nm")
     mask_body(e, c_reg, span_reg)
     ins(f"{label}_nm:")
+    for i in range(16):  # log2-domain scores (masked keys stay -inf: c > 0)
+        ins(f"v_mul_f32 v{E[i]}, %[cs], v{E[i]}")
     ins(f"v_max3_f32 v200, v{E[0]}, v{E[1]}, v{E[2]}")
     for i in range(3, 15, 2):
         ins(f"v_max3_f32 v200, v200, v{E[i]}, v{E[i + 1]}")
@@ -301,8 +321,7 @@ def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jn, l
     ins(f"v_mul_f32 v{l}, v{l}, v203")
     for i in range(32):
         ins(f"v_mul_f32 v{o_base + i}, v{o_base + i}, v203")
-    for i in range(16):
-        ins(f"v_mov_b32 v{bias_base + i}, v204")
+    ins(f"v_mov_b32 v{bias_base}, v204")
     for i in range(16):
         ins(f"v_add_f32 v{E[i]}, v{E[i]}, v204")
 
@@ -331,7 +350,7 @@ def generate():
     read_k(0)
     read_v(0)
     ins("s_waitcnt lgkmcnt(8)")
-    mfma("64:79", K_OPS[0], "128:131", "v[96:111]")
+    mfma("64:79", K_OPS[0], "128:131", "0")
     for t in (1, 2, 3):
         mfma("64:79", K_OPS[t], f"{128 + 4 * t}:{131 + 4 * t}", "v[64:79]")
     ins("s_nop 7")
@@ -344,7 +363,7 @@ def generate():
     ins("s_cbranch_scc1 pro_ma_ok")
     ins("s_call_b64 s[66:67], pff_mask_a")
     ins("pro_ma_ok:")
-    for x in max_ops(64, 82):
+    for x in fma_ops(64, 96) + max_ops(64, 82):
         ins(x)
     # ---- main loop: four tiles (eight chunks) per pass; buffers and entry slots fixed ----
     # (the chunk count may be odd: the loop can end after a tile's first chunk)

@@ -1253,10 +1253,11 @@ int moearc_attn_decode_batched_noalloc(moearc_ctx *c, void *out, unsigned int ou
 
 namespace {
 
-// The single-f16 kernels pre-scale Q by scale*log2(e) in f16, which stays in range for
-// |scale*log2(e)| <= 1 (every softmax scale up to 0.69); larger scales take the precise kernels.
+// The single-f16 kernels multiply each f32 score by scale*log2(e) after masking keys with -inf,
+// which needs a positive finite scale; any other scale takes the precise kernels.
 bool prefill_is_fast(const moearc_ctx *c, float scale) {
-    return !c->prefill_precise && std::fabs(scale * 1.4426950408889634f) <= 1.0f;
+    const float c2 = scale * 1.4426950408889634f;
+    return !c->prefill_precise && c2 > 0.0f && c2 <= 3.0e38f;
 }
 
 // moearc_attn_prefill's checks and launch; out_lo (f16 output, default kernels only) also takes

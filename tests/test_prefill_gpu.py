@@ -1,9 +1,10 @@
 """Chunked-prefill parity on the GPU against the oracle (row i == decode at n_kv = pos0+i+1).
 
 Golden fixtures pin a small gpt-oss-shaped chunk; the oracle covers every GQA group the kernel
-supports, windowed and full layers, ragged chunk ends and page sizes; at BASELINE config 4's full
-size (2048 new tokens after 2048 cached) six rows of every 32-token query tile -- its first and last
-among them -- are compared with the oracle and every row is checked for finiteness. The bar is the north star's: max-abs error <= 2e-3 on the output.
+supports, windowed and full layers, ragged chunk ends and page sizes, score jumps and large scores;
+at BASELINE config 4's full size (2048 new tokens after 2048 cached) every output is compared with
+the oracle, also with config 5's stress pattern. The bar is the north star's: max-abs error <= 2e-3
+on the output.
 """
 from __future__ import annotations
 
@@ -64,9 +65,7 @@ def test_shapes_against_oracle(ctx, group, n_q, pos0, pt, n_swa):
 
 
 # K rows scaled by small factors early and larger ones later: the scores jump by more than 8 in
-# base-2 units (the rescale threshold) where a row first sees the scaled-up keys, with |scores| kept
-# within the default kernels' accuracy (they round the scaled Q to f16: an emulation of their
-# arithmetic puts these cases at 0.9e-3 to 1.5e-3 max-abs error; keys scaled by 6 reach 5e-3).
+# base-2 units (the rescale threshold) where a row first sees the scaled-up keys.
 JUMPS = {
     "late": [(0, 600, 0.02), (600, 4096, 2.0)],
     "early": [(0, 32, 0.02), (32, 128, 1.8), (128, 4096, 0.3)],
@@ -91,6 +90,26 @@ def test_score_jumps_against_oracle(ctx, group, n_q, pos0, n_swa, jumps):
     got = _run(ctx, pc, n_swa)
     assert np.isfinite(got).all()
     _report(f"prefill jumps group={group} n_q={n_q} pos0={pos0} n_swa={n_swa} {jumps}", got, want)
+
+
+# Large scores: the kernels' arithmetic must not lose accuracy as |q|.|k| grows (scaling q by
+# scale*log2(e) in f16 before the product, as an earlier form of the default kernels did, reaches
+# 6e-3 max-abs error on "band6" and 1e-2 on "spike8"). "band6": keys 600 onward scaled by 6;
+# "spike8": BASELINE config 5's stress pattern, 1% of K rows scaled by 8; "all3": every key by 3.
+STRESS = {"band6": dict(boost=[(600, 1 << 20, 6.0)]), "spike8": dict(spike_frac=0.01),
+          "all3": dict(boost=[(0, 1 << 20, 3.0)])}
+
+
+@pytest.mark.parametrize("n_swa", [0, 128])
+@pytest.mark.parametrize("stress", sorted(STRESS))
+def test_large_scores_against_oracle(ctx, stress, n_swa):
+    pc = fx.prefill_case(0x5D0 + len(stress), n_q=256, pos0=1792, pt=32, **STRESS[stress])
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q, pc.pos0,
+                               n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale), sinks=pc.sinks,
+                               n_threads=16)
+    got = _run(ctx, pc, n_swa)
+    assert np.isfinite(got).all()
+    _report(f"prefill {stress} n_q=256 pos0=1792 n_swa={n_swa}", got, want)
 
 
 @pytest.mark.parametrize("precise", [False, True])
@@ -139,31 +158,35 @@ def test_precise_variant_against_oracle(monkeypatch):
             _report(f"precise prefill n_swa={n_swa}", got[g["rows"]], g["expected"], 1e-5)
 
 
-# Rows of config 4 compared with the oracle: residues modulo 32, the default kernel's query tile
-# (256 rows per work-group / group 8 = 32 tokens). Every tile's first and last row (0, 31), the rows
-# either side of the 16-token mid-point (15, 16), and rows 1 and 30; with pos0 = 2048 these are also
-# the rows whose causal diagonal (and, at n_swa = 128, window start) falls on the first, second,
-# second-to-last and last key of a 32-key chunk, where the kernel's per-chunk mask tests switch.
-C4_RESIDUES = (0, 1, 15, 16, 30, 31)
+def _config4(seed, **kw):
+    # BASELINE config 4: 2048 new tokens after 2048 cached, 64q/8kv, d64, f16, sinks
+    return fx.prefill_case(seed, n_q=2048, pos0=2048, pt=256, **kw)
 
 
 @pytest.mark.parametrize("n_swa", [0, 128])
 def test_config4_full_size(ctx, n_swa):
-    # BASELINE config 4: 2048 new tokens after 2048 cached, 64q/8kv, d64, f16, sinks
-    pc = fx.prefill_case(0xC4, n_q=2048, pos0=2048, pt=256)
-    want = np.full((pc.n_q, pc.H, pc.D), np.nan, np.float32)
-    for r in C4_RESIDUES:
-        part = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q,
-                                   pc.pos0, n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale),
-                                   sinks=pc.sinks, rows=(r, 2048, 32), n_threads=16)
-        want[r::32] = part[r::32]
-    rows = np.sort(np.concatenate([np.arange(r, 2048, 32) for r in C4_RESIDUES]))
-    assert rows.size == 64 * len(C4_RESIDUES) and np.isfinite(want[rows]).all()
+    """Every one of the 2048 x 64 x 64 outputs of config 4 against the oracle, f32 and f16 out."""
+    pc = _config4(0xC4)
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q, pc.pos0,
+                               n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale), sinks=pc.sinks,
+                               n_threads=16)
+    assert np.isfinite(want).all()
     for out_type in (OUT_F32, OUT_F16):
         got = _run(ctx, pc, n_swa, out_type=out_type)
         assert np.isfinite(got).all()
-        _report(f"config 4 n_swa={n_swa} out={'f16' if out_type else 'f32'} ({rows.size} rows, "
-                f"first and last of every 32-token tile)", got[rows], want[rows])
+        _report(f"config 4 n_swa={n_swa} out={'f16' if out_type else 'f32'} (all 2048 rows)", got, want)
+
+
+@pytest.mark.parametrize("n_swa", [0, 128])
+def test_config4_full_size_spikes(ctx, n_swa):
+    """Config 4 with config 5's stress pattern (1% of K rows scaled by 8), every output."""
+    pc = _config4(0xC45, spike_frac=0.01)
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q, pc.pos0,
+                               n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale), sinks=pc.sinks,
+                               n_threads=16)
+    got = _run(ctx, pc, n_swa)
+    assert np.isfinite(got).all()
+    _report(f"config 4 spikes n_swa={n_swa} (all 2048 rows)", got, want)
 
 
 def test_refusals(ctx):
