@@ -219,6 +219,7 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
             result["prefill_graph"] = bench_prefill_graph(ctx, hip)
             result["rope_graph"] = bench_rope_append_graph(ctx, hip)
         result["configs"] = bench_configs(ctx, hip, steps, warmup)
+        result["headline_step"] = bench_headline(ctx, hip)
         result["projections"] = bench_matvec(ctx, hip, steps=max(20, steps))
         result["block_chunk"] = bench_block(ctx, hip)
         result["chunk_projections"] = bench_matmul(ctx, hip)
@@ -252,6 +253,8 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
     result["launch_overhead"] = launch_overhead()
     if not skip_cpu:
         result["cpu"] = cpu_baseline(kp, vp, bt, q, sinks)
+        if not skip_prefill:
+            result["cpu_prefill"] = cpu_prefill_baseline()
     return result
 
 
@@ -491,28 +494,19 @@ def mv_launch(ctx, ty, rows, cols, fused, inputs, i):
 
 def bench_matvec(ctx, hip, steps):
     """Each projection case as a captured graph of `steps` launches (each on the next weight copy),
-    replayed once untimed and once between HIP events: the per-launch time excludes host
-    submission, which for kernels this short would otherwise dominate. Achieved bandwidth counts
-    the algorithmic bytes (every weight byte once, the activation, biases and outputs)."""
+    replayed REPS times (the first discarded, bench/PROTOCOL.md:73-87): the per-launch time excludes
+    host submission, which for kernels this short would otherwise dominate. `us` is the median over
+    the repetitions; achieved bandwidth counts the algorithmic bytes (every weight byte once, the
+    activation, biases and outputs)."""
     res = {}
     for label, ty, rows, cols, fused in MV_CASES:
         inputs = mv_inputs(ctx, ty, rows, cols, fused, 128)
-        mv_launch(ctx, ty, rows, cols, fused, inputs, 0)
-        ctx.sync()
-        graph, exe = hip.capture(ctx.stream, lambda: [mv_launch(ctx, ty, rows, cols, fused, inputs, i)
-                                                      for i in range(steps)])
-        e0, e1 = hip.event(), hip.event()
-        hip.launch(exe, ctx.stream)
-        ctx.sync()
-        hip.record(e0, ctx.stream)
-        hip.launch(exe, ctx.stream)
-        hip.record(e1, ctx.stream)
-        ctx.sync()
-        us = hip.elapsed_ms(e0, e1) * 1e3 / steps
-        hip.destroy(graph, exe)
+        st = rep_stats(graph_timed(hip, ctx, lambda i: mv_launch(ctx, ty, rows, cols, fused, inputs, i),
+                                   steps, 2))
+        us = st["median"]
         nbytes = inputs[4] + cols * 4 + sum(rows) * 4 * (2 if fused else 1)
         gbs = nbytes / us / 1e3
-        res[label] = {"us": round(us, 2), "bytes": nbytes, "hbm_gbs": round(gbs, 0),
+        res[label] = {"us": round(us, 2), "us_reps": st, "bytes": nbytes, "hbm_gbs": round(gbs, 0),
                       "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
         del inputs
     return res
@@ -529,8 +523,9 @@ MM_CASES = [
 
 def bench_matmul(ctx, hip, steps=5):
     """Each chunk product as a captured graph of `steps` launches (the activation split included),
-    replayed once untimed and once between HIP events. TFLOP/s counts 2 * tokens * rows * cols;
-    the kernel issues twice that on the f16 MFMA (the activation's hi and lo halves)."""
+    replayed REPS times (the first discarded); `us` is the median per launch. TFLOP/s counts
+    2 * tokens * rows * cols; the kernel issues twice that on the f16 MFMA (the activation's hi and
+    lo halves)."""
     from moearc_amd import QuantType
     res = {}
     rng = np.random.default_rng(0x33A)
@@ -546,21 +541,11 @@ def bench_matmul(ctx, hip, steps=5):
         dx = ctx.upload(rng.standard_normal((n_tok, cols)).astype(np.float32))
         db = ctx.upload(rng.standard_normal(rows).astype(np.float32))
         dy = ctx.alloc(n_tok * rows * 4)
-        ctx.matmul_q(ty, dy, dw, dx, db, n_tok, rows, cols)
-        ctx.sync()
-        graph, exe = hip.capture(ctx.stream, lambda: [ctx.matmul_q(ty, dy, dw, dx, db, n_tok, rows, cols)
-                                                      for _ in range(steps)])
-        e0, e1 = hip.event(), hip.event()
-        hip.launch(exe, ctx.stream)
-        ctx.sync()
-        hip.record(e0, ctx.stream)
-        hip.launch(exe, ctx.stream)
-        hip.record(e1, ctx.stream)
-        ctx.sync()
-        us = hip.elapsed_ms(e0, e1) * 1e3 / steps
-        hip.destroy(graph, exe)
+        st = rep_stats(graph_timed(hip, ctx, lambda i: ctx.matmul_q(ty, dy, dw, dx, db, n_tok, rows, cols),
+                                   steps, 1))
+        us = st["median"]
         tflops = 2.0 * n_tok * rows * cols / us / 1e6
-        res[label] = {"us": round(us, 1), "tflops": round(tflops, 1),
+        res[label] = {"us": round(us, 1), "us_reps": st, "tflops": round(tflops, 1),
                       "mfma_f16_frac_issued": round(2 * tflops / MFMA_F16_PEAK_TFLOPS, 4),
                       "us_per_token": round(us / n_tok, 3)}
     return res
@@ -596,23 +581,27 @@ def bench_block(ctx, hip, n_tok=128):
     from moearc_amd import DeviceView
     views = [(DeviceView(h, t * E * 4, E * 4), DeviceView(x, t * E * 4, E * 4), DeviceView(pos, 4 * t, 4),
               DeviceView(pg, 4 * t, 4), DeviceView(sl, 4 * t, 4)) for t in range(n_tok)]
-    res = {}
-    for label in ("chunked", "token_by_token", "chunked"):
-        ctx.sync()
-        e0, e1 = hip.event(), hip.event()
-        hip.record(e0, ctx.stream)
-        if label == "chunked":
-            ctx.attn_block_chunk(desc, h, x, n_tok, 0, pos, pg, sl)
-        else:
-            for t, (hv, xv, pv, gv, sv) in enumerate(views):
-                ctx.attn_block_chunk(desc, hv, xv, 1, t, pv, gv, sv)
-        hip.record(e1, ctx.stream)
-        ctx.sync()
-        res[label] = hip.elapsed_ms(e0, e1) * 1e3
-    return {"tokens": n_tok, "chunked_us": round(res["chunked"], 1),
-            "token_by_token_us": round(res["token_by_token"], 1),
-            "chunked_us_per_token": round(res["chunked"] / n_tok, 2),
-            "token_by_token_us_per_token": round(res["token_by_token"] / n_tok, 2)}
+    res = {"chunked": [], "token_by_token": []}
+    for _ in range(REPS):  # alternating, each REPS times; the first of each discarded
+        for label in ("chunked", "token_by_token"):
+            ctx.sync()
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0, ctx.stream)
+            if label == "chunked":
+                ctx.attn_block_chunk(desc, h, x, n_tok, 0, pos, pg, sl)
+            else:
+                for t, (hv, xv, pv, gv, sv) in enumerate(views):
+                    ctx.attn_block_chunk(desc, hv, xv, 1, t, pv, gv, sv)
+            hip.record(e1, ctx.stream)
+            ctx.sync()
+            res[label].append(hip.elapsed_ms(e0, e1) * 1e3)
+    ch, tbt = rep_stats(res["chunked"]), rep_stats(res["token_by_token"])
+    return {"tokens": n_tok, "timing": "HIP events around the call, host submission included; "
+            "median of REPS repetitions after a discarded first",
+            "chunked_us": round(ch["median"], 1), "chunked_us_reps": ch,
+            "token_by_token_us": round(tbt["median"], 1), "token_by_token_us_reps": tbt,
+            "chunked_us_per_token": round(ch["median"] / n_tok, 2),
+            "token_by_token_us_per_token": round(tbt["median"] / n_tok, 2)}
 
 
 def host_info():
@@ -746,6 +735,128 @@ def bench_configs(ctx, hip, steps, warmup):
     return out
 
 
+# The reference's own headline quantity for this path: `attn.attend` (the attention call of
+# moe.rs:2043-2061) summed over one decode step of gpt-oss-120b's 36 blocks -- 18 with a 128-token
+# sliding window, 18 full causal -- at B=1 and context depth d, measured on an Arc B580 with
+# MOEARC_SYNC_EACH=1 (every call synchronised): 15.21 ms at 512 and 49.51 ms at 2048
+# (bench/results/2026-09-06-moearc-sync-each.txt:17-18); 187.3 ms at 8192 is the reference's own
+# extrapolation from its fit 3.77 + 0.02240 d ms (bench/baselines/gpt-oss-120b.md:626), not a
+# measurement.
+HEADLINE_DEPTHS = (512, 2048, 8192)
+REF_ATTN_ATTEND_MS = {512: (15.21, "measured"), 2048: (49.51, "measured"),
+                      8192: (187.3, "the reference's extrapolation 3.77 + 0.02240 d")}
+
+
+def bench_headline(ctx, hip):
+    """One decode step's 36 attention calls (blocks alternate SWA-128 and full causal, as gpt-oss
+    declares its window on alternating blocks) at B=1 and depths 512, 2048 and 8192: 64 q / 8 KV
+    heads, head_dim 64, f16 KV in 256-token pages, per-head sinks, f32 q and output (the engine's
+    decode surface, moe.rs:2043-2061). Each full block reads its own pool through its own random
+    page permutation; each windowed block its own two-page ring through the cyclic table (the
+    window's 128 keys touch at most two consecutive pages). Enough independent sets of the 36
+    blocks rotate for a replay cycle to touch more than 512 MiB, so the 256 MB Infinity Cache
+    serves no repeats. Two protocols, each REPS repetitions with the first discarded:
+    graph replay of the steps (device time per step, launches back to back) and sync-each (a
+    host wall clock around every call and its stream synchronisation, summed over the step: the
+    reference's MOEARC_SYNC_EACH=1 protocol, here with the Python binding's call overhead in
+    it)."""
+    from moearc_amd import KvType
+    rng = np.random.default_rng(0x36B)
+    row = G * D
+    q = ctx.upload(rng.standard_normal(H * D).astype(np.float32))
+    sinks = [ctx.upload(rng.standard_normal(H).astype(np.float32)) for _ in range(36)]
+    out = ctx.alloc(H * D * 4)
+    bits = rng.integers(0, 1 << 16, size=(8192 // PT) * PT * row, dtype=np.uint16) & np.uint16(0xBFFF)
+    res = {}
+    for d in HEADLINE_DEPTHS:
+        n_pages = -(-d // PT)
+        pool_bytes = lambda pages: pages * PT * row * 2
+        per_set = 18 * 2 * pool_bytes(n_pages) + 18 * 2 * pool_bytes(2)
+        n_sets = max(2, -(-(512 << 20) // per_set))
+        sets = []
+        for _ in range(n_sets):
+            blocks = []
+            for blk in range(36):
+                if blk % 2 == 0:  # windowed block: ring of two pages, cyclic table
+                    pages, kv_begin = 2, max(0, d - 128)
+                    table = (np.arange(n_pages) % 2).astype(np.uint32)
+                else:
+                    pages, kv_begin = n_pages, 0
+                    table = rng.permutation(n_pages).astype(np.uint32)
+                kp, vp = ctx.upload(bits[:pages * PT * row]), ctx.upload(bits[:pages * PT * row])
+                blocks.append((kp, vp, ctx.upload(table), sinks[blk], kv_begin))
+            sets.append(blocks)
+
+        def step(i):
+            for kp, vp, table, sk, kv_begin in sets[i % n_sets]:
+                ctx.attn_decode_ext(out, q, kp, vp, table, sk, H, G, D, kv_begin, d, PT, 0.125, KvType.F16)
+
+        graph = rep_stats(graph_timed(hip, ctx, step, n_sets, 1))
+        sync_each = []
+        for r in range(REPS):
+            total = 0.0
+            for kp, vp, table, sk, kv_begin in sets[r % n_sets]:
+                t0 = time.perf_counter()
+                ctx.attn_decode_ext(out, q, kp, vp, table, sk, H, G, D, kv_begin, d, PT, 0.125, KvType.F16)
+                ctx.sync()
+                total += time.perf_counter() - t0
+            sync_each.append(total * 1e3)
+        se = rep_stats(sync_each)
+        ref_ms, ref_kind = REF_ATTN_ATTEND_MS[d]
+        full_bytes = 18 * (d * 2 * row * 2 + H * D * 8 + H * 4 + 4 * n_pages)
+        swa_bytes = 18 * (min(128, d) * 2 * row * 2 + H * D * 8 + H * 4 + 8)
+        res[str(d)] = {
+            "us_per_step_graph": round(graph["median"], 2), "graph_reps": graph,
+            "ms_per_step_sync_each": round(se["median"], 4), "sync_each_reps": se,
+            "reference_ms_per_step_b580": ref_ms, "reference_kind": ref_kind,
+            "speedup_vs_reference_sync_each": round(ref_ms / se["median"], 1),
+            "speedup_vs_reference_graph": round(ref_ms * 1e3 / graph["median"], 1),
+            "algorithmic_bytes_per_step": full_bytes + swa_bytes,
+            "gbs_graph": round((full_bytes + swa_bytes) / graph["median"] / 1e3, 1),
+            "sets_rotated": n_sets}
+        del sets
+    return res
+
+
+def cpu_prefill_baseline():
+    """The reference engine's prefill on the CPU: one decode call per prompt token
+    (session.rs:378-381, moe.rs:1856-1862), here the oracle (the f64 CPU twin, reference.rs:821-873,
+    plus the sink) on one thread, over config 4's 2048 tokens after 2048 cached, for both layer types.
+    Bounded sample: evenly spaced rows of the chunk (16 of the full-causal layer, 64 of the
+    SWA-128 layer), REPS passes with the first discarded; the per-key cost of the sample is
+    extrapolated to all 2048 rows (full causal: the exact key count PF_PAIRS_FULL; SWA-128: 128
+    keys per row). Inputs: the same seeded case as the GPU prefill (tests/fixtures.py)."""
+    import fixtures as fx
+    from oracle import oracle
+    oracle.lib()
+    pc = fx.prefill_case(0xC4, n_q=PF_NQ, pos0=PF_POS0, pt=PT)
+    qf = pc.qp.astype(np.float32).reshape(PF_NQ, H * D)
+    bt = np.ascontiguousarray(pc.bt, np.uint32)
+    out = {}
+    for name, n_swa, rows in (("full", 0, np.arange(64, PF_NQ, PF_NQ // 16)),
+                              ("swa128", 128, np.arange(16, PF_NQ, PF_NQ // 64))):
+        per_pass, keys_sample = [], 0
+        for r in range(REPS):
+            keys_sample = 0
+            t0 = time.perf_counter()
+            for i in rows:
+                n_kv = PF_POS0 + int(i) + 1
+                kv_begin = max(0, n_kv - n_swa) if n_swa else 0
+                oracle.attn_decode(qf[i], pc.k_raw, pc.v_raw, bt, H, G, D, kv_begin, n_kv, PT, 0.125,
+                                   kv_type=1, sinks=pc.sinks)
+                keys_sample += n_kv - kv_begin
+            per_pass.append(time.perf_counter() - t0)
+        st = rep_stats(per_pass)
+        keys_total = PF_PAIRS_FULL if n_swa == 0 else PF_NQ * n_swa
+        layer_s = st["median"] / keys_sample * keys_total
+        out[name] = {"seconds_per_layer_call": round(layer_s, 3),
+                     "tokens_per_s": round(PF_NQ / layer_s, 1),
+                     "sample": f"{len(rows)} evenly spaced rows of 2048 ({keys_sample} of {keys_total} "
+                               f"row-keys), extrapolated by key count",
+                     "sample_seconds": st}
+    return {**out, "cores": 1, "kind": "port", **host_info()}
+
+
 def only(what, steps, warmup):
     """Runs one workload eagerly with no timing of its own, for rocprofv3 to wrap:
     decode_graph (the main line's timed region: C2 steps in one graph, replayed), decode (C2), prefill (C4 full then SWA-128),
@@ -811,6 +922,10 @@ def only(what, steps, warmup):
             hip = Hip()
             for _ in range(max(1, steps)):
                 bench_block(ctx, hip)
+        elif what == "headline":
+            r = bench_headline(ctx, Hip())
+            print(json.dumps({k: (v["us_per_step_graph"], v["ms_per_step_sync_each"]) for k, v in r.items()}),
+                  flush=True)
         elif what == "read_floor":
             bufs, out, nbytes = read_floor_inputs(ctx)
             for i in range(warmup + steps):
@@ -836,7 +951,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "prefill_graph", "rope_append", "matvec", "matmul",
-                                       "block", "read_floor", "copy"],
+                                       "block", "headline", "read_floor", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
@@ -931,6 +1046,12 @@ def main():
         line["prefill_swa128_us"] = pf["swa128"]["us"]
         line["prefill"] = pf
     line["configs"] = r["configs"]
+    line["headline_step"] = dict(
+        r["headline_step"],
+        what="the reference's attn.attend per decode step: 36 attention calls (18 SWA-128 + 18 full "
+             "causal, B=1) at context depth d; reference figures from an Arc B580 under "
+             "MOEARC_SYNC_EACH=1 (bench/results/2026-09-06-moearc-sync-each.txt:17-18, "
+             "bench/baselines/gpt-oss-120b.md:626); ms_per_step_sync_each is the same protocol here")
     line["launch_overhead"] = r["launch_overhead"]
     for k in ("projections", "block_chunk", "chunk_projections"):
         if k in r:
@@ -952,6 +1073,17 @@ def main():
             "multithread": {"threads": c["threads"], "us_per_call": c["mt_us"],
                             "value": round(C2_BYTES / c["mt_us"]["mean"] / 1e3, 3)},
         }
+    if "cpu_prefill" in r:
+        cp = r["cpu_prefill"]
+        line["cpu_baseline_prefill"] = {
+            "what": "config 4 prefill as the reference engine runs it on the CPU: one decode call per "
+                    "prompt token (session.rs:378-381), the f64 oracle on one thread; seconds per "
+                    "layer call of 2048 tokens, extrapolated from an evenly spaced row sample",
+            "full": cp["full"], "swa128": cp["swa128"], "cores": 1, "kind": "port",
+            "gpu_speedup_full": round(cp["full"]["seconds_per_layer_call"] * 1e6 / line["prefill_full_us"], 0)
+            if "prefill_full_us" in line else None,
+            "gpu_speedup_swa128": round(cp["swa128"]["seconds_per_layer_call"] * 1e6 / line["prefill_swa128_us"], 0)
+            if "prefill_swa128_us" in line else None}
     print(json.dumps(line), flush=True)
 
 
