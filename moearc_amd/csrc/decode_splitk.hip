@@ -176,7 +176,11 @@ __device__ __forceinline__ void decode_body(const uint16_t *k_pages, const uint1
                                             uint32_t geo0, uint32_t geo1, const DecodeArgs &a) {
     constexpr int WAVES = KB * WPK;
     constexpr uint32_t CHUNK = 32u * TILES * WPK;  // keys of one chunk of the split
-    __shared__ float o_lds[WAVES][16 * 64];
+    // a head's 64 partial outputs per row, rows 68 floats apart: the float4 writes of a 16-lane pass
+    // (16 heads, one channel quad each) then fall on 64 distinct banks (a 64-float stride put all
+    // 16 heads on the same 16 banks)
+    constexpr uint32_t OROW = 68;
+    __shared__ float o_lds[WAVES][16 * OROW];
     __shared__ float m_lds[WAVES][16];
     __shared__ float l_lds[WAVES][16];
 
@@ -321,7 +325,7 @@ __device__ __forceinline__ void decode_body(const uint16_t *k_pages, const uint1
     if (head_ok) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
-            *(float4_t *) (&o_lds[wave][n * 64u + 16u * mb + 4u * g]) = st.O[mb];
+            *(float4_t *) (&o_lds[wave][n * OROW + 16u * mb + 4u * g]) = st.O[mb];
     }
     if (g == 0) {
         m_lds[wave][n] = head_ok && active ? st.m : -INFINITY;
@@ -348,7 +352,7 @@ __device__ __forceinline__ void decode_body(const uint16_t *k_pages, const uint1
             const float mw = m_lds[ww][hn];
             const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);  // a wave without keys drops out
             L += l_lds[ww][hn] * f;
-            acc += o_lds[ww][hn * 64u + d] * f;
+            acc += o_lds[ww][hn * OROW + d] * f;
         }
         const uint32_t hh = kv2 * group + hn;
         if (single) {
