@@ -21,7 +21,8 @@ Register map (VGPRs):
   v216-v217          LDS addresses of the V^T operand reads
   v218 v219 v220 v221  mask parameters c_A, span_A, c_B, span_B (key offset of chunk 0 relative to
                      the row's window start; row position minus window start)
-  v222-v229          block-table entries of four tiles (two per tile: this lane's two copy keys)
+  v222-v229          block-table entries of four tiles (two per tile: this lane's two copy keys;
+                     tiles 0 and 1 are inputs of the statement)
   v230-v233          copy offsets within a tile, uniform path (K copy 0, 1, V copy 0, 1)
   v234-v241          per-lane 64-bit copy bases (K copy 0, 1, V copy 0, 1): pages base + chunk
   v242               this lane's first copy key within a tile (16 * wave + lane / 8)
@@ -330,12 +331,9 @@ def generate():
     # m0 (the LDS base of the copies) is the compiler's register: saved here, restored at the one
     # exit, so the statement leaves it as it found it and needs no m0 clobber
     ins("s_mov_b32 s86, m0")
-    # ---- prologue: entries of tiles 0 and 1, their copies, entries of tiles 2 and 3, step 0 ----
-    ins("s_mov_b32 s80, 0")
-    pid_load(0, 80, "pro_p0")
-    ins("s_mov_b32 s80, 1")
-    pid_load(1, 80, "pro_p1")
-    ins("s_waitcnt vmcnt(0)")
+    # ---- prologue: copies of tiles 0 and 1 (their entries arrive as inputs in v222-v225, loaded
+    # beside the query rows before the statement, so the two loads share one memory round trip),
+    # entries of tiles 2 and 3, step 0 ----
     ins("s_mov_b32 s80, 0")
     copy_tile(0, 80, 0, "pro_c0")
     ins("s_mov_b32 s80, 2")
