@@ -14,9 +14,11 @@ Register map (VGPRs):
   v32-v47 v48-v63    O of block B                              v144-v159  Q of block B
   v64-v79 v80-v95    S of blocks A and B (exponents, weights)  v160-v175  K operands of a chunk
   v96 v112           bias 7 - m of blocks A and B (per row)    v176-v191  V^T operands of a chunk
-                     (v97-v111 and v113-v127 are not used)
+  v100-v103 v104-v107  row sums of blocks A and B (16x16x32 MFMA accumulators: register 0 of lane
+                     n < 32 holds row n's sum, every other element stays 0)
+  v108-v111          the selection operand of the row-sum MFMAs (v97-v99, v113-v127 are not used)
   v192-v199          P operands (one block at a time)          v200-v207  temporaries
-  v208 v209          reference m of A, B                       v210 v211  row sums l of A, B
+  v208 v209          reference m of A, B                       v210 v211  unused
   v212-v215          LDS addresses of the K operand reads (buffer 0, chunk 0)
   v216-v217          LDS addresses of the V^T operand reads
   v218 v219 v220 v221  mask parameters c_A, span_A, c_B, span_B (key offset of chunk 0 relative to
@@ -76,27 +78,6 @@ def fma_ops(e, bias):
     return [f"v_fma_f32 v{e + i}, v{e + i}, %[cs], v{bias}" for i in range(16)]
 
 
-def mix(d, p):
-    """v[d] = lo + hi of the f16 pair in v[p], in f32 (exact: two f16 values)."""
-    return f"v_fma_mix_f32 v{d}, v{p}, 1.0, v{p} op_sel:[0,0,1] op_sel_hi:[1,0,1]"
-
-
-def sum_head():
-    """Row sum of a block's weights as the P.V product sees them (the f16 P operands in v192-v199,
-    so that the normalisation divides by the sum of the very weights the output was formed with):
-    pair sums of v192-v197, each placed after the conversion that writes its pair (extras 1-4 after
-    v192-v195, extras 5-6 after v196-v197)."""
-    return [mix(200 + k, 192 + k) for k in range(6)]
-
-
-def sum_tail(l):
-    """The rest of the row sum: pair sums of v198, v199 (converted before the third MFMA), the tree
-    over v200-v207, and l += the chunk's sum."""
-    a = lambda d, x, y: f"v_add_f32 v{d}, v{x}, v{y}"
-    return [mix(206, 198), mix(207, 199), a(200, 200, 201), a(202, 202, 203), a(204, 204, 205),
-            a(206, 206, 207), a(200, 200, 202), a(204, 204, 206), a(200, 200, 204), a(l, l, 200)]
-
-
 def max_ops(e, flag):
     """Largest exponent input of v[e..e+15] (two chains in v244, v245: free outside tile steps and
     the mask and rescale paths) compared with the rescale threshold: s[flag:flag+1] = lanes whose
@@ -109,32 +90,40 @@ def max_ops(e, flag):
             f"v_cmp_le_f32_e64 s[{flag}:{flag + 1}], %[thr], v244"]
 
 
-def pv(o0, o1, e, extra):
-    """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7], with
-    the VALU instructions `extra` (not writing P or the V^T operands) spread between the MFMAs: 4
-    before the first (they cover the VALU-write -> MFMA-read wait), then the rest in three equal
-    groups after the first three and a smaller one after the last. The chunk places the other
-    block's exponent inputs and rescale test (16 FMAs, a max3 tree and a compare) from the seventh
-    on: after the first MFMA, at least 20 wait states after the MFMAs that wrote the scores."""
+def rowsum(lsum, p):
+    """l += the chunk's weights of every row, on the matrix core: a 16x16x32 MFMA whose B operand is
+    the block's P^T registers read as 32 keys x 16 columns (lane l then holds row l % 32's keys
+    8 (l / 32) .. + 7 of the 16-key half, in column l % 16, k-slots 8 (l / 16) .. + 7) and whose A
+    operand (v108-v111) has ones in row 0 over the k-slots of lanes 0-15 and 32-47 (rows 0-15) and in
+    row 4 over those of lanes 16-31 and 48-63 (rows 16-31): D[0][n] is row n's sum and D[4][n] row
+    n + 16's, which the accumulator layout places in register 0 of lanes n and n + 16."""
+    ins(f"v_mfma_f32_16x16x32_f16 v[{lsum}], v[108:111], v[{p}], v[{lsum}]")
+
+
+def pv(o0, o1, e, extra, lsum, pad=0):
+    """O_0 += V^T(0, s) . P_s, O_1 += V^T(1, s) . P_s, P_s = f16 of weights v[e + 8s .. + 7], and
+    the row sums l += P_s (`rowsum`, into v[lsum]), with the VALU instructions `extra` (not writing
+    P or the V^T operands) spread between the MFMAs in four equal groups, one after each P.V MFMA.
+    All eight P packs come first, so the first group -- the other block's exponent inputs, 16 FMAs
+    on the scores of the previous region's MFMAs -- starts after the first P.V MFMA, at least 20
+    wait states after those MFMAs (`pad` wait states more where the region before is short)."""
     cvt = lambda d, a, b: ins(f"v_cvt_pk_f16_f32 v{d}, v{e + a}, v{e + b}")
     extra = list(extra)
     take = lambda n: [ins(extra.pop(0)) for _ in range(min(n, len(extra)))]
-    group = max(6, -(-(len(extra) - 4) // 4) + 1)
+    group = -(-len(extra) // 4)
     cvt(192, 0, 1); cvt(193, 2, 3); cvt(194, 4, 5); cvt(195, 6, 7)
-    if len(extra) < 2:
-        ins("s_nop 2")  # VALU write -> MFMA read
-    take(4)
+    cvt(196, 8, 9); cvt(197, 10, 11); cvt(198, 12, 13); cvt(199, 14, 15)
     mfma(o0, "176:179", "192:195", f"v[{o0}]")
-    cvt(196, 8, 9); cvt(197, 10, 11)
+    if pad:
+        ins(f"s_nop {pad - 1}")
     take(group)
     mfma(o1, "184:187", "192:195", f"v[{o1}]")
-    cvt(198, 12, 13); cvt(199, 14, 15)
-    if len(extra) < 2:
-        ins("s_nop 2")
+    rowsum(lsum, "192:195")
     take(group)
     mfma(o0, "180:183", "196:199", f"v[{o0}]")
     take(group)
     mfma(o1, "188:191", "196:199", f"v[{o1}]")
+    rowsum(lsum, "196:199")
     take(len(extra))
 
 
@@ -227,10 +216,11 @@ def tile_step(si, label):
 
 
 def chunk(bi, ci, label):
-    """Chunk j = s64 (32 keys): R1 S_B(j) MFMAs | exponentials of A(j); R2 O_A += V(j)^T P_A(j) |
-    row sum of A(j), rescale test of S_B(j); R3 S_A(j + 1) | exponentials of B(j); R4 O_B +=
-    V(j)^T P_B(j) | row sum of B(j), rescale test of S_A(j + 1). Each rescale test is taken at
-    the start of the next region that exponentiates the block, long after its compare."""
+    """Chunk j = s64 (32 keys): R1 S_B(j) MFMAs | exponentials of A(j); R2 O_A += V(j)^T P_A(j)
+    and A(j)'s row sums (MFMAs) | f16 P_A(j), exponent inputs and rescale test of S_B(j); R3
+    S_A(j + 1) | exponentials of B(j); R4 O_B += V(j)^T P_B(j) and B(j)'s row sums | f16 P_B(j),
+    exponent inputs and rescale test of S_A(j + 1). Each rescale test is taken at the start of the
+    next region that exponentiates the block, long after its compare."""
     bn = (bi + 1) % NBUF if ci else bi
     off = bi * BUF + 4096 * ci
     offn = bn * BUF + 4096 * (ci ^ 1)
@@ -249,14 +239,14 @@ def chunk(bi, ci, label):
     ool_block(f"{label}_ra", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_rescale_a"], f"{label}_a_ok")
     qk_exp("80:95", 144, 64)
     read_k(offn)
-    # R2: mask of S_B(j); O_A += V(j)^T . P_A(j) | row sum of A(j), rescale test of S_B(j)
+    # R2: mask of S_B(j); O_A += V(j)^T . P_A(j), row sums of A(j) | exponent inputs and rescale test of S_B(j)
     ins("s_waitcnt lgkmcnt(4)")
     ins("s_sub_u32 s79, s64, %[jlob]")
     ins("s_cmp_ge_u32 s79, %[jnb]")
     ins(f"s_cbranch_scc1 {label}_mb")
     ins(f"{label}_mb_ok:")
     ool_block(f"{label}_mb", ["s_mov_b32 s78, s64", "s_call_b64 s[66:67], pff_mask_b"], f"{label}_mb_ok")
-    pv("0:15", "16:31", 64, sum_head() + fma_ops(80, 112) + max_ops(80, 84) + sum_tail(210))
+    pv("0:15", "16:31", 64, fma_ops(80, 112) + max_ops(80, 84), "100:103")
     # R3: S_A(j + 1) | weights of B(j)
     ins("s_cmp_lg_u64 s[84:85], 0")
     ins(f"s_cbranch_scc1 {label}_rb")
@@ -265,13 +255,13 @@ def chunk(bi, ci, label):
                               "s_call_b64 s[66:67], pff_rescale_b"], f"{label}_b_ok")
     ins("s_waitcnt lgkmcnt(0)")
     qk_exp("64:79", 128, 80)
-    # R4: mask of S_A(j + 1); O_B += V(j)^T . P_B(j) | row sum of B(j), rescale test of S_A(j + 1)
+    # R4: mask of S_A(j + 1); O_B += V(j)^T . P_B(j), row sums of B(j) | exponent inputs and rescale test of S_A(j + 1)
     ins("s_sub_u32 s79, s64, %[jloa1]")           # (j + 1) - jlo_A
     ins("s_cmp_ge_u32 s79, %[jna]")
     ins(f"s_cbranch_scc1 {label}_ma")
     ins(f"{label}_ma_ok:")
     ool_block(f"{label}_ma", ["s_add_u32 s78, s64, 1", "s_call_b64 s[66:67], pff_mask_a"], f"{label}_ma_ok")
-    pv("32:47", "48:63", 80, sum_head() + fma_ops(64, 96) + max_ops(64, 82) + sum_tail(211))
+    pv("32:47", "48:63", 80, fma_ops(64, 96) + max_ops(64, 82), "104:107", pad=4)
     read_v(offn)
     ins("s_add_u32 s64, s64, 1")
 
@@ -387,7 +377,7 @@ def generate():
     mask_body(80, 220, 221)
     ins("s_setpc_b64 s[66:67]")
     ins("pff_rescale_a:")  # K(j) is in v160-v175
-    rescale_body("64:79", 64, 128, 0, 96, 208, 210, 218, 219, "%[jloa]", "%[jna]", "ra")
+    rescale_body("64:79", 64, 128, 0, 96, 208, 100, 218, 219, "%[jloa]", "%[jna]", "ra")
     ins("s_setpc_b64 s[66:67]")
     ins("pff_rescale_b:")  # K(j + 1) is in v160-v175: read K(j) (LDS offset s76), then K(j + 1) (s77)
     for t in range(4):
@@ -396,7 +386,7 @@ def generate():
     for t in range(4):
         ins(f"ds_read_b128 v[{160 + 4 * t}:{163 + 4 * t}], v{244 + t}")
     ins("s_waitcnt lgkmcnt(0)")
-    rescale_body("80:95", 80, 144, 32, 112, 209, 211, 220, 221, "%[jlob]", "%[jnb]", "rb")
+    rescale_body("80:95", 80, 144, 32, 112, 209, 104, 220, 221, "%[jlob]", "%[jnb]", "rb")
     for t in range(4):
         ins(f"v_add_u32 v{244 + t}, s77, v{212 + t}")
     for t in range(4):
