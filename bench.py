@@ -217,6 +217,7 @@ def run(steps, warmup, skip_cpu=False, skip_prefill=False):
         # and right after them it measures ~15% slower
         if not skip_prefill:
             result["prefill_graph"] = bench_prefill_graph(ctx, hip)
+            result["mfma_floor"] = bench_mfma_floor(ctx, hip)
             result["rope_graph"] = bench_rope_append_graph(ctx, hip)
         result["configs"] = bench_configs(ctx, hip, steps, warmup)
         result["headline_step"] = bench_headline(ctx, hip)
@@ -334,6 +335,35 @@ def bench_prefill_graph(ctx, hip, calls=PF_SETS, warmup=3):
                              PF_POS0, n_swa, H, G, D, PT, 0.125, KvType.F16, out_type=OUT_F16)
         out[name] = rep_stats(graph_timed(hip, ctx, call, calls, warmup))
     return out
+
+
+# Matrix-core calibration beside the prefill: 512 work-groups of 4 waves (the prefill's grid and two
+# waves per SIMD), MF_ITERS rounds of 8 v_mfma_f32_32x32x16_f16 per wave on N(0,1) f16 operands, so a
+# call does about as much matrix work as the full-causal prefill and runs as long.
+MF_WGS, MF_ITERS = 512, 384
+MF_FLOPS = MF_WGS * 4 * MF_ITERS * 8 * 32768
+
+
+def bench_mfma_floor(ctx, hip, calls=12, warmup=3):
+    """moearc_mfma_floor timed as the prefill is (graph replay of `calls` calls, REPS replays, the
+    first discarded): the f16 MFMA rate this device sustains on data like the prefill's, with the
+    clock the power limit leaves it. Returns µs statistics and TFLOP/s."""
+    rng = np.random.default_rng(0xF100)
+    out = ctx.alloc(MF_WGS * 16)
+    res = {}
+    for name, data in (("normal", rng.standard_normal(MF_WGS * 16384).astype(np.float16)),
+                       ("zeros", np.zeros(MF_WGS * 16384, np.float16))):
+        src = ctx.upload(data)
+        st = rep_stats(graph_timed(hip, ctx, lambda i: ctx.mfma_floor(out, src, MF_WGS, MF_ITERS), calls, warmup))
+        tflops = MF_FLOPS / st["median"] / 1e6
+        res[name] = {"us": round(st["median"], 2), "us_reps": st, "tflops": round(tflops, 1),
+                     "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        del src
+    return {**res["normal"], "flops": MF_FLOPS, "zero_operands": res["zeros"],
+            "note": "moearc_mfma_floor: dense 32x32x16 f16 MFMA chains, 512 x 4 waves (two per SIMD, the "
+                    "prefill's occupancy), on N(0,1) operands (the practical MFMA ceiling for the "
+                    "prefill's data) and on zero operands (the same instructions with little switching: "
+                    "the gap is the power limit's clock)"}
 
 
 def bench_prefill(ctx, steps, warmup, graph=None, rope_graph=None):
@@ -926,6 +956,10 @@ def only(what, steps, warmup):
             r = bench_headline(ctx, Hip())
             print(json.dumps({k: (v["us_per_step_graph"], v["ms_per_step_sync_each"]) for k, v in r.items()}),
                   flush=True)
+        elif what == "mfma_floor":
+            r = bench_mfma_floor(ctx, Hip())
+            print(f"graph replay: {r['us']:.2f} us per call, {r['tflops']:.1f} TFLOP/s; zero operands "
+                  f"{r['zero_operands']['us']:.2f} us, {r['zero_operands']['tflops']:.1f} TFLOP/s", flush=True)
         elif what == "read_floor":
             bufs, out, nbytes = read_floor_inputs(ctx)
             for i in range(warmup + steps):
@@ -951,7 +985,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--only", choices=["decode", "decode_graph", "prefill", "prefill_graph", "rope_append", "matvec", "matmul",
-                                       "block", "headline", "read_floor", "copy"],
+                                       "block", "headline", "read_floor", "mfma_floor", "copy"],
                     help="run one workload without timing, for rocprofv3 to wrap")
     ap.add_argument("--configs", action="store_true",
                     help="time BASELINE configs 1, 3 and 5 instead (one JSON line each)")
@@ -1045,6 +1079,10 @@ def main():
         line["prefill_swa128_hbm_frac"] = pf["swa128"]["roofline_frac"]
         line["prefill_swa128_us"] = pf["swa128"]["us"]
         line["prefill"] = pf
+        if "mfma_floor" in r:
+            mf = r["mfma_floor"]
+            line["mfma_floor"] = mf
+            line["prefill_full_frac_of_mfma_floor"] = round(pf["full"]["tflops"] / mf["tflops"], 4)
     line["configs"] = r["configs"]
     line["headline_step"] = dict(
         r["headline_step"],

@@ -96,6 +96,9 @@ unsafe extern "C" {
     pub fn moearc_add(c: *mut MoearcCtx, out: *mut c_float, a: *const c_float, b: *const c_float, n: c_ulong) -> c_int;
     /// Calibration read (no counterpart in the reference): out[g] = xor of the g-th 64 KiB at src.
     pub fn moearc_read_floor(c: *mut MoearcCtx, out: *mut c_uint, src: *const c_void, bytes: c_ulong) -> c_int;
+    /// Matrix-core calibration (no counterpart in the reference): dense f16 MFMA chains over the
+    /// operands at src; out[w] = wave w's accumulator sum.
+    pub fn moearc_mfma_floor(c: *mut MoearcCtx, out: *mut c_float, src: *const c_void, n_wgs: c_ulong, iters: c_ulong) -> c_int;
     pub fn moearc_quantize_f16(c: *mut MoearcCtx, dst: *mut c_void, src: *const c_float, n: c_ulong) -> c_int;
     #[allow(clippy::too_many_arguments)]
     pub fn moearc_kv_append(

@@ -231,6 +231,17 @@ int moearc_add(moearc_ctx *c, float *out, const float *a, const float *b, unsign
  * src -> -2. */
 int moearc_read_floor(moearc_ctx *c, unsigned int *out, const void *src, unsigned long bytes);
 
+/* Calibration of the matrix cores. No counterpart in the reference: for measurements that set the
+ * prefill kernels' MFMA utilisation beside the rate the device sustains on such data. n_wgs
+ * work-groups of 4 waves; wave w takes eight 1 KiB operand blocks of f16 values at
+ * src + 8 KiB * w (four A and four B operands of v_mfma_f32_32x32x16_f16, lane l holding bytes
+ * 16 l .. 16 l + 15 of each) and runs four accumulator chains for `iters` rounds of two MFMAs each
+ * (round i, chain c: A[(c + i) % 4] times B[(c + i) % 4]); out[w] = the sum of its accumulators
+ * over all lanes. src holds n_wgs * 32 KiB. Null pointer -> -1; n_wgs 0 or above 2^29 - 1,
+ * iters 0, not a multiple of 4 or above 2^30, or a misaligned src -> -2. */
+int moearc_mfma_floor(moearc_ctx *c, float *out, const void *src, unsigned long n_wgs,
+                      unsigned long iters);
+
 /* Extension (no counterpart in the reference, which runs three moearc_matvec_q and up to three
  * moearc_add calls for attn.qkv, moe.rs:1942-1959): projection i (0 q, 1 k, 2 v) writes
  * out[i][r] = sum_c W_i[r][c] x[c] + bias[i][r] for r < rows[i] (bias[i] may be null), one launch

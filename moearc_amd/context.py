@@ -409,6 +409,13 @@ class Context:
         out.require("checksums", (nbytes + 65535) // 65536 * 4)
         self.finish(self._lib.moearc_read_floor(self.raw, out.ptr, src.ptr, nbytes), "read_floor")
 
+    def mfma_floor(self, out: DeviceBuffer, src: DeviceBuffer, n_wgs: int, iters: int) -> None:
+        """Calibration of the matrix cores (moearc_mfma_floor): n_wgs x 4 waves of dense f16 MFMA
+        chains over the operands at src (32 KiB per work-group); out[w] = wave w's accumulator sum."""
+        src.require("operands", n_wgs * 32768)
+        out.require("checksums", n_wgs * 4 * 4)
+        self.finish(self._lib.moearc_mfma_floor(self.raw, out.ptr, src.ptr, n_wgs, iters), "mfma_floor")
+
     def add(self, out: DeviceBuffer, a: DeviceBuffer, b: DeviceBuffer, n: int) -> None:
         """out = a + b, element-wise (kernels.cpp:1676-1683)."""
         for buf, what in ((out, "output"), (a, "left operand"), (b, "right operand")):

@@ -96,3 +96,47 @@ extern "C" __global__ void __launch_bounds__(256) moearc_read_floor_k(unsigned i
     __syncthreads();
     if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
+
+// Calibration of the matrix cores (moearc_mfma_floor): the f16 MFMA rate this device sustains on
+// data like the prefill's, for comparison with the prefill kernels. Each wave loads eight operand
+// quads of f16 values (16 bytes per lane each) from src + 8 KiB * (global wave index) -- four A and
+// four B operands of v_mfma_f32_32x32x16_f16 -- and runs four independent accumulator chains for
+// `iters` rounds; in round i chain c multiplies A[(c + i) % 4] by B[(c + i) % 4], so every
+// operand's bits keep entering the matrix core (its power, and with it the clock, depends on
+// them). Two MFMAs per chain and round: 8 x 32,768 flops per wave and round. out[w] = the sum of
+// wave w's 4 x 16 accumulators over its 64 lanes, which a host can recompute from src.
+typedef float float16v_t __attribute__((ext_vector_type(16)));
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moearc_mfma_floor_k(float *out, const u32x4_t *src, uint32_t iters) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t w = (uint64_t) blockIdx.x * 4u + (threadIdx.x >> 6);
+    half8_t A[4], B[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        A[k] = __builtin_bit_cast(half8_t, src[w * 512u + 64u * k + lane]);
+        B[k] = __builtin_bit_cast(half8_t, src[w * 512u + 64u * (4 + k) + lane]);
+    }
+    float16v_t D[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) D[c][i] = 0.f;
+    for (uint32_t it = 0; it < iters; it += 4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int k = (c + r) & 3;
+                D[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[k], B[k], D[c], 0, 0, 0);
+                D[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[k], B[k], D[c], 0, 0, 0);
+            }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s += D[c][i];
+#pragma unroll
+    for (uint32_t m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, (int) m);
+    if (lane == 0) out[w] = s;
+}

@@ -87,7 +87,7 @@ struct moearc_ctx {
     hipFunction_t f_dec_merge = nullptr;
     unsigned merge_threads = 0;  // the merge kernel's launch bound (its work-group size)
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
-    hipFunction_t f_add = nullptr, f_read_floor = nullptr;
+    hipFunction_t f_add = nullptr, f_read_floor = nullptr, f_mfma_floor = nullptr;
     hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_split8 = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
     hipFunction_t f_mm2[2] = {};  // Q8_0, F16: 128 x 128 tiles on the 32x32x16 MFMA
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
@@ -597,6 +597,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_dec_merge, "moearc_attn_decode_merge_p1"},
         {&c->f_add, "moearc_add_k"},
         {&c->f_read_floor, "moearc_read_floor_k"},
+        {&c->f_mfma_floor, "moearc_mfma_floor_k"},
         {&c->f_mm[0][0], "moearc_matmul_q8_0_r1_k"},
         {&c->f_mm[0][1], "moearc_matmul_q8_0_r2_k"},
         {&c->f_mm[1][0], "moearc_matmul_f16_r1_k"},
@@ -1076,6 +1077,20 @@ int moearc_read_floor(moearc_ctx *c, unsigned int *out, const void *src, unsigne
         uint64_t n16;
     } args{out, src, bytes / 16};
     return launch(c, c->f_read_floor, (unsigned) wgs, 256, args, nullptr, bytes, 0, "read_floor");
+}
+
+int moearc_mfma_floor(moearc_ctx *c, float *out, const void *src, unsigned long n_wgs,
+                      unsigned long iters) {
+    if (!c || !out || !src) return ERR;
+    if (n_wgs == 0 || n_wgs > 0x7FFFFFFFul / 4 || iters == 0 || iters % 4 != 0 || iters > 0x40000000ul ||
+        (uintptr_t) src % 16 != 0)
+        return ERR_ARG;
+    struct {
+        float *o;
+        const void *s;
+        uint32_t it;
+    } args{out, src, (uint32_t) iters};
+    return launch(c, c->f_mfma_floor, (unsigned) n_wgs, 256, args, nullptr, n_wgs, iters, "mfma_floor");
 }
 
 int moearc_attn_out(moearc_ctx *c, unsigned int type_id, float *h, const void *w, const float *bias,

@@ -40,6 +40,7 @@ SIGNATURES = {
     "moearc_matvec_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong, _c_ulong]),
     "moearc_add": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong]),
     "moearc_read_floor": (ctypes.c_int, [_vp, _vp, _vp, _c_ulong]),
+    "moearc_mfma_floor": (ctypes.c_int, [_vp, _vp, _vp, _c_ulong, _c_ulong]),
     "moearc_attn_qkv": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_ulong]),
     "moearc_attn_block_chunk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_ulong, _c_ulong, _vp, _vp, _vp]),
     "moearc_matmul_q": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _c_ulong, _c_ulong, _c_ulong]),
