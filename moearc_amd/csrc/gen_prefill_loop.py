@@ -207,6 +207,11 @@ def tile_step(si, label):
     meet the other waves, copy tile t + 2 into buffer (t + 2) % 4, load the entries of tile t + 4.
     Six memory operations per step, so the wait is vmcnt(6)."""
     sc = (si + 2) % NBUF
+    # a pair's second work-group leaves its raised issue priority at tile %[btile]
+    ins("s_cmp_eq_u32 s65, %[btile]")
+    ins(f"s_cbranch_scc0 {label}_np")
+    ins("s_setprio 0")
+    ins(f"{label}_np:")
     ins("s_waitcnt vmcnt(6)")
     ins("s_barrier")
     ins("s_add_u32 s80, s65, 2")

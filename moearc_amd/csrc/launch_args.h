@@ -102,6 +102,10 @@ struct PrefillArgs {
     uint32_t n_qtiles;            // query tiles per KV head
     uint16_t *out_lo;             // with f16 output: also f16(o - hi) here, the low half of the
                                   // chunk product's activation split (default kernels; else null)
+    uint32_t pair_half;           // the grid is two work-groups per CU, i and i + pair_half sharing
+                                  // one (the dispatcher's order): pair_half; otherwise 0
+    float boost_a, boost_b;       // the second work-group of a pair keeps a raised issue priority
+                                  // for boost_a * its chunks - boost_b * its partner's chunks
 };
 
 // RoPE parameters (moearc_rope, moearc_rope_kv_append_chunk): theta_scale = freq_base^(-2/n_dims),
