@@ -1499,7 +1499,7 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     if (rc == OK) {
         const uint64_t n = a.part_stride;
         rc = launch2d(c, c->f_mm_reduce, (unsigned) std::min<uint64_t>((n + 255) / 256, 65536), 1, 256,
-                      MmReduceLaunch{a, (uint32_t) slices}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
+                      MmReduceLaunch{a, (uint32_t) slices, 0u}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
     }
     --c->scope_depth;
     if (call0) record_bracket(c, call0, what, n_rows, n_tok);
