@@ -287,11 +287,23 @@ def bench_read_floor(ctx, hip, steps, warmup):
     want = np.bitwise_xor.reduce(host.reshape(-1, 16384), axis=1)
     reps = graph_timed(hip, ctx, lambda i: ctx.read_floor(out, bufs[i % COPIES], nbytes), steps, warmup)
     st = rep_stats(reps)
+    # the same read followed by a dependent one-work-group launch (a 64-float fill), as the decode
+    # call's split launch is followed by its merge; and that tiny launch alone, back to back
+    tiny = ctx.alloc(64 * 4)
+
+    def chain(i):
+        ctx.read_floor(out, bufs[i % COPIES], nbytes)
+        ctx.zero(tiny, 64)
+    ch = rep_stats(graph_timed(hip, ctx, chain, steps, warmup))
+    tl = rep_stats(graph_timed(hip, ctx, lambda i: ctx.zero(tiny, 64), steps, warmup))
     del bufs
     return {"bytes": nbytes, "us": st["median"], "us_reps": st,
             "gbs": round(nbytes / st["median"] / 1e3, 1),
             "frac_of_peak": round(nbytes / st["median"] / 1e3 / HBM_PEAK_GBS, 4),
-            "checksums_match": bool(np.array_equal(got, want))}
+            "checksums_match": bool(np.array_equal(got, want)),
+            "with_dependent_launch_us": ch["median"], "with_dependent_launch_reps": ch,
+            "dependent_launch_us": round(ch["median"] - st["median"], 3),
+            "tiny_launch_alone_us": tl["median"], "tiny_launch_alone_reps": tl}
 
 
 def launch_overhead():
@@ -1065,9 +1077,13 @@ def main():
             "call_us_events": round(ev["attn_decode r64 m64"], 2) if "attn_decode r64 m64" in ev else None,
         },
         "read_floor": dict(r["read_floor"], decode_frac_of_floor=round(r["read_floor"]["us"] / step_us, 4),
+                           decode_frac_of_two_launch_floor=round(
+                               r["read_floor"]["with_dependent_launch_us"] / step_us, 4),
                            note="moearc_read_floor over the same 64 MiB copies and graph replay: a plain "
                                 "streaming read of the call's KV bytes; decode_frac_of_floor = its time "
-                                "over the decode call's"),
+                                "over the decode call's; with_dependent_launch_us: the same read followed "
+                                "by a dependent one-work-group launch, as the split launch is followed "
+                                "by the merge (decode_frac_of_two_launch_floor = that over the call's time)"),
         "device": r.get("device"),
         "commit": git_head(),
         "source_sha16": source_sha16(),
