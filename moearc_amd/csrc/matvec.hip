@@ -332,10 +332,18 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
         }
     };
 
-    // The first row's weights are in flight before anything waits on the activation.
+    // The first row's weights are in flight before anything waits on the activation; the bias and
+    // residual of the wave's rows (lane i: row r0 + i, at most 64 rows per wave) follow them, so
+    // that no row waits for its own.
+    const bool with_bias = (a.bias_mask >> seg) & 1u, with_res = (a.res_mask >> seg) & 1u;
+    float bias_l = 0.f, res_l = 0.f;
     if (has_rows) {
         issue(0, ga, da, na);
         issue(min(1u, units - 1u), gb, db, nb);  // always two units in flight (re-reads past the end)
+        if (lane < r1 - r0) {
+            if (with_bias) bias_l = a.bias[seg][r0 + lane];
+            if (with_res) res_l = a.out[seg][r0 + lane];
+        }
     }
     if (a.x_in_lds) {  // activation -> LDS, piece p's values at floats [p * XPAD, p * XPAD + PE)
         constexpr uint32_t XB = 8;  // loads in flight per thread before their stores
@@ -404,10 +412,6 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
             const uint32_t gi = lane + 64u * k;
             if (gi < ng) *(u32x4_t *) (wb + 16u * gi) = g[k];
         }
-        // The row's bias (a.bias[seg] points at readable memory even without one) is requested
-        // before the next loads so that waiting for it never waits for them.
-        const float bv = a.bias[seg][r];
-        const float rv = a.out[seg][r];  // the residual, when the result is added to it
         issue(min(u + 2u, units - 1u), g, delta_ref, ng_ref);
         __builtin_amdgcn_wave_barrier();
         if (u == 0 || n_slabs > 1u) load_x(sl);
@@ -424,9 +428,10 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs &a) {
         __builtin_amdgcn_wave_barrier();
         if (sl + 1u == n_slabs) {
             acc = wave_sum_to_lane63(acc);
-            if (lane == 63u) {
-                const float y = (a.bias_mask >> seg) & 1u ? acc + bv : acc;
-                a.out[seg][r] = (a.res_mask >> seg) & 1u ? rv + y : y;
+            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 63));
+            if (lane == r - r0) {  // the lane holding this row's bias and residual
+                const float y = with_bias ? tot + bias_l : tot;
+                a.out[seg][r] = with_res ? res_l + y : y;
             }
             acc = 0.f;
         }
