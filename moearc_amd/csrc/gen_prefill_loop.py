@@ -205,17 +205,34 @@ def copy_tile(slot, tile_sgpr, buf, label):
 def tile_step(si, label):
     """Tile step t = s65: wait for this wave's copies of tile t and the entries of tile t + 2,
     meet the other waves, copy tile t + 2 into buffer (t + 2) % 4, load the entries of tile t + 4.
-    Six memory operations per step, so the wait is vmcnt(6)."""
+    Six memory operations per step, so the wait is vmcnt(6); tiles past the last are not copied,
+    so the step after the last copy (t + 1 >= ntiles) waits vmcnt(2), its predecessor's two entry
+    loads being the only younger operations."""
     sc = (si + 2) % NBUF
     # a pair's second work-group leaves its raised issue priority at tile %[btile]
     ins("s_cmp_eq_u32 s65, %[btile]")
     ins(f"s_cbranch_scc0 {label}_np")
     ins("s_setprio 0")
     ins(f"{label}_np:")
-    ins("s_waitcnt vmcnt(6)")
+    if label == "pro_t0":
+        ins("s_waitcnt vmcnt(6)")
+    else:
+        # the step before the last issued no copies (tile t + 1 past the last): its two entry loads
+        # are the only younger memory operations
+        ins("s_add_u32 s79, s65, 1")
+        ins("s_cmp_ge_u32 s79, %[ntiles]")
+        ins(f"s_cbranch_scc1 {label}_w2")
+        ins("s_waitcnt vmcnt(6)")
+        ins(f"{label}_wd:")
+        ool_block(f"{label}_w2", ["s_waitcnt vmcnt(2)"], f"{label}_wd")
     ins("s_barrier")
     ins("s_add_u32 s80, s65, 2")
+    # no copies of tiles past the last (the clamped copy would repeat the last tile into a buffer
+    # nothing reads, and the loop's end would wait for it)
+    ins("s_cmp_ge_u32 s80, %[ntiles]")
+    ins(f"s_cbranch_scc1 {label}_cd")
     copy_tile(sc, 80, sc, f"{label}_c")
+    ins(f"{label}_cd:")
     ins("s_add_u32 s80, s65, 4")
     pid_load(si, 80, f"{label}_p")
 
