@@ -339,13 +339,34 @@ def rescale_body(sd, e, q0, o_base, bias_base, m, l, c_reg, span_reg, jlo, jn, l
         ins(f"v_add_f32 v{E[i]}, v{E[i]}, v204")
 
 
+def first_max(e, m, bias, inputs):
+    """m = max(m, the row maximum of the log2-domain scores of v[e..e+15] over lanes n and n + 32),
+    bias = 7 - m; with `inputs`, v[e..] become the exponent inputs (s c) + bias, as the rescale
+    path leaves them."""
+    E = list(range(e, e + 16))
+    for i in range(16):
+        ins(f"v_mul_f32 v{E[i]}, %[cs], v{E[i]}")
+    ins(f"v_max3_f32 v200, v{E[0]}, v{E[1]}, v{E[2]}")
+    for i in range(3, 15, 2):
+        ins(f"v_max3_f32 v200, v200, v{E[i]}, v{E[i + 1]}")
+    ins(f"v_max_f32 v200, v200, v{E[15]}")
+    ins("ds_bpermute_b32 v202, v243, v200")
+    ins("s_waitcnt lgkmcnt(0)")
+    ins(f"v_max3_f32 v202, v202, v200, v{m}")
+    ins(f"v_mov_b32 v{m}, v202")
+    ins(f"v_sub_f32 v{bias}, 0x40e00000, v202")
+    if inputs:
+        for i in range(16):
+            ins(f"v_add_f32 v{E[i]}, v{E[i]}, v{bias}")
+
+
 def generate():
     # m0 (the LDS base of the copies) is the compiler's register: saved here, restored at the one
     # exit, so the statement leaves it as it found it and needs no m0 clobber
     ins("s_mov_b32 s86, m0")
     # ---- prologue: copies of tiles 0 and 1 (their entries arrive as inputs in v222-v225, loaded
     # beside the query rows before the statement, so the two loads share one memory round trip),
-    # entries of tiles 2 and 3, step 0 ----
+    # entries of tiles 2 and 3, step 0, both blocks' reference m from chunk 0 ----
     ins("s_mov_b32 s80, 0")
     copy_tile(0, 80, 0, "pro_c0")
     ins("s_mov_b32 s80, 2")
@@ -373,8 +394,23 @@ def generate():
     ins("s_cbranch_scc1 pro_ma_ok")
     ins("s_call_b64 s[66:67], pff_mask_a")
     ins("pro_ma_ok:")
-    for x in fma_ops(64, 96) + max_ops(64, 82):
-        ins(x)
+    # S_B(0) too (R1 of chunk 0 computes it again for the loop), masked
+    mfma("80:95", K_OPS[0], "144:147", "0")
+    for t in (1, 2, 3):
+        mfma("80:95", K_OPS[t], f"{144 + 4 * t}:{147 + 4 * t}", "v[80:95]")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_nop 7")
+    ins("s_sub_u32 s79, 0, %[jlob]")
+    ins("s_cmp_lt_u32 s79, %[jnb]")
+    ins("s_cbranch_scc1 pro_mb_ok")
+    ins("s_call_b64 s[66:67], pff_mask_b")
+    ins("pro_mb_ok:")
+    # each block's reference m starts at chunk 0's row maximum (no rescale of chunk 0); A's exponent
+    # inputs follow, B's are taken by the loop's first R2
+    first_max(64, 208, 96, True)
+    first_max(80, 209, 112, False)
+    ins("s_mov_b64 s[82:83], 0")
     # ---- main loop: four tiles (eight chunks) per pass; buffers and entry slots fixed ----
     # (the chunk count may be odd: the loop can end after a tile's first chunk)
     ins("pff_loop:")
