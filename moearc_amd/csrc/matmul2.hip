@@ -45,6 +45,14 @@ constexpr uint32_t MM2_NBUF = 3u;
 constexpr uint32_t MM2_QTAIL = MM2_ROWS * 64u;
 constexpr uint32_t MM2_QPAIR = MM2_QTAIL + 4u * 256u;
 
+// Q4_K (per work-group, after the activation buffers): the k-blocks' per-token block sums (128
+// floats, three buffers), each pair of sub-blocks' 32 payload bytes per row (the low nibbles are
+// the pair's first sub-block, the high ones its second; three buffers) and each super-block's
+// 16-byte header per row (d, dmin, the 12 scale bytes; two buffers)
+constexpr uint32_t MM2_KXS = MM2_TOK * 4u;
+constexpr uint32_t MM2_KPAIR = MM2_ROWS * 32u;
+constexpr uint32_t MM2_KHDR = MM2_ROWS * 16u;
+
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
 
@@ -64,6 +72,24 @@ __device__ __forceinline__ half8_t mm2_i8_to_f16(mm2_u32x2 q) {
         const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
         const half2_t h0 = __builtin_bit_cast(half2_t, p0) - half2_t{(_Float16) 1152.f, (_Float16) 1152.f};
         const half2_t h1 = __builtin_bit_cast(half2_t, p1) - half2_t{(_Float16) 1152.f, (_Float16) 1152.f};
+        r[4 * i] = h0[0];
+        r[4 * i + 1] = h0[1];
+        r[4 * i + 2] = h1[0];
+        r[4 * i + 3] = h1[1];
+    }
+    return r;
+}
+
+// 8 nibbles (one per byte, values 0 .. 15) in two dwords -> 8 exact f16: under exponent 0x64 the
+// byte is 1024 + q
+__device__ __forceinline__ half8_t mm2_u4_to_f16(mm2_u32x2 q) {
+    half8_t r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, q[i], 0x04010400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, q[i], 0x04030402u);
+        const half2_t h0 = __builtin_bit_cast(half2_t, p0) - half2_t{(_Float16) 1024.f, (_Float16) 1024.f};
+        const half2_t h1 = __builtin_bit_cast(half2_t, p1) - half2_t{(_Float16) 1024.f, (_Float16) 1024.f};
         r[4 * i] = h0[0];
         r[4 * i + 1] = h0[1];
         r[4 * i + 2] = h1[0];
@@ -102,11 +128,14 @@ __device__ __forceinline__ uint32_t mm2_lds4(uint32_t off) {
 
 template <uint32_t TY>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
-    constexpr bool Q8 = TY == 8;
-    // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair buffers
-    constexpr uint32_t BUF = MM2_ACT + (Q8 ? 0u : MM2_ROWS * 64u);
+    constexpr bool Q8 = TY == 8, Q4K = TY == 12;
+    // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair
+    // buffers, (Q4_K) the block sums, pair and header buffers
+    constexpr uint32_t BUF = MM2_ACT + (TY == 1 ? MM2_ROWS * 64u : 0u);
     constexpr uint32_t QBASE = MM2_NBUF * BUF;
-    __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + (Q8 ? MM2_NBUF * MM2_QPAIR : 0u)];
+    constexpr uint32_t KXS = QBASE, KPAIR = KXS + MM2_NBUF * MM2_KXS, KHDR = KPAIR + MM2_NBUF * MM2_KPAIR;
+    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * MM2_QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR : 0u;
+    __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + EXTRA];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31u, h = lane >> 5;
@@ -150,12 +179,31 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         for (int i = 0; i < 4; ++i)
             mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + buf * BUF + (4u * wave + (uint32_t) i) * 1024u),
                        xsrc[i] + 32u * b);
-        if constexpr (!Q8) {
+        if constexpr (TY == 1) {
 #pragma unroll
             for (int i = 0; i < 2; ++i)
                 mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + buf * BUF + MM2_ACT + (2u * wave + (uint32_t) i) * 1024u),
                            wsrc[i] + 64u * b);
         }
+    };
+    // Q4_K: per k-block b (into buffers buf, qb and the header buffer of b's super-block) the block
+    // sums of the tile's tokens, b's pair of sub-blocks, b's super-block header -- three copies for
+    // every block, whichever of them repeat the previous block's bytes, so each step issues the
+    // same count. Waves 2 and 3 copy the same sums and headers as waves 0 and 1 (the same bytes to
+    // the same places). Pair slot q = 64 wave + lane holds row q / 2's 16-byte chunk
+    // (q & 1) ^ ((row >> 3) & 1) of the pair's 32 payload bytes (qs[32 g .. 32 g + 31]).
+    const uint32_t k_row = (64u * wave + lane) >> 1;
+    const uint8_t *k_psrc = sg.w + (uint64_t) min(r0 + k_row, sg.rows - 1u) * sg.row_bytes + 16u +
+                            16u * ((lane & 1u) ^ ((k_row >> 3) & 1u));
+    const uint8_t *k_hsrc = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes;
+    const float *k_xsrc = a.xs + (uint64_t) min(t0 + 64u * (wave & 1u) + lane, a.n_tok - 1u) * (a.cols / 32u) + kb0;
+    auto kcopy = [&](uint32_t b, uint32_t buf, uint32_t qb) {
+        const uint32_t kb = kb0 + b;  // super-block kb / 8, pair (kb % 8) / 2
+        mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + KXS + buf * MM2_KXS + (wave & 1u) * 256u), k_xsrc + b);
+        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + KPAIR + qb * MM2_KPAIR + wave * 1024u),
+                   k_psrc + 144u * (uint64_t) (kb >> 3) + 32u * ((kb & 7u) >> 1));
+        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR + (wave & 1u) * 1024u),
+                   k_hsrc + 144u * (uint64_t) (kb >> 3));
     };
     // Q8_0: the weights of blocks b, b + 1 (b even) into pair buffer qb
     auto qcopy = [&](uint32_t b, uint32_t qb) {
@@ -205,8 +253,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         }
     }
 
-    // block b from activation buffer buf and (Q8_0) pair buffer qb, b odd: the pair's second block
-    auto compute = [&](uint32_t buf, uint32_t qb, bool odd) {
+    // block b from activation buffer buf and (Q8_0, Q4_K) pair buffer qb, b odd: the pair's second block
+    auto compute = [&](uint32_t buf, uint32_t qb, bool odd, uint32_t b) {
         half8_t ah[2][2], al[2][2], bw[2][2];
         float d[2];
 #pragma unroll
@@ -217,6 +265,56 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
                 ah[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off));
                 al[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off + MM2_HALF));
             }
+        if constexpr (Q4K) {
+            // this lane's 16 payload bytes of the pair (its k of both sub-blocks) and the
+            // super-block header (d, dmin, 12 scale bytes) of each row tile: both stay in their
+            // buffers for every step that reads them
+            const uint32_t sb = b & 7u;  // sub-block within the super-block (slices start on one)
+            float d1[2], m1[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
+                const u32x4_t kq = mm2_lds16(lds0 + KPAIR + qb * MM2_KPAIR + 32u * rl + 16u * (h ^ ((rl >> 3) & 1u)));
+                const u32x4_t hd = mm2_lds16(lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR + 16u * rl);
+                // get_scale_min_k4 (reference.rs:150-160) over the 12 scale bytes hd.y .. hd.w
+                // (a mask, not a branch or a select: those split the step and its registers spill)
+                const uint32_t i = 8u * (sb & 3u);
+                const uint32_t a1 = hd[1] >> i, a2 = hd[2] >> i, a3 = hd[3] >> i;
+                const uint32_t lo = sb < 4u ? ~0u : 0u;  // uniform
+                const uint32_t sc = ((a1 & 63u) & lo) | (((a3 & 15u) | (((a1 >> 6) & 3u) << 4)) & ~lo);
+                const uint32_t mn = ((a2 & 63u) & lo) | ((((a3 >> 4) & 15u) | (((a2 >> 6) & 3u) << 4)) & ~lo);
+                d1[rt] = (float) __builtin_bit_cast(_Float16, (uint16_t) (hd[0] & 0xFFFFu)) * (float) sc;
+                m1[rt] = (float) __builtin_bit_cast(_Float16, (uint16_t) (hd[0] >> 16)) * (float) mn;
+                const uint32_t sh = odd ? 4u : 0u;  // the pair's first sub-block: low nibbles
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    bw[rt][s] = mm2_u4_to_f16(mm2_u32x2{(kq[2 * s] >> sh) & 0x0F0F0F0Fu,
+                                                        (kq[2 * s + 1] >> sh) & 0x0F0F0F0Fu});
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                // the block sums of this lane's accumulators: element j is token 8 (j / 4) + 4 h + j % 4
+                float4_t xs[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    xs[q] = *(const __attribute__((address_space(3))) float4_t *) (uintptr_t) (
+                        lds0 + KXS + buf * MM2_KXS + 4u * (64u * (wave & 1u) + 32u * tt + 8u * q + 4u * h));
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    mm2_f32x16 sblk = {};
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][s], bw[rt][s], sblk, 0, 0, 0);
+                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][s], bw[rt][s], sblk, 0, 0, 0);
+                    }
+                    // d1 * (sum q x) - m1 * (sum x): the reference's sub-block regrouped
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        acc[tt][rt][j] = fmaf(-m1[rt], xs[j >> 2][j & 3], fmaf(d1[rt], sblk[j], acc[tt][rt][j]));
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             if constexpr (Q8) {
@@ -275,12 +373,16 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // in line, which nothing reads, so every step issues the same copies.
     copy(0, 0);
     if constexpr (Q8) qcopy(0, 0);
+    if constexpr (Q4K) kcopy(0, 0, 0);
     copy(min(1u, nb - 1u), 1);
+    if constexpr (Q4K) kcopy(min(1u, nb - 1u), 1, 0);
     auto step = [&](uint32_t b, uint32_t buf, uint32_t qb, bool odd) {
         // block b's copies have landed and every LDS read of block b - 1 has returned, in this wave;
         // then in every wave
         __builtin_amdgcn_sched_barrier(0);
-        if (!Q8)
+        if (Q4K)
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
+        else if (!Q8)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(6u));
         else if (odd)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
@@ -291,8 +393,9 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         copy(min(b + 2u, nb - 1u), (buf + 2u) % 3u);
         if constexpr (Q8)
             if (!odd) qcopy(min(b + 2u, nb - 2u), (qb + 1u) % 3u);
+        if constexpr (Q4K) kcopy(min(b + 2u, nb - 1u), (buf + 2u) % 3u, (qb + 1u) % 3u);
         __builtin_amdgcn_sched_barrier(0);
-        compute(buf, qb, odd);
+        compute(buf, qb, odd, b);
     };
     uint32_t b = 0;
     for (; b + 6u <= nb; b += 6u) {
@@ -346,3 +449,5 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_q8_0_k(MatmulArgs a) { mm2_body<8>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_f16_k(MatmulArgs a) { mm2_body<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moearc_matmul2_q4_k_k(MatmulArgs a) { mm2_body<12>(a); }
