@@ -45,13 +45,13 @@ constexpr uint32_t MM2_NBUF = 3u;
 constexpr uint32_t MM2_QTAIL = MM2_ROWS * 64u;
 constexpr uint32_t MM2_QPAIR = MM2_QTAIL + 4u * 256u;
 
-// Q4_K (per work-group, after the activation buffers): the k-blocks' per-token block sums (128
-// floats, three buffers), each pair of sub-blocks' 32 payload bytes per row (the low nibbles are
-// the pair's first sub-block, the high ones its second; three buffers) and each super-block's
-// 16-byte header per row (d, dmin, the 12 scale bytes; two buffers)
+// Q4_K, Q5_K (per work-group, after the activation buffers): the k-blocks' per-token block sums
+// (128 floats, three buffers), each pair of sub-blocks' 32 payload bytes per row (the low nibbles
+// are the pair's first sub-block, the high ones its second; three buffers) and each super-block's
+// header per row (d, dmin, the 12 scale bytes; Q5_K: and the 32 bytes of fifth bits; two buffers)
 constexpr uint32_t MM2_KXS = MM2_TOK * 4u;
 constexpr uint32_t MM2_KPAIR = MM2_ROWS * 32u;
-constexpr uint32_t MM2_KHDR = MM2_ROWS * 16u;
+__host__ __device__ constexpr uint32_t mm2_khdr(uint32_t ty) { return MM2_ROWS * (ty == 13 ? 48u : 16u); }
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
@@ -128,7 +128,9 @@ __device__ __forceinline__ uint32_t mm2_lds4(uint32_t off) {
 
 template <uint32_t TY>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
-    constexpr bool Q8 = TY == 8, Q4K = TY == 12;
+    constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13;
+    constexpr uint32_t KSB = Q5K ? 176u : 144u, KQS = Q5K ? 48u : 16u;  // super-block bytes, qs offset
+    constexpr uint32_t MM2_KHDR = mm2_khdr(TY);
     // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair
     // buffers, (Q4_K) the block sums, pair and header buffers
     constexpr uint32_t BUF = MM2_ACT + (TY == 1 ? MM2_ROWS * 64u : 0u);
@@ -193,7 +195,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // the same places). Pair slot q = 64 wave + lane holds row q / 2's 16-byte chunk
     // (q & 1) ^ ((row >> 3) & 1) of the pair's 32 payload bytes (qs[32 g .. 32 g + 31]).
     const uint32_t k_row = (64u * wave + lane) >> 1;
-    const uint8_t *k_psrc = sg.w + (uint64_t) min(r0 + k_row, sg.rows - 1u) * sg.row_bytes + 16u +
+    const uint8_t *k_psrc = sg.w + (uint64_t) min(r0 + k_row, sg.rows - 1u) * sg.row_bytes + KQS +
                             16u * ((lane & 1u) ^ ((k_row >> 3) & 1u));
     const uint8_t *k_hsrc = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes;
     const float *k_xsrc = a.xs + (uint64_t) min(t0 + 64u * (wave & 1u) + lane, a.n_tok - 1u) * (a.cols / 32u) + kb0;
@@ -201,9 +203,19 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         const uint32_t kb = kb0 + b;  // super-block kb / 8, pair (kb % 8) / 2
         mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + KXS + buf * MM2_KXS + (wave & 1u) * 256u), k_xsrc + b);
         mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + KPAIR + qb * MM2_KPAIR + wave * 1024u),
-                   k_psrc + 144u * (uint64_t) (kb >> 3) + 32u * ((kb & 7u) >> 1));
-        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR + (wave & 1u) * 1024u),
-                   k_hsrc + 144u * (uint64_t) (kb >> 3));
+                   k_psrc + KSB * (uint64_t) (kb >> 3) + 32u * ((kb & 7u) >> 1));
+        const uint32_t hbase = lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR;
+        if constexpr (Q5K) {
+#pragma unroll
+            for (uint32_t i = 0; i < 2; ++i) {
+                const uint32_t slot0 = wave < 2u ? 128u * wave + 64u * i : 128u + 64u * wave;
+                const uint32_t q = slot0 + lane;
+                const uint8_t *src = sg.w + (uint64_t) min(r0 + q / 3u, sg.rows - 1u) * sg.row_bytes + 16u * (q % 3u);
+                mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + 16u * slot0), src + KSB * (uint64_t) (kb >> 3));
+            }
+        } else {
+            mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), k_hsrc + KSB * (uint64_t) (kb >> 3));
+        }
     };
     // Q8_0: the weights of blocks b, b + 1 (b even) into pair buffer qb
     auto qcopy = [&](uint32_t b, uint32_t qb) {
@@ -275,7 +287,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
             for (int rt = 0; rt < 2; ++rt) {
                 const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
                 const u32x4_t kq = mm2_lds16(lds0 + KPAIR + qb * MM2_KPAIR + 32u * rl + 16u * (h ^ ((rl >> 3) & 1u)));
-                const u32x4_t hd = mm2_lds16(lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR + 16u * rl);
+                const uint32_t hrow = lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR + (Q5K ? 48u : 16u) * rl;
+                const u32x4_t hd = mm2_lds16(hrow);
                 // get_scale_min_k4 (reference.rs:150-160) over the 12 scale bytes hd.y .. hd.w
                 // (a mask, not a branch or a select: those split the step and its registers spill)
                 const uint32_t i = 8u * (sb & 3u);
@@ -286,10 +299,19 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
                 d1[rt] = (float) __builtin_bit_cast(_Float16, (uint16_t) (hd[0] & 0xFFFFu)) * (float) sc;
                 m1[rt] = (float) __builtin_bit_cast(_Float16, (uint16_t) (hd[0] >> 16)) * (float) mn;
                 const uint32_t sh = odd ? 4u : 0u;  // the pair's first sub-block: low nibbles
+                // Q5_K: element e's fifth bit is bit sb of qh[e]; this lane's elements 16 h ..
+                // + 15 have qh[16 h .. 16 h + 15], the header's chunk 1 + h
+                u32x4_t qh = {};
+                if constexpr (Q5K) qh = mm2_lds16(hrow + 16u + 16u * h);
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    bw[rt][s] = mm2_u4_to_f16(mm2_u32x2{(kq[2 * s] >> sh) & 0x0F0F0F0Fu,
-                                                        (kq[2 * s + 1] >> sh) & 0x0F0F0F0Fu});
+                for (int s = 0; s < 2; ++s) {
+                    uint32_t w0 = (kq[2 * s] >> sh) & 0x0F0F0F0Fu, w1 = (kq[2 * s + 1] >> sh) & 0x0F0F0F0Fu;
+                    if constexpr (Q5K) {
+                        w0 |= ((qh[2 * s] >> sb) & 0x01010101u) << 4;
+                        w1 |= ((qh[2 * s + 1] >> sb) & 0x01010101u) << 4;
+                    }
+                    bw[rt][s] = mm2_u4_to_f16(mm2_u32x2{w0, w1});
+                }
             }
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -380,7 +402,9 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         // block b's copies have landed and every LDS read of block b - 1 has returned, in this wave;
         // then in every wave
         __builtin_amdgcn_sched_barrier(0);
-        if (Q4K)
+        if (Q5K)
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(8u));
+        else if (Q4K)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
         else if (!Q8)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(6u));
@@ -451,3 +475,5 @@ extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_q8_0_k(MatmulAr
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_f16_k(MatmulArgs a) { mm2_body<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moearc_matmul2_q4_k_k(MatmulArgs a) { mm2_body<12>(a); }
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moearc_matmul2_q5_k_k(MatmulArgs a) { mm2_body<13>(a); }
