@@ -560,7 +560,31 @@ MM_CASES = [
     ("attn_q Q8_0 2048 tokens x 4096 x 2880", 8, 2048, 4096, 2880),
     ("attn.proj Q8_0 2048 tokens x 2880 x 4096", 8, 2048, 2880, 4096),
     ("attn_q F16 2048 tokens x 4096 x 2880", 1, 2048, 4096, 2880),
+    # Qwen3-30B-A3B's attn_q (Q4_K in its Q4_K_M files) over a chunk of the same length
+    ("attn_q Q4_K qwen3-30b 2048 tokens x 4096 x 2048", 12, 2048, 4096, 2048),
 ]
+
+
+def mm_weights(rng, ty, rows, cols):
+    """Synthetic weights of one format: random payload bytes, block scales set to small normal
+    f16 values (so no block is inf or NaN), MXFP4 exponents near 2^0."""
+    from moearc_amd import QuantType
+    qt = QuantType(ty)
+    nbytes = rows * qt.row_bytes(cols)
+    if ty == 1:
+        return (rng.standard_normal(nbytes // 2) * 0.05).astype(np.float16).view(np.uint8)
+    w = rng.integers(0, 256, nbytes, dtype=np.uint8).reshape(-1, qt.block_bytes)
+    f16 = lambda v: np.frombuffer(np.full(w.shape[0], v, np.uint16).tobytes(), np.uint8).reshape(-1, 2)
+    if ty == 8:
+        w[:, 0:2] = f16(0x1800)
+    elif ty in (12, 13):
+        w[:, 0:2] = f16(0x1800)
+        w[:, 2:4] = f16(0x1400)
+    elif ty == 14:
+        w[:, 208:210] = f16(0x1800)
+    elif ty == 39:
+        w[:, 0] = 120
+    return w.reshape(-1)
 
 
 def bench_matmul(ctx, hip, steps=5):
@@ -568,18 +592,10 @@ def bench_matmul(ctx, hip, steps=5):
     replayed REPS times (the first discarded); `us` is the median per launch. TFLOP/s counts
     2 * tokens * rows * cols; the kernel issues twice that on the f16 MFMA (the activation's hi and
     lo halves)."""
-    from moearc_amd import QuantType
     res = {}
     rng = np.random.default_rng(0x33A)
     for label, ty, n_tok, rows, cols in MM_CASES:
-        qt = QuantType(ty)
-        nbytes = rows * qt.row_bytes(cols)
-        if ty == 1:
-            w = (rng.standard_normal(nbytes // 2) * 0.05).astype(np.float16).view(np.uint8)
-        else:
-            w = rng.integers(0, 256, nbytes, dtype=np.uint8).reshape(-1, 34)
-            w[:, 0:2] = np.frombuffer(np.full(w.shape[0], 0x1800, np.uint16).tobytes(), np.uint8).reshape(-1, 2)
-        dw = ctx.upload(w)
+        dw = ctx.upload(mm_weights(rng, ty, rows, cols))
         dx = ctx.upload(rng.standard_normal((n_tok, cols)).astype(np.float32))
         db = ctx.upload(rng.standard_normal(rows).astype(np.float32))
         dy = ctx.alloc(n_tok * rows * 4)
