@@ -52,6 +52,11 @@ constexpr uint32_t MM2_QPAIR = MM2_QTAIL + 4u * 256u;
 constexpr uint32_t MM2_KXS = MM2_TOK * 4u;
 constexpr uint32_t MM2_KPAIR = MM2_ROWS * 32u;
 __host__ __device__ constexpr uint32_t mm2_khdr(uint32_t ty) { return MM2_ROWS * (ty == 13 ? 48u : 16u); }
+// Q6_K (per work-group, after the activation buffers): each half super-block's (four k-blocks')
+// 64 bytes of ql and 32 of qh per row (two buffers), and each super-block's 16 scale bytes per row
+// followed by a dword per row ending on d (bytes 206 .. 209; two buffers)
+constexpr uint32_t MM2_6QUAD = MM2_ROWS * 96u;
+constexpr uint32_t MM2_6HDR = MM2_ROWS * 20u;
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
@@ -98,6 +103,23 @@ __device__ __forceinline__ half8_t mm2_u4_to_f16(mm2_u32x2 q) {
     return r;
 }
 
+// The same for 6-bit values q + 32 (0 .. 63) -> exact f16 q in [-32, 31]
+__device__ __forceinline__ half8_t mm2_u6_to_f16(mm2_u32x2 q) {
+    half8_t r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, q[i], 0x04010400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, q[i], 0x04030402u);
+        const half2_t h0 = __builtin_bit_cast(half2_t, p0) - half2_t{(_Float16) 1056.f, (_Float16) 1056.f};
+        const half2_t h1 = __builtin_bit_cast(half2_t, p1) - half2_t{(_Float16) 1056.f, (_Float16) 1056.f};
+        r[4 * i] = h0[0];
+        r[4 * i + 1] = h0[1];
+        r[4 * i + 2] = h1[0];
+        r[4 * i + 3] = h1[1];
+    }
+    return r;
+}
+
 // LDS-DMA copies of 16 (or 4) bytes per lane from src to LDS byte lds + 16 lane (4 lane). Issued as
 // asm (m0 saved and restored, memory clobbered), out of the compiler's wait bookkeeping: with such
 // copies in flight it would drain every memory operation (vmcnt(0)) before each step's LDS reads,
@@ -128,7 +150,7 @@ __device__ __forceinline__ uint32_t mm2_lds4(uint32_t off) {
 
 template <uint32_t TY>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
-    constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13;
+    constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13, Q6K = TY == 14;
     constexpr uint32_t KSB = Q5K ? 176u : 144u, KQS = Q5K ? 48u : 16u;  // super-block bytes, qs offset
     constexpr uint32_t MM2_KHDR = mm2_khdr(TY);
     // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair
@@ -136,7 +158,9 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     constexpr uint32_t BUF = MM2_ACT + (TY == 1 ? MM2_ROWS * 64u : 0u);
     constexpr uint32_t QBASE = MM2_NBUF * BUF;
     constexpr uint32_t KXS = QBASE, KPAIR = KXS + MM2_NBUF * MM2_KXS, KHDR = KPAIR + MM2_NBUF * MM2_KPAIR;
-    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * MM2_QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR : 0u;
+    constexpr uint32_t K6Q = QBASE, K6H = K6Q + 2u * MM2_6QUAD;
+    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * MM2_QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR
+                             : Q6K ? 2u * MM2_6QUAD + 2u * MM2_6HDR : 0u;
     __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + EXTRA];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -241,7 +265,9 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const uint32_t tok = 64u * (wave & 1u) + 32u * tt + n;
-            aoff[tt][s] = lds0 + tok * 64u + 16u * ((2u * h + s) ^ mm2_swz(tok));
+            // Q6_K: slice s holds one 16-wide scale group, k 16 s + 8 h .. + 7, chunk 2 s + h
+            const uint32_t ch = Q6K ? 2u * s + h : 2u * h + s;
+            aoff[tt][s] = lds0 + tok * 64u + 16u * (ch ^ mm2_swz(tok));
         }
     // B operand (weights) of row tile rt: row 64 (w >> 1) + 32 rt + n. F16 slice s: chunk 2 h + s.
     // Q8_0 (pair buffer 0): [0] chunk h, [1] chunk h + 1, [2] chunk h + 2, [3] chunk 3 (h = 0) or the
@@ -265,6 +291,28 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         }
     }
 
+    // Q6_K: per k-block b (into the buffers of b's half super-block and super-block) its half
+    // super-block's ql and qh (128 rows x six 16-byte chunks: slot q = 192 i + 64 wave... holds row
+    // q / 6's chunk q % 6, three copies a lane) and its super-block's scales and d (a 16-byte copy
+    // and a dword copy per row: waves 2 and 3 repeat waves 0 and 1) -- every block, whichever of them
+    // repeat the previous block's bytes, so each step issues the same five copies
+    auto k6copy = [&](uint32_t b) {
+        const uint32_t kb = kb0 + b;  // super-block kb / 8, half (kb % 8) / 4
+        const uint64_t sbo = 210u * (uint64_t) (kb >> 3);
+        const uint32_t qbase = lds0 + K6Q + ((b >> 2) & 1u) * MM2_6QUAD;
+#pragma unroll
+        for (uint32_t i = 0; i < 3; ++i) {
+            const uint32_t slot0 = 256u * i + 64u * wave, q = slot0 + lane;
+            const uint32_t r = q / 6u, c = q % 6u;  // ql chunks 0 .. 3, qh chunks 4 and 5
+            const uint32_t off = c < 4u ? 64u * ((kb >> 2) & 1u) + 16u * c : 128u + 32u * ((kb >> 2) & 1u) + 16u * (c - 4u);
+            mm2_copy16(__builtin_amdgcn_readfirstlane(qbase + 16u * slot0),
+                       sg.w + (uint64_t) min(r0 + r, sg.rows - 1u) * sg.row_bytes + sbo + off);
+        }
+        const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * MM2_6HDR;
+        const uint8_t *hrow = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes + sbo;
+        mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), hrow + 192u);
+        mm2_copy4(__builtin_amdgcn_readfirstlane(hbase + MM2_ROWS * 16u + (wave & 1u) * 256u), hrow + 206u);
+    };
     // block b from activation buffer buf and (Q8_0, Q4_K) pair buffer qb, b odd: the pair's second block
     auto compute = [&](uint32_t buf, uint32_t qb, bool odd, uint32_t b) {
         half8_t ah[2][2], al[2][2], bw[2][2];
@@ -277,6 +325,52 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
                 ah[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off));
                 al[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off + MM2_HALF));
             }
+        if constexpr (Q6K) {
+            // k-block c of half super-block hf: low four bits from ql[64 hf + 32 (c & 1) + l]
+            // (nibble c >> 1), high two from qh[32 hf + l] (bits 2c, 2c + 1), l the element; this
+            // lane's slice s holds l = 16 s + 8 h .. + 7 (scale group s)
+            const uint32_t kb = kb0 + b, c = kb & 3u, hf = (kb >> 2) & 1u;
+            const uint32_t shl = 4u * (c >> 1), shh = 2u * c;
+            float ds[2][2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
+                const uint32_t qrow = lds0 + K6Q + ((b >> 2) & 1u) * MM2_6QUAD + 96u * rl;
+                const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * MM2_6HDR;
+                const uint32_t scw = *(const __attribute__((address_space(3))) uint32_t *) (uintptr_t) (
+                    hbase + 16u * rl + 4u * (2u * hf + (c >> 1)));  // scales[8 hf + 2c], + 1
+                const uint32_t dw = *(const __attribute__((address_space(3))) uint32_t *) (uintptr_t) (
+                    hbase + MM2_ROWS * 16u + 4u * rl);
+                const float d = (float) __builtin_bit_cast(_Float16, (uint16_t) (dw >> 16));
+                const uint32_t sco = 16u * (c & 1u);
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) ds[rt][s2] = d * (float) (int8_t) (uint8_t) (scw >> (sco + 8u * (uint32_t) s2));
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const mm2_u32x2 ql = *(const __attribute__((address_space(3))) mm2_u32x2 *) (uintptr_t) (
+                        qrow + 16u * (2u * (c & 1u) + (uint32_t) s) + 8u * h);
+                    const mm2_u32x2 qh = *(const __attribute__((address_space(3))) mm2_u32x2 *) (uintptr_t) (
+                        qrow + 64u + 16u * (uint32_t) s + 8u * h);
+                    const uint32_t w0 = ((ql[0] >> shl) & 0x0F0F0F0Fu) | (((qh[0] >> shh) & 0x03030303u) << 4);
+                    const uint32_t w1 = ((ql[1] >> shl) & 0x0F0F0F0Fu) | (((qh[1] >> shh) & 0x03030303u) << 4);
+                    bw[rt][s] = mm2_u6_to_f16(mm2_u32x2{w0, w1});
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    mm2_f32x16 sg0 = {}, sg1 = {};
+                    sg0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][0], bw[rt][0], sg0, 0, 0, 0);
+                    sg0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][0], bw[rt][0], sg0, 0, 0, 0);
+                    sg1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][1], bw[rt][1], sg1, 0, 0, 0);
+                    sg1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][1], bw[rt][1], sg1, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        acc[tt][rt][j] = fmaf(ds[rt][1], sg1[j], fmaf(ds[rt][0], sg0[j], acc[tt][rt][j]));
+                }
+            return;
+        }
         if constexpr (Q4K) {
             // this lane's 16 payload bytes of the pair (its k of both sub-blocks) and the
             // super-block header (d, dmin, 12 scale bytes) of each row tile: both stay in their
@@ -396,13 +490,17 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     copy(0, 0);
     if constexpr (Q8) qcopy(0, 0);
     if constexpr (Q4K) kcopy(0, 0, 0);
+    if constexpr (Q6K) k6copy(0);
     copy(min(1u, nb - 1u), 1);
     if constexpr (Q4K) kcopy(min(1u, nb - 1u), 1, 0);
+    if constexpr (Q6K) k6copy(min(1u, nb - 1u));
     auto step = [&](uint32_t b, uint32_t buf, uint32_t qb, bool odd) {
         // block b's copies have landed and every LDS read of block b - 1 has returned, in this wave;
         // then in every wave
         __builtin_amdgcn_sched_barrier(0);
-        if (Q5K)
+        if (Q6K)
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(9u));
+        else if (Q5K)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(8u));
         else if (Q4K)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
@@ -418,6 +516,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         if constexpr (Q8)
             if (!odd) qcopy(min(b + 2u, nb - 2u), (qb + 1u) % 3u);
         if constexpr (Q4K) kcopy(min(b + 2u, nb - 1u), (buf + 2u) % 3u, (qb + 1u) % 3u);
+        if constexpr (Q6K) k6copy(min(b + 2u, nb - 1u));
         __builtin_amdgcn_sched_barrier(0);
         compute(buf, qb, odd, b);
     };
@@ -477,3 +576,5 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 moearc_matmul2_q4_k_k(MatmulArgs a) { mm2_body<12>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moearc_matmul2_q5_k_k(MatmulArgs a) { mm2_body<13>(a); }
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moearc_matmul2_q6_k_k(MatmulArgs a) { mm2_body<14>(a); }

@@ -227,6 +227,8 @@ def test_matvec_refusals_and_empty_shapes(ctx):
     (QuantType.Q4_K, 96, 160, 1280), (QuantType.Q4_K, 128, 512, 2048),
     (QuantType.Q5_K, 64, 128, 256), (QuantType.Q5_K, 200, 300, 512), (QuantType.Q5_K, 130, 257, 1280),
     (QuantType.Q5_K, 128, 512, 2048),
+    (QuantType.Q6_K, 64, 128, 256), (QuantType.Q6_K, 200, 300, 512), (QuantType.Q6_K, 130, 257, 1280),
+    (QuantType.Q6_K, 128, 512, 2048),
     # grids of at most one work-group per CU split the reduction into k-slices (also above: every
     # case with 16 or more k-blocks and a small grid, K-quant slices on super-block bounds, a ragged
     # last slice) -- here a 128-token chunk's output projection at gpt-oss shapes (11 slices)
