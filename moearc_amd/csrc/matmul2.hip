@@ -223,6 +223,14 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
                             16u * ((lane & 1u) ^ ((k_row >> 3) & 1u));
     const uint8_t *k_hsrc = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes;
     const float *k_xsrc = a.xs + (uint64_t) min(t0 + 64u * (wave & 1u) + lane, a.n_tok - 1u) * (a.cols / 32u) + kb0;
+    // Q5_K header slots q of instruction i: waves 0 and 1 fill 0 .. 255, waves 2 and 3 256 .. 383
+    // (their second instruction repeats the first); slot q is row q / 3's 16-byte chunk q % 3
+    const uint8_t *k5hsrc[2];
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+        const uint32_t q = (wave < 2u ? 128u * wave + 64u * i : 128u + 64u * wave) + lane;
+        k5hsrc[i] = sg.w + (uint64_t) min(r0 + q / 3u, sg.rows - 1u) * sg.row_bytes + 16u * (q % 3u);
+    }
     auto kcopy = [&](uint32_t b, uint32_t buf, uint32_t qb) {
         const uint32_t kb = kb0 + b;  // super-block kb / 8, pair (kb % 8) / 2
         mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + KXS + buf * MM2_KXS + (wave & 1u) * 256u), k_xsrc + b);
@@ -231,12 +239,9 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         const uint32_t hbase = lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR;
         if constexpr (Q5K) {
 #pragma unroll
-            for (uint32_t i = 0; i < 2; ++i) {
-                const uint32_t slot0 = wave < 2u ? 128u * wave + 64u * i : 128u + 64u * wave;
-                const uint32_t q = slot0 + lane;
-                const uint8_t *src = sg.w + (uint64_t) min(r0 + q / 3u, sg.rows - 1u) * sg.row_bytes + 16u * (q % 3u);
-                mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + 16u * slot0), src + KSB * (uint64_t) (kb >> 3));
-            }
+            for (uint32_t i = 0; i < 2; ++i)
+                mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + 16u * (wave < 2u ? 128u * wave + 64u * i : 128u + 64u * wave)),
+                           k5hsrc[i] + KSB * (uint64_t) (kb >> 3));
         } else {
             mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), k_hsrc + KSB * (uint64_t) (kb >> 3));
         }
@@ -296,20 +301,26 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // q / 6's chunk q % 6, three copies a lane) and its super-block's scales and d (a 16-byte copy
     // and a dword copy per row: waves 2 and 3 repeat waves 0 and 1) -- every block, whichever of them
     // repeat the previous block's bytes, so each step issues the same five copies
+    // (each lane's three chunk sources within super-block 0 and their step per half super-block)
+    const uint8_t *k6src[3];
+    uint32_t k6hstep[3];
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i) {
+        const uint32_t q = 256u * i + 64u * wave + lane, r = q / 6u, c = q % 6u;  // ql chunks 0 .. 3, qh 4, 5
+        k6src[i] = sg.w + (uint64_t) min(r0 + r, sg.rows - 1u) * sg.row_bytes + 210u * (uint64_t) (kb0 >> 3) +
+                   (c < 4u ? 16u * c : 128u + 16u * (c - 4u));
+        k6hstep[i] = c < 4u ? 64u : 32u;
+    }
     auto k6copy = [&](uint32_t b) {
         const uint32_t kb = kb0 + b;  // super-block kb / 8, half (kb % 8) / 4
-        const uint64_t sbo = 210u * (uint64_t) (kb >> 3);
+        const uint64_t sbo = 210u * (uint64_t) (b >> 3);
         const uint32_t qbase = lds0 + K6Q + ((b >> 2) & 1u) * MM2_6QUAD;
 #pragma unroll
-        for (uint32_t i = 0; i < 3; ++i) {
-            const uint32_t slot0 = 256u * i + 64u * wave, q = slot0 + lane;
-            const uint32_t r = q / 6u, c = q % 6u;  // ql chunks 0 .. 3, qh chunks 4 and 5
-            const uint32_t off = c < 4u ? 64u * ((kb >> 2) & 1u) + 16u * c : 128u + 32u * ((kb >> 2) & 1u) + 16u * (c - 4u);
-            mm2_copy16(__builtin_amdgcn_readfirstlane(qbase + 16u * slot0),
-                       sg.w + (uint64_t) min(r0 + r, sg.rows - 1u) * sg.row_bytes + sbo + off);
-        }
+        for (uint32_t i = 0; i < 3; ++i)
+            mm2_copy16(__builtin_amdgcn_readfirstlane(qbase + 16u * (256u * i + 64u * wave)),
+                       k6src[i] + sbo + ((kb >> 2) & 1u) * k6hstep[i]);
         const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * MM2_6HDR;
-        const uint8_t *hrow = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes + sbo;
+        const uint8_t *hrow = k_hsrc + 210u * (uint64_t) (kb >> 3);
         mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), hrow + 192u);
         mm2_copy4(__builtin_amdgcn_readfirstlane(hbase + MM2_ROWS * 16u + (wave & 1u) * 256u), hrow + 206u);
     };
