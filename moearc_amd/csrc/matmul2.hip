@@ -57,6 +57,10 @@ __host__ __device__ constexpr uint32_t mm2_khdr(uint32_t ty) { return MM2_ROWS *
 // followed by a dword per row ending on d (bytes 206 .. 209; two buffers)
 constexpr uint32_t MM2_6QUAD = MM2_ROWS * 96u;
 constexpr uint32_t MM2_6HDR = MM2_ROWS * 20u;
+// MXFP4 (per work-group, after the activation buffers): each pair of 17-byte blocks' 34 bytes per
+// row, as two 16-byte chunks (bytes 0 .. 31) and a 4-byte tail (bytes 30 .. 33, which ends on the
+// pair's last byte, so no copy reads past a row); three buffers
+constexpr uint32_t MM2_XPAIR = MM2_ROWS * 36u;
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
@@ -150,7 +154,7 @@ __device__ __forceinline__ uint32_t mm2_lds4(uint32_t off) {
 
 template <uint32_t TY>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
-    constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13, Q6K = TY == 14;
+    constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13, Q6K = TY == 14, MX = TY == 39;
     constexpr uint32_t KSB = Q5K ? 176u : 144u, KQS = Q5K ? 48u : 16u;  // super-block bytes, qs offset
     constexpr uint32_t MM2_KHDR = mm2_khdr(TY);
     // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair
@@ -160,7 +164,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     constexpr uint32_t KXS = QBASE, KPAIR = KXS + MM2_NBUF * MM2_KXS, KHDR = KPAIR + MM2_NBUF * MM2_KPAIR;
     constexpr uint32_t K6Q = QBASE, K6H = K6Q + 2u * MM2_6QUAD;
     constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * MM2_QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR
-                             : Q6K ? 2u * MM2_6QUAD + 2u * MM2_6HDR : 0u;
+                             : Q6K ? 2u * MM2_6QUAD + 2u * MM2_6HDR : MX ? MM2_NBUF * MM2_XPAIR : 0u;
     __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + EXTRA];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -324,6 +328,21 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), hrow + 192u);
         mm2_copy4(__builtin_amdgcn_readfirstlane(hbase + MM2_ROWS * 16u + (wave & 1u) * 256u), hrow + 206u);
     };
+    // MXFP4: per k-block b the pair (b's and its partner's 34 bytes per row) into pair buffer qb --
+    // every block, the odd one repeating the even one's bytes, so each step issues the same two
+    // copies. Chunk slot q = 64 wave + lane holds row q / 2's chunk (q & 1) ^ ((row >> 3) & 1); the
+    // tails (rows 64 (wave & 1) + lane) sit after the 128 rows' chunks, waves 2 and 3 repeating
+    // waves 0 and 1.
+    const uint8_t *x_csrc = sg.w + (uint64_t) min(r0 + k_row, sg.rows - 1u) * sg.row_bytes + 17u * (uint64_t) kb0 +
+                            16u * ((lane & 1u) ^ ((k_row >> 3) & 1u));
+    const uint8_t *x_tsrc = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes +
+                            17u * (uint64_t) kb0 + 30u;
+    auto xcopy = [&](uint32_t b, uint32_t qb) {
+        const uint64_t po = 34u * (uint64_t) (b >> 1);
+        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + QBASE + qb * MM2_XPAIR + wave * 1024u), x_csrc + po);
+        mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + QBASE + qb * MM2_XPAIR + MM2_ROWS * 32u + (wave & 1u) * 256u),
+                  x_tsrc + po);
+    };
     // block b from activation buffer buf and (Q8_0, Q4_K) pair buffer qb, b odd: the pair's second block
     auto compute = [&](uint32_t buf, uint32_t qb, bool odd, uint32_t b) {
         half8_t ah[2][2], al[2][2], bw[2][2];
@@ -336,6 +355,67 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
                 ah[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off));
                 al[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off + MM2_HALF));
             }
+        if constexpr (MX) {
+            // block (odd: the pair's second) of 17 bytes: E8M0 exponent e, then element j in the low
+            // nibble of data byte j and element j + 16 in its high nibble. This lane's k are
+            // 16 h .. 16 h + 15: the low (h = 0) or high (h = 1) nibbles of all 16 data bytes.
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
+                const uint32_t prow = lds0 + QBASE + qb * MM2_XPAIR;
+                const uint32_t sw = (rl >> 3) & 1u;
+                const u32x4_t c0 = mm2_lds16(prow + 32u * rl + 16u * sw);          // bytes 0 .. 15
+                const u32x4_t c1 = mm2_lds16(prow + 32u * rl + 16u * (1u ^ sw));   // bytes 16 .. 31
+                const uint32_t tl = mm2_lds4(prow + MM2_ROWS * 32u + 4u * rl);     // bytes 30 .. 33
+                uint32_t dw[4], e;
+                if (!odd) {  // data bytes 1 .. 16
+                    dw[0] = __builtin_amdgcn_alignbyte(c0[1], c0[0], 1u);
+                    dw[1] = __builtin_amdgcn_alignbyte(c0[2], c0[1], 1u);
+                    dw[2] = __builtin_amdgcn_alignbyte(c0[3], c0[2], 1u);
+                    dw[3] = __builtin_amdgcn_alignbyte(c1[0], c0[3], 1u);
+                    e = c0[0] & 0xFFu;
+                } else {  // data bytes 18 .. 33
+                    dw[0] = __builtin_amdgcn_alignbyte(c1[1], c1[0], 2u);
+                    dw[1] = __builtin_amdgcn_alignbyte(c1[2], c1[1], 2u);
+                    dw[2] = __builtin_amdgcn_alignbyte(c1[3], c1[2], 2u);
+                    dw[3] = __builtin_amdgcn_alignbyte(tl >> 16, c1[3], 2u);
+                    e = (c1[0] >> 8) & 0xFFu;
+                }
+                d[rt] = __uint_as_float(e ? e << 23 : 0x00400000u);  // 2^(e - 127)
+                // codes of elements (16 h + 4 i ..): nibble h of the dword's bytes, paired into bytes
+                // 0 and 2 as (element, next element) for the two-value conversions
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    half8_t v;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint32_t x = (dw[2 * s + i] >> (4u * h)) & 0x0F0F0F0Fu;
+                        const uint32_t y = x | (x >> 4);
+                        const half2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(y, 1.0f, 0);
+                        const half2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(y, 1.0f, 2);
+                        v[4 * i] = p0[0];
+                        v[4 * i + 1] = p0[1];
+                        v[4 * i + 2] = p1[0];
+                        v[4 * i + 3] = p1[1];
+                    }
+                    bw[rt][s] = v;
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    mm2_f32x16 sblk = {};
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tt][s], bw[rt][s], sblk, 0, 0, 0);
+                        sblk = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tt][s], bw[rt][s], sblk, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[tt][rt][j] = fmaf(d[rt], sblk[j], acc[tt][rt][j]);
+                }
+            return;
+        }
         if constexpr (Q6K) {
             // k-block c of half super-block hf: low four bits from ql[64 hf + 32 (c & 1) + l]
             // (nibble c >> 1), high two from qh[32 hf + l] (bits 2c, 2c + 1), l the element; this
@@ -502,9 +582,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     if constexpr (Q8) qcopy(0, 0);
     if constexpr (Q4K) kcopy(0, 0, 0);
     if constexpr (Q6K) k6copy(0);
+    if constexpr (MX) xcopy(0, 0);
     copy(min(1u, nb - 1u), 1);
     if constexpr (Q4K) kcopy(min(1u, nb - 1u), 1, 0);
     if constexpr (Q6K) k6copy(min(1u, nb - 1u));
+    if constexpr (MX) xcopy(min(1u, nb - 1u), 0);
     auto step = [&](uint32_t b, uint32_t buf, uint32_t qb, bool odd) {
         // block b's copies have landed and every LDS read of block b - 1 has returned, in this wave;
         // then in every wave
@@ -516,7 +598,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         else if (Q4K)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
         else if (!Q8)
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(6u));
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(6u));  // F16: 4 + 2 copies; MXFP4: 4 + 2
         else if (odd)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
         else
@@ -528,6 +610,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
             if (!odd) qcopy(min(b + 2u, nb - 2u), (qb + 1u) % 3u);
         if constexpr (Q4K) kcopy(min(b + 2u, nb - 1u), (buf + 2u) % 3u, (qb + 1u) % 3u);
         if constexpr (Q6K) k6copy(min(b + 2u, nb - 1u));
+        if constexpr (MX) xcopy(min(b + 2u, nb - 1u), (qb + 1u) % 3u);
         __builtin_amdgcn_sched_barrier(0);
         compute(buf, qb, odd, b);
     };
@@ -589,3 +672,5 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 moearc_matmul2_q5_k_k(MatmulArgs a) { mm2_body<13>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moearc_matmul2_q6_k_k(MatmulArgs a) { mm2_body<14>(a); }
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moearc_matmul2_mxfp4_k(MatmulArgs a) { mm2_body<39>(a); }

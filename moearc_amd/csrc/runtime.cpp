@@ -89,7 +89,7 @@ struct moearc_ctx {
     hipFunction_t f_mv[7][4] = {};  // matvec: format (F32 F16 Q8_0 Q4_K Q5_K Q6_K MXFP4) x pieces per lane 1/2/4/8
     hipFunction_t f_add = nullptr, f_read_floor = nullptr, f_mfma_floor = nullptr;
     hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_split8 = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
-    hipFunction_t f_mm2[5] = {};  // Q8_0, F16, Q4_K, Q5_K, Q6_K: 128 x 128 tiles on the 32x32x16 MFMA
+    hipFunction_t f_mm2[6] = {};  // Q8_0, F16, Q4_K, Q5_K, Q6_K, MXFP4: 128 x 128 tiles on the 32x32x16 MFMA
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     float *mm_part = nullptr;   // the k-slices' sums of split chunk products
@@ -621,6 +621,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm2[2], "moearc_matmul2_q4_k_k"},
         {&c->f_mm2[3], "moearc_matmul2_q5_k_k"},
         {&c->f_mm2[4], "moearc_matmul2_q6_k_k"},
+        {&c->f_mm2[5], "moearc_matmul2_mxfp4_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
         {&c->f_split8, "moearc_split_f16_v8_k"},
@@ -1421,17 +1422,18 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
         n_rows += m[i].rows;
         tiles128 += (m[i].rows + 127) / 128;
     }
-    // Q8_0, F16 and the K-quants over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
-    // (matmul2.hip; Q8_0 weights arrive there in pairs of k-blocks, so its rows must hold an even
-    // number of them). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
+    // Every format over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
+    // (matmul2.hip; Q8_0 and MXFP4 weights arrive there in pairs of k-blocks, so their rows must
+    // hold an even number of them). Otherwise 32 rows per wave halves the activation loads per MFMA, but only
     // pays while the launch still has about two work-groups per CU; shorter chunks take 16.
     hipFunction_t f;
     unsigned long rows_per_tile;
     unsigned gy;
-    const bool mm2 = (ty == 1u || ty == 12u || ty == 13u || ty == 14u || (ty == 8u && (n_cols / 32) % 2 == 0)) &&
+    const bool pairs = ty == 8u || ty == 39u;
+    const bool mm2 = (ty == 1u || ty == 12u || ty == 13u || ty == 14u || (pairs && (n_cols / 32) % 2 == 0)) &&
                      n_tok >= 64;
     if (mm2) {
-        f = c->f_mm2[ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : 4];
+        f = c->f_mm2[ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 14u ? 4 : 5];
         rows_per_tile = 128;
         gy = (unsigned) ((n_tok + 127) / 128);
     } else {
@@ -1465,9 +1467,9 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     // chunks of one or two 128-token tiles and two above (measured on gpt-oss blocks: at 128 and 256
     // tokens the reduction's traffic, which grows with the slices, outweighs a second work-group per
     // CU; at 512 the reverse); MOEARC_MM_SPLIT_WG sets the aim. K-quant slices start on a
-    // 256-element super-block (a multiple of 8 k-blocks), matmul2.hip's Q8_0 slices on a pair.
+    // 256-element super-block (a multiple of 8 k-blocks), matmul2.hip's Q8_0 and MXFP4 slices on a pair.
     const uint64_t nb = n_cols / 32, tiles = (uint64_t) gx * gy;
-    const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : (mm2 && ty == 8u) ? 2 : 1;
+    const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : (mm2 && pairs) ? 2 : 1;
     uint64_t slices = 1, kb_per = nb;
     const uint64_t aim = c->mm_split_wg >= 0 ? (uint64_t) c->mm_split_wg : gy <= 2 ? 1 : 2;
     if (tiles <= kMmCUs && nb >= 8 && aim) {

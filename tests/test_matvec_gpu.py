@@ -229,6 +229,9 @@ def test_matvec_refusals_and_empty_shapes(ctx):
     (QuantType.Q5_K, 128, 512, 2048),
     (QuantType.Q6_K, 64, 128, 256), (QuantType.Q6_K, 200, 300, 512), (QuantType.Q6_K, 130, 257, 1280),
     (QuantType.Q6_K, 128, 512, 2048),
+    # MXFP4 on the 128 x 128 tiles (pairs of 17-byte blocks; odd block counts take the 16x16 kernels)
+    (QuantType.MXFP4, 64, 128, 64), (QuantType.MXFP4, 200, 300, 192), (QuantType.MXFP4, 130, 257, 2880),
+    (QuantType.MXFP4, 96, 160, 96), (QuantType.MXFP4, 128, 512, 2048),
     # grids of at most one work-group per CU split the reduction into k-slices (also above: every
     # case with 16 or more k-blocks and a small grid, K-quant slices on super-block bounds, a ragged
     # last slice) -- here a 128-token chunk's output projection at gpt-oss shapes (11 slices)
