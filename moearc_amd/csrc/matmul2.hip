@@ -1,10 +1,11 @@
-// Chunk-form projections for Q8_0 and F16 weights on v_mfma_f32_32x32x16_f16:
-// Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the tokens of a prompt chunk -- the GEMM that the
-// reference's prefill performs as one matvec per token (moe.rs:1942-1959, 2063-2071;
+// Chunk-form projections on v_mfma_f32_32x32x16_f16, for F16, Q8_0, Q4_K, Q5_K, Q6_K and MXFP4
+// weights: Y[t][r] = sum_c W[r][c] X[t][c] (+ bias[r]) for the tokens of a prompt chunk -- the GEMM
+// that the reference's prefill performs as one matvec per token (moe.rs:1942-1959, 2063-2071;
 // kernels.cpp:1046-1111). Precision is matmul.hip's: X is split into f16 hi + lo on the host side of
-// the launch (x - hi - lo <= 2^-22 |x|), a Q8_0 block's payload enters the MFMA as exact f16
-// integers, each 32-wide block's f32 sum q . (hi + lo) is scaled by the block's d in f32; F16
-// weights enter as they are. Activations must stay below 65504 in magnitude.
+// the launch (x - hi - lo <= 2^-22 |x|), a block's payload enters the MFMA as exact f16 integers
+// (E2M1 code points for MXFP4), each 32-wide block's (Q6_K: 16-wide group's) f32 sum q . (hi + lo)
+// is scaled by the block's factor in f32 (and, for Q4_K and Q5_K, its min times the activation's
+// block sum subtracted); F16 weights enter as they are. Activations must stay below 65504.
 //
 // The product is computed transposed, D[token][row] = X . W^T, so that the weight rows are the MFMA's
 // N side: lane l holds D column l % 32 -- one weight row -- in all 16 of its accumulators, and a
