@@ -23,10 +23,11 @@ N + 1 for `s_nop N`):
      result (v_exp_f32 and the like) not by another VALU instruction within 1, and an SGPR written by
      v_readfirstlane / v_readlane not read by a VALU instruction within 2;
   7. the data registers of a vector-memory store of more than 8 bytes (dwordx3 / dwordx4) are not
-     written by the next instruction: the store reads them after issue and needs 1 wait state
-     (hipcc inserts it after its own stores, not after an inline-asm store -- a 16-byte asm store
-     followed at once by a VALU write of its data stored the new value) -- in every kernel of the
-     code object.
+     written within 2 wait states of it: the store reads them after issue (hipcc puts s_nop 1
+     between its own such stores and a VALU write of their data on gfx950, and nothing after an
+     inline-asm store -- a 16-byte asm store followed at once by a VALU write of its data stored the
+     new value, and with one wait state it still did, now and then, under load) -- in every kernel
+     of the code object.
 
 Usage: python check_asm_hazards.py [kernel-name-prefix ...]   (default: moearc_attn_prefill_g)
 Exit status 1 when a hazard is found.
@@ -252,7 +253,7 @@ def load_hazards(ins):
     return out
 
 
-STORE_WAIT = 1  # VALU write of a >64-bit store's data VGPRs after the store
+STORE_WAIT = 2  # wait states before a VALU write of a >64-bit store's data VGPRs (gfx950)
 
 
 def store_data_hazards(ins, labels):

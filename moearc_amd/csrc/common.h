@@ -22,10 +22,12 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // microseconds of the dispatch. It pays for whole-line writes (the prefill's output rows); 4-byte
 // pieces written this way measured slower (the chunk product's epilogue: +7%), the L2 no longer
 // merging them into lines.
-// The store reads its 16 data bytes after issue: the next instruction must not overwrite them (1
-// wait state, which hipcc inserts after its own stores but not after an asm one).
+// The store reads its 16 data bytes after issue: no VALU instruction may overwrite them within 2
+// wait states on gfx950 (hipcc puts s_nop 1 between its own 16-byte stores and such a write, but
+// knows nothing of an asm one). With a single wait state the split's stores wrote, now and then
+// under load, the register's next value (the f32 of hi) into the first dword of a piece.
 __device__ __forceinline__ void store_through16(void *p, u32x4_t v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" : : "v"(p), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void store_through8(void *p, u32x2_t v) {
