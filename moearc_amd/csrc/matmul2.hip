@@ -13,7 +13,10 @@
 // feeds k 16h + 8s .. + 7 to the MFMA of k slice s, for both operands.
 //
 // Work-group: 4 waves over 128 tokens x 128 weight rows; wave w takes tokens 64 (w & 1) .. + 63 and
-// rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. Both operands reach LDS by LDS DMA
+// rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. F16 and Q8_0 also come as a wide form, 8
+// waves over 128 tokens x 256 rows, one work-group per CU: the same waves' steps, with each
+// k-block's copies shared by twice the rows (the CU's intake of copied bytes costs time beside
+// the MFMAs, whatever the copies' destination). Both operands reach LDS by LDS DMA
 // (global_load_lds_dwordx4: 16 bytes per lane, written at the instruction's LDS base + 16 lane),
 // two k-blocks ahead, and are read from there in operand layout; one barrier per k-block. Every
 // copy reads 64-byte row pieces, four lanes per row: a memory instruction costs in proportion to
@@ -36,15 +39,13 @@
 namespace {
 
 constexpr uint32_t MM2_TOK = 128;   // tokens per work-group
-constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group
+constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group (the wide F16 / Q8_0 form: 256)
 constexpr uint32_t MM2_HALF = MM2_TOK * 64u;    // bytes of one half (hi or lo) of an activation tile
 constexpr uint32_t MM2_ACT = 2u * MM2_HALF;     // one k-block's activation tile
 constexpr uint32_t MM2_NBUF = 3u;
-// Q8_0 pair buffer: the rows' 64-byte pieces, their tails (rows 0 .. 63 from wave 0, 64 .. 127 from
-// wave 1), and 512 bytes that waves 2 and 3 fill with the same tails (so every wave issues the same
-// copies; nothing reads them)
-constexpr uint32_t MM2_QTAIL = MM2_ROWS * 64u;
-constexpr uint32_t MM2_QPAIR = MM2_QTAIL + 4u * 256u;
+// Q8_0 pair buffer (mm2_body's QPAIR): the rows' 64-byte pieces, their tails (rows 0 .. 63 from
+// wave 0, 64 .. 127 from wave 1, ...), and 256 bytes per remaining wave that it fills with the same
+// tails as the wave it repeats (so every wave issues the same copies; nothing reads them)
 
 // Q4_K, Q5_K (per work-group, after the activation buffers): the k-blocks' per-token block sums
 // (128 floats, three buffers), each pair of sub-blocks' 32 payload bytes per row (the low nibbles
@@ -153,37 +154,44 @@ __device__ __forceinline__ uint32_t mm2_lds4(uint32_t off) {
     return *(const __attribute__((address_space(3))) uint32_t *) (uintptr_t) off;
 }
 
-template <uint32_t TY>
+template <uint32_t TY, bool WIDE = false>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13, Q6K = TY == 14, MX = TY == 39;
     constexpr uint32_t KSB = Q5K ? 176u : 144u, KQS = Q5K ? 48u : 16u;  // super-block bytes, qs offset
     constexpr uint32_t MM2_KHDR = mm2_khdr(TY);
+    // WIDE (F16, Q8_0): eight waves over 128 tokens x 256 rows, one work-group per CU; the
+    // per-wave tiles and steps are the same, each k-block's copies are shared by twice the rows
+    static_assert(!WIDE || TY == 1 || TY == 8, "wide tiles: F16 and Q8_0");
+    constexpr uint32_t NW = WIDE ? 8u : 4u;                 // waves
+    constexpr uint32_t ROWS = WIDE ? 2u * MM2_ROWS : MM2_ROWS;  // weight rows per work-group
+    constexpr uint32_t NAI = 16u / NW;                      // activation copies per wave and step
+    constexpr uint32_t QTAIL = ROWS * 64u, QPAIR = QTAIL + NW * 256u;
     // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair
     // buffers, (Q4_K) the block sums, pair and header buffers
-    constexpr uint32_t BUF = MM2_ACT + (TY == 1 ? MM2_ROWS * 64u : 0u);
+    constexpr uint32_t BUF = MM2_ACT + (TY == 1 ? ROWS * 64u : 0u);
     constexpr uint32_t QBASE = MM2_NBUF * BUF;
     constexpr uint32_t KXS = QBASE, KPAIR = KXS + MM2_NBUF * MM2_KXS, KHDR = KPAIR + MM2_NBUF * MM2_KPAIR;
     constexpr uint32_t K6Q = QBASE, K6H = K6Q + 2u * MM2_6QUAD;
-    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * MM2_QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR
+    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR
                              : Q6K ? 2u * MM2_6QUAD + 2u * MM2_6HDR : MX ? MM2_NBUF * MM2_XPAIR : 0u;
     __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + EXTRA];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31u, h = lane >> 5;
     const MmSegView sg = mm_seg(a, blockIdx.x);
-    const uint32_t t0 = blockIdx.y * MM2_TOK, r0 = sg.tile * MM2_ROWS;
+    const uint32_t t0 = blockIdx.y * MM2_TOK, r0 = sg.tile * ROWS;
     // this work-group's k-slice: blocks kb0 .. kb0 + nb (Q8_0: both even)
     const uint32_t kb0 = blockIdx.z * a.kb_per, nb = min(a.kb_per, a.cols / 32u - kb0);
     const uint32_t lds0 =
         __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) tiles);
 
-    // Activation copies: instruction i of wave w fills region R = 4 w + i (1 KiB): half R >> 3,
+    // Activation copies: instruction i of wave w fills region R = NAI w + i (1 KiB): half R >> 3,
     // tokens 16 (R & 7) .. + 15; lane L writes slot L of the region = chunk position L & 3 of token
     // L >> 2, which holds chunk (L & 3) ^ swz(token).
-    const uint16_t *xsrc[4];
+    const uint16_t *xsrc[NAI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t R = 4u * wave + (uint32_t) i;
+    for (int i = 0; i < (int) NAI; ++i) {
+        const uint32_t R = NAI * wave + (uint32_t) i;
         const uint32_t tok = 16u * (R & 7u) + (lane >> 2);
         const uint32_t c = (lane & 3u) ^ mm2_swz(tok);
         const uint64_t tg = min(t0 + tok, a.n_tok - 1u);
@@ -192,7 +200,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // Weight copies: instruction i of wave w fills rows 16 (2 w + i) .. + 15 of the 64-byte pieces
     // (F16: one k-block; Q8_0: bytes 0 .. 63 of a pair), lane L row 16 (2 w + i) + (L >> 2), whose
     // position L & 3 holds chunk (L & 3) ^ swz(row); Q8_0: wave w also copies the tails of rows
-    // 64 (w & 1) .. + 63 (lane L: row 64 (w & 1) + L). Rows past the last copy the last row (not stored).
+    // 64 (w & 1) .. + 63 (lane L: row 64 (w & 1) + L; wide: 64 (w & 3) + L, waves 4-7 repeating
+    // 0-3 into slots nothing reads). Rows past the last copy the last row (not stored).
     constexpr uint32_t wbb = Q8 ? 34u : 64u;  // bytes of a row per k-block
     const uint8_t *wsrc[2];
 #pragma unroll
@@ -202,13 +211,13 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
                   16u * ((lane & 3u) ^ mm2_swz(rl));
     }
     const uint8_t *wtail =
-        sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes + 34u * (uint64_t) kb0 + 64u;
+        sg.w + (uint64_t) min(r0 + 64u * (wave % (ROWS / 64u)) + lane, sg.rows - 1u) * sg.row_bytes + 34u * (uint64_t) kb0 + 64u;
 
     // block b's activations (F16: and weights) into buffer buf
     auto copy = [&](uint32_t b, uint32_t buf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + buf * BUF + (4u * wave + (uint32_t) i) * 1024u),
+        for (int i = 0; i < (int) NAI; ++i)
+            mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + buf * BUF + (NAI * wave + (uint32_t) i) * 1024u),
                        xsrc[i] + 32u * b);
         if constexpr (TY == 1) {
 #pragma unroll
@@ -253,11 +262,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     };
     // Q8_0: the weights of blocks b, b + 1 (b even) into pair buffer qb
     auto qcopy = [&](uint32_t b, uint32_t qb) {
-        const uint32_t base = lds0 + QBASE + qb * MM2_QPAIR;
+        const uint32_t base = lds0 + QBASE + qb * QPAIR;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             mm2_copy16(__builtin_amdgcn_readfirstlane(base + (2u * wave + (uint32_t) i) * 1024u), wsrc[i] + 34u * b);
-        mm2_copy4(__builtin_amdgcn_readfirstlane(base + MM2_QTAIL + wave * 256u), wtail + 34u * b);
+        mm2_copy4(__builtin_amdgcn_readfirstlane(base + QTAIL + wave * 256u), wtail + 34u * b);
     };
 
     mm2_f32x16 acc[2][2];
@@ -292,7 +301,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
             woff[rt][0] = base + 16u * (h ^ sw);
             woff[rt][1] = base + 16u * ((h + 1u) ^ sw);
             woff[rt][2] = base + 16u * ((h + 2u) ^ sw);
-            woff[rt][3] = h ? lds0 + QBASE + MM2_QTAIL + rl * 4u : base + 16u * (3u ^ sw);
+            woff[rt][3] = h ? lds0 + QBASE + QTAIL + rl * 4u : base + 16u * (3u ^ sw);
             woff[rt][4] = base + 16u * sw;
             woff[rt][5] = base + 16u * (2u ^ sw);
         } else {
@@ -526,7 +535,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             if constexpr (Q8) {
-                const uint32_t qo = qb * MM2_QPAIR;
+                const uint32_t qo = qb * QPAIR;
                 u32x4_t q;
                 uint32_t dd;
                 if (!odd) {  // window bytes 2 + 16h .. 17 + 16h
@@ -574,11 +583,13 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // k-block b's activations in buffer b % 3 (F16: its weights beside them); Q8_0: pair b / 2 in
     // pair buffer (b / 2) % 3. Step b: wait for block b's copies (b even, Q8_0: and its pair's), meet
     // the other waves (every wave has finished block b - 1, whose buffers are refilled next),
-    // request block b + 2 (Q8_0, b even: and pair b + 2, b + 3), compute block b. Copies issued after
-    // block b's activations, which may stay in flight: F16, block b + 1's (6); Q8_0, b even: pair b's
-    // weights, then block b + 1's activations (4); b odd: block b + 1's activations and pair b + 1's
-    // weights (7). Past the end, the requests repeat the last block and pair into the buffers next
-    // in line, which nothing reads, so every step issues the same copies.
+    // request block b + 2 (Q8_0, b even: and pair b + 2, b + 3), compute block b. A wave issues NAI
+    // activation copies per block (4; 2 in the wide form), F16 two weight copies beside them, Q8_0
+    // three pair copies after every even block's. Copies that may stay in flight at step b: F16,
+    // block b + 1's (NAI + 2); Q8_0, b even: block b + 1's activations (NAI); b odd: block b + 1's
+    // activations and pair b + 1's weights (NAI + 3). Past the end, the requests repeat the last
+    // block and pair into the buffers next in line, which nothing reads, so every step issues the
+    // same copies.
     copy(0, 0);
     if constexpr (Q8) qcopy(0, 0);
     if constexpr (Q4K) kcopy(0, 0, 0);
@@ -599,11 +610,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         else if (Q4K)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
         else if (!Q8)
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(6u));  // F16: 4 + 2 copies; MXFP4: 4 + 2
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI + 2u));  // F16: NAI + 2 copies; MXFP4: 4 + 2
         else if (odd)
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI + 3u));
         else
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(4u));
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         copy(min(b + 2u, nb - 1u), (buf + 2u) % 3u);
@@ -667,6 +678,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_q8_0_k(MatmulArgs a) { mm2_body<8>(a); }
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_f16_k(MatmulArgs a) { mm2_body<1>(a); }
+extern "C" __global__ void __launch_bounds__(512) moearc_matmul2w_q8_0_k(MatmulArgs a) { mm2_body<8, true>(a); }
+extern "C" __global__ void __launch_bounds__(512) moearc_matmul2w_f16_k(MatmulArgs a) { mm2_body<1, true>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moearc_matmul2_q4_k_k(MatmulArgs a) { mm2_body<12>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))

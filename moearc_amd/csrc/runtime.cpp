@@ -90,6 +90,7 @@ struct moearc_ctx {
     hipFunction_t f_add = nullptr, f_read_floor = nullptr, f_mfma_floor = nullptr;
     hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_split8 = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
     hipFunction_t f_mm2[6] = {};  // Q8_0, F16, Q4_K, Q5_K, Q6_K, MXFP4: 128 x 128 tiles on the 32x32x16 MFMA
+    hipFunction_t f_mm2w[2] = {};  // Q8_0, F16: 128 tokens x 256 rows, eight waves
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     float *mm_part = nullptr;   // the k-slices' sums of split chunk products
@@ -131,6 +132,7 @@ struct moearc_ctx {
     // of the issue slots; with a = 1.41, b = 0.77 the younger keeps priority 1 for as long as makes
     // the two end together (loop ends 104.4 / 104.8 µs against 94.9 / 108.0 without).
     float pf_boost_a = 1.41f, pf_boost_b = 0.77f;
+    int mm_wide = -1;  // MOEARC_MM_WIDE: the chunk product's wide tiles (0: never, 1: always, -1: by grid)
     int mm_split_wg = -1;  // MOEARC_MM_SPLIT_WG: work-groups per CU the chunk product's split-K aims at (0: none; -1: by chunk)
 };
 
@@ -622,6 +624,8 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm2[3], "moearc_matmul2_q5_k_k"},
         {&c->f_mm2[4], "moearc_matmul2_q6_k_k"},
         {&c->f_mm2[5], "moearc_matmul2_mxfp4_k"},
+        {&c->f_mm2w[0], "moearc_matmul2w_q8_0_k"},
+        {&c->f_mm2w[1], "moearc_matmul2w_f16_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
         {&c->f_split8, "moearc_split_f16_v8_k"},
@@ -689,6 +693,7 @@ moearc_ctx *moearc_ctx_create(void) {
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && ncu > 0)
             c->n_cu = (unsigned) ncu;
     }
+    if (const char *s = std::getenv("MOEARC_MM_WIDE")) c->mm_wide = std::strtoul(s, nullptr, 10) ? 1 : 0;
     if (const char *s = std::getenv("MOEARC_MM_SPLIT_WG")) c->mm_split_wg = (int) std::min(8ul, std::strtoul(s, nullptr, 10));
     return c;
 }
@@ -1417,10 +1422,11 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     a.cols = (uint32_t) n_cols;
     a.n_tok = (uint32_t) n_tok;
     a.n_seg = n_mat;
-    unsigned long n_rows = 0, tiles128 = 0;
+    unsigned long n_rows = 0, tiles128 = 0, tiles256 = 0;
     for (unsigned i = 0; i < n_mat; ++i) {
         n_rows += m[i].rows;
         tiles128 += (m[i].rows + 127) / 128;
+        tiles256 += (m[i].rows + 255) / 256;
     }
     // Every format over chunks of at least 64 tokens: 128 x 128 tiles on the 32x32x16 MFMA
     // (matmul2.hip; Q8_0 and MXFP4 weights arrive there in pairs of k-blocks, so their rows must
@@ -1432,7 +1438,19 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     const bool pairs = ty == 8u || ty == 39u;
     const bool mm2 = (ty == 1u || ty == 12u || ty == 13u || ty == 14u || (pairs && (n_cols / 32) % 2 == 0)) &&
                      n_tok >= 64;
-    if (mm2) {
+    // F16 and Q8_0 take work-groups of eight waves over 128 tokens x 256 rows (one per CU) when
+    // those tiles alone cover every CU: each k-block's copies into LDS then serve twice the rows,
+    // and the copies' volume is what the CU pays for beside the MFMAs (at gpt-oss's attn_q over 2048
+    // tokens F16 -20%, Q8_0 -4%; with fewer tiles than CUs the 128 x 128 form is faster).
+    const bool wide = mm2 && (ty == 1u || ty == 8u) &&
+                      (c->mm_wide > 0 || (c->mm_wide < 0 && tiles256 * ((n_tok + 127) / 128) >= kMmCUs));
+    unsigned threads = 256;
+    if (wide) {
+        f = c->f_mm2w[ty == 8u ? 0 : 1];
+        rows_per_tile = 256;
+        threads = 512;
+        gy = (unsigned) ((n_tok + 127) / 128);
+    } else if (mm2) {
         f = c->f_mm2[ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 14u ? 4 : 5];
         rows_per_tile = 128;
         gy = (unsigned) ((n_tok + 127) / 128);
@@ -1471,7 +1489,7 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     const uint64_t nb = n_cols / 32, tiles = (uint64_t) gx * gy;
     const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : (mm2 && pairs) ? 2 : 1;
     uint64_t slices = 1, kb_per = nb;
-    const uint64_t aim = c->mm_split_wg >= 0 ? (uint64_t) c->mm_split_wg : gy <= 2 ? 1 : 2;
+    const uint64_t aim = c->mm_split_wg >= 0 ? (uint64_t) c->mm_split_wg : (gy <= 2 || wide) ? 1 : 2;
     if (tiles <= kMmCUs && nb >= 8 && aim) {
         const uint64_t fill = (kMmCUs + tiles - 1) / tiles;  // slices for one work-group on every CU
         const uint64_t want = std::max<uint64_t>(1, std::min<uint64_t>(std::max(fill, aim * kMmCUs / tiles), nb / 4));
@@ -1480,7 +1498,7 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
         slices = (nb + kb_per - 1) / kb_per;
     }
     a.kb_per = (uint32_t) kb_per;
-    if (slices < 2) return launch2d(c, f, gx, gy, 256, a, what, n_rows, n_tok);
+    if (slices < 2) return launch2d(c, f, gx, gy, threads, a, what, n_rows, n_tok);
     const size_t part = (size_t) slices * a.part_stride;
     if (part > c->mm_part_floats) {
         if (c->mm_part) {
@@ -1501,7 +1519,7 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
         }
     }
     ++c->scope_depth;
-    int rc = launch3d(c, f, gx, gy, (unsigned) slices, 256, a, what, n_rows, n_tok);
+    int rc = launch3d(c, f, gx, gy, (unsigned) slices, threads, a, what, n_rows, n_tok);
     if (rc == OK) {
         const uint64_t n = a.part_stride;
         rc = launch2d(c, c->f_mm_reduce, (unsigned) std::min<uint64_t>((n + 255) / 256, 65536), 1, 256,

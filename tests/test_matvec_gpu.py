@@ -259,6 +259,74 @@ def test_chunk_matmul_meets_the_matvec_bound(ctx, ty, n_tok, rows, cols):
     assert worst <= 1.0
 
 
+def _matmul_with(env, ty, w, x, bias, n_tok, rows, cols):
+    """The chunk product in a fresh context created under the given environment (the launch-shape
+    switches are read at context creation)."""
+    import os
+    from moearc_amd import Context
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        with Context() as c:
+            y = c.alloc(n_tok * rows * 4)
+            c.matmul_q(ty, y, c.upload(w), c.upload(x), c.upload(bias), n_tok, rows, cols)
+            return c.download(y, np.float32, (n_tok, rows))
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def _within_bound(label, got, ty, w, x, bias, rows, cols, tokens):
+    worst = 0.0
+    for t in tokens:
+        want, absum = oracle.matvec_q(int(ty), w, x[t], rows, cols, n_threads=16)
+        err = np.abs(got[t].astype(np.float64) - (want.astype(np.float64) + bias))
+        tol = fx.matvec_tolerance(cols, absum) + 2.0 * 32 * 2.0 ** -24 * absum + 2.0 ** -23 * np.abs(want + bias)
+        worst = max(worst, float(np.max(err / tol)))
+    print(f"{label}: worst / bound = {worst:.3f}", flush=True)
+    assert worst <= 1.0
+
+
+@pytest.mark.parametrize("ty,n_tok,rows,cols", [
+    # F16 and Q8_0 on eight-wave work-groups of 128 tokens x 256 rows: ragged row and token tiles,
+    # k-block counts around the three-deep pipeline and its six-block unroll, a 128-token chunk's
+    # output projection at gpt-oss shapes
+    (QuantType.Q8_0, 200, 300, 64), (QuantType.Q8_0, 130, 513, 320), (QuantType.Q8_0, 64, 256, 448),
+    (QuantType.Q8_0, 100, 260, 192), (QuantType.F16, 100, 257, 32), (QuantType.F16, 190, 600, 160),
+    (QuantType.F16, 65, 136, 352), (QuantType.Q8_0, 128, 2880, 4096)], ids=str)
+def test_chunk_matmul_wide_tiles(ty, n_tok, rows, cols):
+    # forced on (MOEARC_MM_WIDE=1) against forced off: without split-K both accumulate every output
+    # in the same k order, so they must agree bit for bit; with the split-K the wide form's launch
+    # picks, the oracle's bound
+    w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x3B3 + rows)
+    x = fx.synth.unit(0x3B4 + cols, n_tok * cols).reshape(n_tok, cols)
+    bias = fx.synth.unit(0x3B5, rows)
+    narrow = _matmul_with({"MOEARC_MM_WIDE": "0", "MOEARC_MM_SPLIT_WG": "0"}, ty, w, x, bias, n_tok, rows, cols)
+    wide = _matmul_with({"MOEARC_MM_WIDE": "1", "MOEARC_MM_SPLIT_WG": "0"}, ty, w, x, bias, n_tok, rows, cols)
+    assert np.array_equal(wide.view(np.uint32), narrow.view(np.uint32))
+    split = _matmul_with({"MOEARC_MM_WIDE": "1"}, ty, w, x, bias, n_tok, rows, cols)
+    _within_bound(f"wide {ty.name} {n_tok}x{rows}x{cols}", split, ty, w, x, bias, rows, cols, range(n_tok))
+
+
+@pytest.mark.parametrize("ty", [QuantType.Q8_0, QuantType.F16], ids=lambda t: t.name)
+def test_chunk_matmul_full_size_attn_q(ctx, ty):
+    # gpt-oss's attn_q over a config-4 chunk (2048 tokens x 4096 rows x 2880), which takes the wide
+    # tiles by default (256 of them): every row of 40 tokens spread over all 16 token tiles
+    n_tok, rows, cols = 2048, 4096, 2880
+    w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x3C3)
+    x = fx.synth.unit(0x3C4, n_tok * cols).reshape(n_tok, cols)
+    bias = fx.synth.unit(0x3C5, rows)
+    y = ctx.alloc(n_tok * rows * 4)
+    ctx.matmul_q(ty, y, ctx.upload(w), ctx.upload(x), ctx.upload(bias), n_tok, rows, cols)
+    got = ctx.download(y, np.float32, (n_tok, rows))
+    assert np.all(np.isfinite(got))
+    tokens = sorted(set(range(0, n_tok, 53)) | {1, 127, 128, n_tok - 1})
+    _within_bound(f"matmul {ty.name} {n_tok}x{rows}x{cols}", got, ty, w, x, bias, rows, cols, tokens)
+
+
 def test_chunk_matmul_activation_alignment(ctx):
     # the activation's f16 split runs eight elements per thread from a 16-byte aligned x and one
     # element per thread otherwise: the same arithmetic, so the products agree to the bit
