@@ -311,11 +311,14 @@ def test_chunk_matmul_wide_tiles(ty, n_tok, rows, cols):
     _within_bound(f"wide {ty.name} {n_tok}x{rows}x{cols}", split, ty, w, x, bias, rows, cols, range(n_tok))
 
 
-@pytest.mark.parametrize("ty", [QuantType.Q8_0, QuantType.F16], ids=lambda t: t.name)
-def test_chunk_matmul_full_size_attn_q(ctx, ty):
-    # gpt-oss's attn_q over a config-4 chunk (2048 tokens x 4096 rows x 2880), which takes the wide
-    # tiles by default (256 of them): every row of 40 tokens spread over all 16 token tiles
-    n_tok, rows, cols = 2048, 4096, 2880
+@pytest.mark.parametrize("ty,rows,cols", [
+    # gpt-oss's attn_q over a config-4 chunk (Q8_0 and F16 take the wide tiles there by default)
+    (QuantType.Q8_0, 4096, 2880), (QuantType.F16, 4096, 2880), (QuantType.MXFP4, 4096, 2880),
+    # Qwen3-30B-A3B's attn_q (K-quant rows of whole super-blocks)
+    (QuantType.Q4_K, 4096, 2048), (QuantType.Q5_K, 4096, 2048), (QuantType.Q6_K, 4096, 2048)], ids=str)
+def test_chunk_matmul_full_size_attn_q(ctx, ty, rows, cols):
+    # a 2048-token chunk: every row of 40 tokens spread over all 16 token tiles
+    n_tok = 2048
     w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x3C3)
     x = fx.synth.unit(0x3C4, n_tok * cols).reshape(n_tok, cols)
     bias = fx.synth.unit(0x3C5, rows)
