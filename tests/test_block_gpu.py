@@ -162,6 +162,19 @@ def test_gpt_oss_shape_chunks_then_decode(ctx, n_swa):
     blk.step(ctx, 1, 25, f"{label}, decode step")
 
 
+@pytest.mark.parametrize("n_swa", [0, 128])
+def test_gpt_oss_shape_long_chunk(ctx, n_swa):
+    # one 1024-token chunk through the block at gpt-oss-20b's shape: eight token tiles in every
+    # launch (the q/k/v product without split-K, the output projection with it, the group-8
+    # prefill over 1024 rows), then a decode step
+    blk = Block(ctx, (8, 8, 8, 8), 0xB70C + n_swa, n_swa=n_swa, n_ctx=1088, chunk=1024,
+                scaling=RopeScaling.yarn(64, 4096, 150000.0, 32.0), freq_base=150000.0, dims=GPT_OSS,
+                x_scale=0.03)
+    label = f"gpt-oss {'SWA-128 ring' if n_swa else 'full'}"
+    blk.step(ctx, 1024, 31, f"{label}, 1024-token chunk")
+    blk.step(ctx, 1, 33, f"{label}, decode step")
+
+
 def test_chunk_equals_token_by_token(ctx):
     # the chunked call against the reference's shape of work, one token per call, both on the GPU
     a, b = Block(ctx, (8, 8, 8, 8), 0xB30C, sinks=False), Block(ctx, (8, 8, 8, 8), 0xB30C, sinks=False)
