@@ -590,6 +590,72 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // activations and pair b + 1's weights (NAI + 3). Past the end, the requests repeat the last
     // block and pair into the buffers next in line, which nothing reads, so every step issues the
     // same copies.
+    if constexpr (WIDE && TY == 1) {
+        // Register pipeline (F16, wide): step b reads block b + 1's operands from LDS into registers
+        // while block b's MFMAs run on the operands read one step earlier, and requests block b + 3
+        // into the buffer block b has left. (In the wide form the two waves of a SIMD belong to one
+        // work-group and meet at every barrier, so neither covers the other's wait for its reads.)
+        constexpr uint32_t PER = NAI + 2u;  // copies per step
+        struct Ops {
+            half8_t ah[2][2], al[2][2], bw[2][2];
+        };
+        auto rd = [&](uint32_t buf) {
+            Ops o;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const uint32_t off = aoff[tt][s] + buf * BUF;
+                    o.ah[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off));
+                    o.al[tt][s] = __builtin_bit_cast(half8_t, mm2_lds16(off + MM2_HALF));
+                }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) o.bw[rt][s] = __builtin_bit_cast(half8_t, mm2_lds16(woff[rt][s] + buf * BUF));
+            return o;
+        };
+        auto mm = [&](const Ops &o) {
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.ah[tt][s], o.bw[rt][s], acc[tt][rt], 0, 0, 0);
+                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.al[tt][s], o.bw[rt][s], acc[tt][rt], 0, 0, 0);
+                    }
+        };
+        // blocks 0, 1, 2 requested; block 0's have landed everywhere
+        copy(0u, 0u);
+        copy(min(1u, nb - 1u), 1u);
+        copy(min(2u, nb - 1u), 2u);
+        __builtin_amdgcn_s_waitcnt(mm2_vmcnt(2u * PER));
+        __builtin_amdgcn_s_barrier();
+        Ops cur = rd(0u);
+        // step b (buffer of block b: i = b % 3): block b + 1's copies have landed and every LDS read
+        // of block b has returned, in this wave, then in every wave
+        auto pstep = [&](uint32_t b, uint32_t i) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(PER));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            const Ops nxt = rd((i + 1u) % 3u);
+            copy(min(b + 3u, nb - 1u), i);
+            __builtin_amdgcn_sched_barrier(0);
+            mm(cur);
+            cur = nxt;
+        };
+        uint32_t b = 0;
+        for (; b + 3u <= nb; b += 3u) {
+            pstep(b, 0u);
+            pstep(b + 1u, 1u);
+            pstep(b + 2u, 2u);
+        }
+        if (b < nb) pstep(b, 0u);
+        if (b + 1u < nb) pstep(b + 1u, 1u);
+        __builtin_amdgcn_s_waitcnt(mm2_vmcnt(0));  // no copy outlives the work-group
+    } else {
     copy(0, 0);
     if constexpr (Q8) qcopy(0, 0);
     if constexpr (Q4K) kcopy(0, 0, 0);
@@ -641,6 +707,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     if (b + 3u < nb) step(b + 3u, 0, 1, true);
     if (b + 4u < nb) step(b + 4u, 1, 2, false);
     __builtin_amdgcn_s_waitcnt(mm2_vmcnt(0));  // no copy outlives the work-group
+    }
 
     // D[token][row]: lane l holds row r0 + 64 (w >> 1) + 32 rt + n, tokens 8 (j / 4) + 4 h + j % 4 of
     // tile tt -- 32 consecutive rows per store instruction
