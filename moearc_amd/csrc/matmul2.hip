@@ -13,7 +13,7 @@
 // feeds k 16h + 8s .. + 7 to the MFMA of k slice s, for both operands.
 //
 // Work-group: 4 waves over 128 tokens x 128 weight rows; wave w takes tokens 64 (w & 1) .. + 63 and
-// rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. F16 and Q8_0 also come as a wide form, 8
+// rows 64 (w >> 1) .. + 63 as 2 x 2 tiles of 32 x 32. F16, Q8_0 and MXFP4 also come as a wide form, 8
 // waves over 128 tokens x 256 rows, one work-group per CU: the same waves' steps, with each
 // k-block's copies shared by twice the rows (the CU's intake of copied bytes costs time beside
 // the MFMAs, whatever the copies' destination). Both operands reach LDS by LDS DMA
@@ -39,7 +39,7 @@
 namespace {
 
 constexpr uint32_t MM2_TOK = 128;   // tokens per work-group
-constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group (the wide F16 / Q8_0 form: 256)
+constexpr uint32_t MM2_ROWS = 128;  // weight rows per work-group (the wide form: 256)
 constexpr uint32_t MM2_HALF = MM2_TOK * 64u;    // bytes of one half (hi or lo) of an activation tile
 constexpr uint32_t MM2_ACT = 2u * MM2_HALF;     // one k-block's activation tile
 constexpr uint32_t MM2_NBUF = 3u;
@@ -52,17 +52,14 @@ constexpr uint32_t MM2_NBUF = 3u;
 // are the pair's first sub-block, the high ones its second; three buffers) and each super-block's
 // header per row (d, dmin, the 12 scale bytes; Q5_K: and the 32 bytes of fifth bits; two buffers)
 constexpr uint32_t MM2_KXS = MM2_TOK * 4u;
-constexpr uint32_t MM2_KPAIR = MM2_ROWS * 32u;
-__host__ __device__ constexpr uint32_t mm2_khdr(uint32_t ty) { return MM2_ROWS * (ty == 13 ? 48u : 16u); }
+// (The per-row buffers' sizes follow the tile's row count: mm2_body's KPAIR_B, KHDR_B, QUAD6_B,
+// HDR6_B and XPAIR_B.)
 // Q6_K (per work-group, after the activation buffers): each half super-block's (four k-blocks')
 // 64 bytes of ql and 32 of qh per row (two buffers), and each super-block's 16 scale bytes per row
 // followed by a dword per row ending on d (bytes 206 .. 209; two buffers)
-constexpr uint32_t MM2_6QUAD = MM2_ROWS * 96u;
-constexpr uint32_t MM2_6HDR = MM2_ROWS * 20u;
 // MXFP4 (per work-group, after the activation buffers): each pair of 17-byte blocks' 34 bytes per
 // row, as two 16-byte chunks (bytes 0 .. 31) and a 4-byte tail (bytes 30 .. 33, which ends on the
 // pair's last byte, so no copy reads past a row); three buffers
-constexpr uint32_t MM2_XPAIR = MM2_ROWS * 36u;
 
 typedef float mm2_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t mm2_u32x2 __attribute__((ext_vector_type(2)));
@@ -158,22 +155,28 @@ template <uint32_t TY, bool WIDE = false>
 __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13, Q6K = TY == 14, MX = TY == 39;
     constexpr uint32_t KSB = Q5K ? 176u : 144u, KQS = Q5K ? 48u : 16u;  // super-block bytes, qs offset
-    constexpr uint32_t MM2_KHDR = mm2_khdr(TY);
-    // WIDE (F16, Q8_0): eight waves over 128 tokens x 256 rows, one work-group per CU; the
-    // per-wave tiles and steps are the same, each k-block's copies are shared by twice the rows
-    static_assert(!WIDE || TY == 1 || TY == 8, "wide tiles: F16 and Q8_0");
+    // WIDE: eight waves over 128 tokens x 256 rows, one work-group per CU; the per-wave tiles and
+    // steps are the same, each k-block's copies are shared by twice the rows. The K-quants build it
+    // too but measured no gain (Q4_K, Q5_K within noise, Q6_K 6% slower): the two waves of a SIMD
+    // then belong to one work-group and meet at every barrier, and in their VALU-heavy steps they
+    // contend where two work-groups' waves would interleave.
+    static_assert(!WIDE || TY == 1 || TY == 8 || TY == 39, "wide tiles: F16, Q8_0 and MXFP4");
     constexpr uint32_t NW = WIDE ? 8u : 4u;                 // waves
     constexpr uint32_t ROWS = WIDE ? 2u * MM2_ROWS : MM2_ROWS;  // weight rows per work-group
+    constexpr uint32_t RQ = ROWS / 64u;                     // 64-row quarters: per-row copies by waves w % RQ
     constexpr uint32_t NAI = 16u / NW;                      // activation copies per wave and step
     constexpr uint32_t QTAIL = ROWS * 64u, QPAIR = QTAIL + NW * 256u;
+    // the per-row weight buffers at this tile's row count
+    constexpr uint32_t KPAIR_B = ROWS * 32u, KHDR_B = ROWS * (Q5K ? 48u : 16u);
+    constexpr uint32_t QUAD6_B = ROWS * 96u, HDR6_B = ROWS * 20u, XPAIR_B = ROWS * 36u;
     // LDS: per buffer a k-block's activation tile and (F16) its weight tile; then (Q8_0) the pair
     // buffers, (Q4_K) the block sums, pair and header buffers
     constexpr uint32_t BUF = MM2_ACT + (TY == 1 ? ROWS * 64u : 0u);
     constexpr uint32_t QBASE = MM2_NBUF * BUF;
-    constexpr uint32_t KXS = QBASE, KPAIR = KXS + MM2_NBUF * MM2_KXS, KHDR = KPAIR + MM2_NBUF * MM2_KPAIR;
-    constexpr uint32_t K6Q = QBASE, K6H = K6Q + 2u * MM2_6QUAD;
-    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * QPAIR : Q4K ? KHDR - QBASE + 2u * MM2_KHDR
-                             : Q6K ? 2u * MM2_6QUAD + 2u * MM2_6HDR : MX ? MM2_NBUF * MM2_XPAIR : 0u;
+    constexpr uint32_t KXS = QBASE, KPAIR = KXS + MM2_NBUF * MM2_KXS, KHDR = KPAIR + MM2_NBUF * KPAIR_B;
+    constexpr uint32_t K6Q = QBASE, K6H = K6Q + 2u * QUAD6_B;
+    constexpr uint32_t EXTRA = Q8 ? MM2_NBUF * QPAIR : Q4K ? KHDR - QBASE + 2u * KHDR_B
+                             : Q6K ? 2u * QUAD6_B + 2u * HDR6_B : MX ? MM2_NBUF * XPAIR_B : 0u;
     __shared__ __attribute__((aligned(1024))) uint8_t tiles[QBASE + EXTRA];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -229,35 +232,36 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // Q4_K: per k-block b (into buffers buf, qb and the header buffer of b's super-block) the block
     // sums of the tile's tokens, b's pair of sub-blocks, b's super-block header -- three copies for
     // every block, whichever of them repeat the previous block's bytes, so each step issues the
-    // same count. Waves 2 and 3 copy the same sums and headers as waves 0 and 1 (the same bytes to
-    // the same places). Pair slot q = 64 wave + lane holds row q / 2's 16-byte chunk
-    // (q & 1) ^ ((row >> 3) & 1) of the pair's 32 payload bytes (qs[32 g .. 32 g + 31]).
+    // same count. Waves from 2 on copy the same sums as waves 0 and 1, waves from RQ on the same
+    // headers as waves 0 .. RQ - 1 (the same bytes to the same places). Pair slot q = 64 wave + lane
+    // holds row q / 2's 16-byte chunk (q & 1) ^ ((row >> 3) & 1) of the pair's 32 payload bytes
+    // (qs[32 g .. 32 g + 31]).
     const uint32_t k_row = (64u * wave + lane) >> 1;
     const uint8_t *k_psrc = sg.w + (uint64_t) min(r0 + k_row, sg.rows - 1u) * sg.row_bytes + KQS +
                             16u * ((lane & 1u) ^ ((k_row >> 3) & 1u));
-    const uint8_t *k_hsrc = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes;
+    const uint8_t *k_hsrc = sg.w + (uint64_t) min(r0 + 64u * (wave % RQ) + lane, sg.rows - 1u) * sg.row_bytes;
     const float *k_xsrc = a.xs + (uint64_t) min(t0 + 64u * (wave & 1u) + lane, a.n_tok - 1u) * (a.cols / 32u) + kb0;
-    // Q5_K header slots q of instruction i: waves 0 and 1 fill 0 .. 255, waves 2 and 3 256 .. 383
-    // (their second instruction repeats the first); slot q is row q / 3's 16-byte chunk q % 3
+    // Q5_K header slots: instruction i of wave w fills slots 64 s .. + 63, s = min(2 w + i, 3 RQ - 1)
+    // (the last waves repeat the last 64 slots); slot q is row q / 3's 16-byte chunk q % 3
+    auto k5slot = [&](uint32_t i) { return 64u * min(2u * wave + i, 3u * RQ - 1u); };
     const uint8_t *k5hsrc[2];
 #pragma unroll
     for (uint32_t i = 0; i < 2; ++i) {
-        const uint32_t q = (wave < 2u ? 128u * wave + 64u * i : 128u + 64u * wave) + lane;
+        const uint32_t q = k5slot(i) + lane;
         k5hsrc[i] = sg.w + (uint64_t) min(r0 + q / 3u, sg.rows - 1u) * sg.row_bytes + 16u * (q % 3u);
     }
     auto kcopy = [&](uint32_t b, uint32_t buf, uint32_t qb) {
         const uint32_t kb = kb0 + b;  // super-block kb / 8, pair (kb % 8) / 2
         mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + KXS + buf * MM2_KXS + (wave & 1u) * 256u), k_xsrc + b);
-        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + KPAIR + qb * MM2_KPAIR + wave * 1024u),
+        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + KPAIR + qb * KPAIR_B + wave * 1024u),
                    k_psrc + KSB * (uint64_t) (kb >> 3) + 32u * ((kb & 7u) >> 1));
-        const uint32_t hbase = lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR;
+        const uint32_t hbase = lds0 + KHDR + ((b >> 3) & 1u) * KHDR_B;
         if constexpr (Q5K) {
 #pragma unroll
             for (uint32_t i = 0; i < 2; ++i)
-                mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + 16u * (wave < 2u ? 128u * wave + 64u * i : 128u + 64u * wave)),
-                           k5hsrc[i] + KSB * (uint64_t) (kb >> 3));
+                mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + 16u * k5slot(i)), k5hsrc[i] + KSB * (uint64_t) (kb >> 3));
         } else {
-            mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), k_hsrc + KSB * (uint64_t) (kb >> 3));
+            mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave % RQ) * 1024u), k_hsrc + KSB * (uint64_t) (kb >> 3));
         }
     };
     // Q8_0: the weights of blocks b, b + 1 (b even) into pair buffer qb
@@ -320,7 +324,7 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     uint32_t k6hstep[3];
 #pragma unroll
     for (uint32_t i = 0; i < 3; ++i) {
-        const uint32_t q = 256u * i + 64u * wave + lane, r = q / 6u, c = q % 6u;  // ql chunks 0 .. 3, qh 4, 5
+        const uint32_t q = 64u * (NW * i + wave) + lane, r = q / 6u, c = q % 6u;  // ql chunks 0 .. 3, qh 4, 5
         k6src[i] = sg.w + (uint64_t) min(r0 + r, sg.rows - 1u) * sg.row_bytes + 210u * (uint64_t) (kb0 >> 3) +
                    (c < 4u ? 16u * c : 128u + 16u * (c - 4u));
         k6hstep[i] = c < 4u ? 64u : 32u;
@@ -328,15 +332,15 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     auto k6copy = [&](uint32_t b) {
         const uint32_t kb = kb0 + b;  // super-block kb / 8, half (kb % 8) / 4
         const uint64_t sbo = 210u * (uint64_t) (b >> 3);
-        const uint32_t qbase = lds0 + K6Q + ((b >> 2) & 1u) * MM2_6QUAD;
+        const uint32_t qbase = lds0 + K6Q + ((b >> 2) & 1u) * QUAD6_B;
 #pragma unroll
         for (uint32_t i = 0; i < 3; ++i)
-            mm2_copy16(__builtin_amdgcn_readfirstlane(qbase + 16u * (256u * i + 64u * wave)),
+            mm2_copy16(__builtin_amdgcn_readfirstlane(qbase + 16u * (64u * (NW * i + wave))),
                        k6src[i] + sbo + ((kb >> 2) & 1u) * k6hstep[i]);
-        const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * MM2_6HDR;
+        const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * HDR6_B;
         const uint8_t *hrow = k_hsrc + 210u * (uint64_t) (kb >> 3);
-        mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave & 1u) * 1024u), hrow + 192u);
-        mm2_copy4(__builtin_amdgcn_readfirstlane(hbase + MM2_ROWS * 16u + (wave & 1u) * 256u), hrow + 206u);
+        mm2_copy16(__builtin_amdgcn_readfirstlane(hbase + (wave % RQ) * 1024u), hrow + 192u);
+        mm2_copy4(__builtin_amdgcn_readfirstlane(hbase + ROWS * 16u + (wave % RQ) * 256u), hrow + 206u);
     };
     // MXFP4: per k-block b the pair (b's and its partner's 34 bytes per row) into pair buffer qb --
     // every block, the odd one repeating the even one's bytes, so each step issues the same two
@@ -345,12 +349,12 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     // waves 0 and 1.
     const uint8_t *x_csrc = sg.w + (uint64_t) min(r0 + k_row, sg.rows - 1u) * sg.row_bytes + 17u * (uint64_t) kb0 +
                             16u * ((lane & 1u) ^ ((k_row >> 3) & 1u));
-    const uint8_t *x_tsrc = sg.w + (uint64_t) min(r0 + 64u * (wave & 1u) + lane, sg.rows - 1u) * sg.row_bytes +
+    const uint8_t *x_tsrc = sg.w + (uint64_t) min(r0 + 64u * (wave % RQ) + lane, sg.rows - 1u) * sg.row_bytes +
                             17u * (uint64_t) kb0 + 30u;
     auto xcopy = [&](uint32_t b, uint32_t qb) {
         const uint64_t po = 34u * (uint64_t) (b >> 1);
-        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + QBASE + qb * MM2_XPAIR + wave * 1024u), x_csrc + po);
-        mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + QBASE + qb * MM2_XPAIR + MM2_ROWS * 32u + (wave & 1u) * 256u),
+        mm2_copy16(__builtin_amdgcn_readfirstlane(lds0 + QBASE + qb * XPAIR_B + wave * 1024u), x_csrc + po);
+        mm2_copy4(__builtin_amdgcn_readfirstlane(lds0 + QBASE + qb * XPAIR_B + ROWS * 32u + (wave % RQ) * 256u),
                   x_tsrc + po);
     };
     // block b from activation buffer buf and (Q8_0, Q4_K) pair buffer qb, b odd: the pair's second block
@@ -372,11 +376,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
                 const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
-                const uint32_t prow = lds0 + QBASE + qb * MM2_XPAIR;
+                const uint32_t prow = lds0 + QBASE + qb * XPAIR_B;
                 const uint32_t sw = (rl >> 3) & 1u;
                 const u32x4_t c0 = mm2_lds16(prow + 32u * rl + 16u * sw);          // bytes 0 .. 15
                 const u32x4_t c1 = mm2_lds16(prow + 32u * rl + 16u * (1u ^ sw));   // bytes 16 .. 31
-                const uint32_t tl = mm2_lds4(prow + MM2_ROWS * 32u + 4u * rl);     // bytes 30 .. 33
+                const uint32_t tl = mm2_lds4(prow + ROWS * 32u + 4u * rl);     // bytes 30 .. 33
                 uint32_t dw[4], e;
                 if (!odd) {  // data bytes 1 .. 16
                     dw[0] = __builtin_amdgcn_alignbyte(c0[1], c0[0], 1u);
@@ -436,12 +440,12 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
                 const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
-                const uint32_t qrow = lds0 + K6Q + ((b >> 2) & 1u) * MM2_6QUAD + 96u * rl;
-                const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * MM2_6HDR;
+                const uint32_t qrow = lds0 + K6Q + ((b >> 2) & 1u) * QUAD6_B + 96u * rl;
+                const uint32_t hbase = lds0 + K6H + ((b >> 3) & 1u) * HDR6_B;
                 const uint32_t scw = *(const __attribute__((address_space(3))) uint32_t *) (uintptr_t) (
                     hbase + 16u * rl + 4u * (2u * hf + (c >> 1)));  // scales[8 hf + 2c], + 1
                 const uint32_t dw = *(const __attribute__((address_space(3))) uint32_t *) (uintptr_t) (
-                    hbase + MM2_ROWS * 16u + 4u * rl);
+                    hbase + ROWS * 16u + 4u * rl);
                 const float d = (float) __builtin_bit_cast(_Float16, (uint16_t) (dw >> 16));
                 const uint32_t sco = 16u * (c & 1u);
 #pragma unroll
@@ -481,8 +485,8 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
                 const uint32_t rl = 64u * (wave >> 1) + 32u * rt + n;
-                const u32x4_t kq = mm2_lds16(lds0 + KPAIR + qb * MM2_KPAIR + 32u * rl + 16u * (h ^ ((rl >> 3) & 1u)));
-                const uint32_t hrow = lds0 + KHDR + ((b >> 3) & 1u) * MM2_KHDR + (Q5K ? 48u : 16u) * rl;
+                const u32x4_t kq = mm2_lds16(lds0 + KPAIR + qb * KPAIR_B + 32u * rl + 16u * (h ^ ((rl >> 3) & 1u)));
+                const uint32_t hrow = lds0 + KHDR + ((b >> 3) & 1u) * KHDR_B + (Q5K ? 48u : 16u) * rl;
                 const u32x4_t hd = mm2_lds16(hrow);
                 // get_scale_min_k4 (reference.rs:150-160) over the 12 scale bytes hd.y .. hd.w
                 // (a mask, not a branch or a select: those split the step and its registers spill)
@@ -670,11 +674,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
         // then in every wave
         __builtin_amdgcn_sched_barrier(0);
         if (Q6K)
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(9u));
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI + 5u));  // NAI + 3 quads + header 2
         else if (Q5K)
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(8u));
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI + 4u));  // NAI + sums + pair + header 2
         else if (Q4K)
-            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(7u));
+            __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI + 3u));  // NAI + sums + pair + header
         else if (!Q8)
             __builtin_amdgcn_s_waitcnt(mm2_vmcnt_lgkm0(NAI + 2u));  // F16: NAI + 2 copies; MXFP4: 4 + 2
         else if (odd)
@@ -747,6 +751,7 @@ extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_q8_0_k(MatmulAr
 extern "C" __global__ void __launch_bounds__(256) moearc_matmul2_f16_k(MatmulArgs a) { mm2_body<1>(a); }
 extern "C" __global__ void __launch_bounds__(512) moearc_matmul2w_q8_0_k(MatmulArgs a) { mm2_body<8, true>(a); }
 extern "C" __global__ void __launch_bounds__(512) moearc_matmul2w_f16_k(MatmulArgs a) { mm2_body<1, true>(a); }
+extern "C" __global__ void __launch_bounds__(512) moearc_matmul2w_mxfp4_k(MatmulArgs a) { mm2_body<39, true>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moearc_matmul2_q4_k_k(MatmulArgs a) { mm2_body<12>(a); }
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))

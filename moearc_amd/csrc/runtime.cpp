@@ -90,7 +90,7 @@ struct moearc_ctx {
     hipFunction_t f_add = nullptr, f_read_floor = nullptr, f_mfma_floor = nullptr;
     hipFunction_t f_mm[6][2] = {}, f_split = nullptr, f_split8 = nullptr, f_bsums = nullptr;  // Q8_0 F16 Q4_K Q5_K MXFP4 Q6_K x 16 / 32 rows per wave
     hipFunction_t f_mm2[6] = {};  // Q8_0, F16, Q4_K, Q5_K, Q6_K, MXFP4: 128 x 128 tiles on the 32x32x16 MFMA
-    hipFunction_t f_mm2w[2] = {};  // Q8_0, F16: 128 tokens x 256 rows, eight waves
+    hipFunction_t f_mm2w[3] = {};  // Q8_0, F16, MXFP4 on 128 tokens x 256 rows, eight waves
     uint16_t *mm_ws = nullptr;  // f16 hi / lo split of a chunk's activations
     size_t mm_ws_halves = 0;
     float *mm_part = nullptr;   // the k-slices' sums of split chunk products
@@ -626,6 +626,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_mm2[5], "moearc_matmul2_mxfp4_k"},
         {&c->f_mm2w[0], "moearc_matmul2w_q8_0_k"},
         {&c->f_mm2w[1], "moearc_matmul2w_f16_k"},
+        {&c->f_mm2w[2], "moearc_matmul2w_mxfp4_k"},
         {&c->f_bsums, "moearc_block_sums_k"},
         {&c->f_split, "moearc_split_f16_k"},
         {&c->f_split8, "moearc_split_f16_v8_k"},
@@ -1438,20 +1439,22 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     const bool pairs = ty == 8u || ty == 39u;
     const bool mm2 = (ty == 1u || ty == 12u || ty == 13u || ty == 14u || (pairs && (n_cols / 32) % 2 == 0)) &&
                      n_tok >= 64;
-    // F16 and Q8_0 take work-groups of eight waves over 128 tokens x 256 rows (one per CU) when
-    // those tiles alone cover every CU: each k-block's copies into LDS then serve twice the rows,
-    // and the copies' volume is what the CU pays for beside the MFMAs (at gpt-oss's attn_q over 2048
-    // tokens F16 -20%, Q8_0 -4%; with fewer tiles than CUs the 128 x 128 form is faster).
-    const bool wide = mm2 && (ty == 1u || ty == 8u) &&
+    // F16, Q8_0 and MXFP4 take work-groups of eight waves over 128 tokens x 256 rows (one per CU)
+    // when those tiles alone cover every CU: each k-block's copies into LDS then serve twice the
+    // rows, and the copies' volume is what the CU pays for beside the MFMAs (at gpt-oss's attn_q
+    // over 2048 tokens F16 -20%, Q8_0 -4%, MXFP4 -6%; with fewer tiles than CUs, and for the
+    // K-quants, the 128 x 128 form is as fast or faster).
+    const bool wide = mm2 && (ty == 1u || ty == 8u || ty == 39u) &&
                       (c->mm_wide > 0 || (c->mm_wide < 0 && tiles256 * ((n_tok + 127) / 128) >= kMmCUs));
     unsigned threads = 256;
+    const int mm2_i = ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 14u ? 4 : 5;
     if (wide) {
-        f = c->f_mm2w[ty == 8u ? 0 : 1];
+        f = c->f_mm2w[ty == 8u ? 0 : ty == 1u ? 1 : 2];
         rows_per_tile = 256;
         threads = 512;
         gy = (unsigned) ((n_tok + 127) / 128);
     } else if (mm2) {
-        f = c->f_mm2[ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 14u ? 4 : 5];
+        f = c->f_mm2[mm2_i];
         rows_per_tile = 128;
         gy = (unsigned) ((n_tok + 127) / 128);
     } else {

@@ -291,12 +291,15 @@ def _within_bound(label, got, ty, w, x, bias, rows, cols, tokens):
 
 
 @pytest.mark.parametrize("ty,n_tok,rows,cols", [
-    # F16 and Q8_0 on eight-wave work-groups of 128 tokens x 256 rows: ragged row and token tiles,
+    # F16, Q8_0 and MXFP4 on eight-wave work-groups of 128 tokens x 256 rows: ragged row and token tiles,
     # k-block counts around the three-deep pipeline and its six-block unroll, a 128-token chunk's
     # output projection at gpt-oss shapes
     (QuantType.Q8_0, 200, 300, 64), (QuantType.Q8_0, 130, 513, 320), (QuantType.Q8_0, 64, 256, 448),
     (QuantType.Q8_0, 100, 260, 192), (QuantType.F16, 100, 257, 32), (QuantType.F16, 190, 600, 160),
-    (QuantType.F16, 65, 136, 352), (QuantType.Q8_0, 128, 2880, 4096)], ids=str)
+    (QuantType.F16, 65, 136, 352), (QuantType.Q8_0, 128, 2880, 4096),
+    # MXFP4 pairs of 17-byte blocks
+    (QuantType.MXFP4, 200, 300, 192), (QuantType.MXFP4, 130, 513, 2880), (QuantType.MXFP4, 64, 260, 64)],
+    ids=str)
 def test_chunk_matmul_wide_tiles(ty, n_tok, rows, cols):
     # forced on (MOEARC_MM_WIDE=1) against forced off: without split-K both accumulate every output
     # in the same k order, so they must agree bit for bit; with the split-K the wide form's launch
