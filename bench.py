@@ -560,6 +560,7 @@ MM_CASES = [
     ("attn_q Q8_0 2048 tokens x 4096 x 2880", 8, 2048, 4096, 2880),
     ("attn.proj Q8_0 2048 tokens x 2880 x 4096", 8, 2048, 2880, 4096),
     ("attn_q F16 2048 tokens x 4096 x 2880", 1, 2048, 4096, 2880),
+    ("attn_q MXFP4 2048 tokens x 4096 x 2880", 39, 2048, 4096, 2880),
     # Qwen3-30B-A3B's attn_q (Q4_K in its Q4_K_M files) over a chunk of the same length
     ("attn_q Q4_K qwen3-30b 2048 tokens x 4096 x 2048", 12, 2048, 4096, 2048),
 ]
