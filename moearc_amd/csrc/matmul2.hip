@@ -156,10 +156,11 @@ __device__ __forceinline__ void mm2_body(const MatmulArgs &a) {
     constexpr bool Q8 = TY == 8, Q4K = TY == 12 || TY == 13, Q5K = TY == 13, Q6K = TY == 14, MX = TY == 39;
     constexpr uint32_t KSB = Q5K ? 176u : 144u, KQS = Q5K ? 48u : 16u;  // super-block bytes, qs offset
     // WIDE: eight waves over 128 tokens x 256 rows, one work-group per CU; the per-wave tiles and
-    // steps are the same, each k-block's copies are shared by twice the rows. The K-quants build it
-    // too but measured no gain (Q4_K, Q5_K within noise, Q6_K 6% slower): the two waves of a SIMD
-    // then belong to one work-group and meet at every barrier, and in their VALU-heavy steps they
-    // contend where two work-groups' waves would interleave.
+    // steps are the same, each k-block's copies are shared by twice the rows. The K-quants, built
+    // this way (their per-row buffers and header copies below follow ROWS and RQ), measured no gain
+    // (Q4_K, Q5_K within noise, Q6_K 6% slower): the two waves of a SIMD then belong to one
+    // work-group and meet at every barrier, and in their VALU-heavy steps they contend where two
+    // work-groups' waves would interleave.
     static_assert(!WIDE || TY == 1 || TY == 8 || TY == 39, "wide tiles: F16, Q8_0 and MXFP4");
     constexpr uint32_t NW = WIDE ? 8u : 4u;                 // waves
     constexpr uint32_t ROWS = WIDE ? 2u * MM2_ROWS : MM2_ROWS;  // weight rows per work-group
