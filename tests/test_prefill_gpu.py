@@ -189,6 +189,21 @@ def test_config4_full_size_spikes(ctx, n_swa):
     _report(f"config 4 spikes n_swa={n_swa} (all 2048 rows)", got, want)
 
 
+@pytest.mark.parametrize("n_swa", [0, 128])
+@pytest.mark.parametrize("n_q,pos0", [(2048, 1001), (2000, 1001)])
+def test_full_size_unaligned_chunks(ctx, n_q, pos0, n_swa):
+    """Config-4 sized chunks starting off a 32-key boundary: 2048 rows (512 work-groups, so the
+    pair balance runs, with every tile's key range ragged) and 2000 rows (a last tile of 16 tokens);
+    every output against the oracle."""
+    pc = fx.prefill_case(0xC46 + n_q, n_q=n_q, pos0=pos0, pt=256)
+    want = oracle.attn_prefill(pc.qp.astype(np.float32), pc.k_raw, pc.v_raw, pc.bt, pc.n_q, pc.pos0,
+                               n_swa, pc.H, pc.G, pc.D, pc.pt, float(pc.scale), sinks=pc.sinks,
+                               n_threads=16)
+    got = _run(ctx, pc, n_swa, out_type=OUT_F16)
+    assert np.isfinite(got).all()
+    _report(f"prefill n_q={n_q} pos0={pos0} n_swa={n_swa} (all rows)", got, want)
+
+
 def test_refusals(ctx):
     buf, bt = ctx.alloc(1 << 16), ctx.alloc(64)
     with pytest.raises(BadArgument):  # head_dim 128 is not the prefill kernel's
