@@ -262,6 +262,27 @@ def test_config2_depth_32k_against_oracle(ctx):
     _report("split-K decode 32K", got, want, TOL_NS)
 
 
+@pytest.mark.parametrize("n_kv,kv_begin", [(20000, 0), (20000, 19872)], ids=["full", "swa128"])
+def test_f32_kv_long_context_against_oracle(ctx, n_kv, kv_begin):
+    # an f32 KV cache (the reference's other KvType, reference.rs:728-752) at a long context, both
+    # a full span and a 128-key window, through a random page permutation: the general kernel
+    c = fx.north_star_case(0xF32, n_kv, pt=256)
+    row = c.G * c.D
+    kvals = np.zeros((c.k_raw.shape[0], row), np.float32)
+    vvals = np.zeros_like(kvals)
+    live = c.bt[np.arange(n_kv) // c.pt].astype(np.int64) * c.pt + np.arange(n_kv) % c.pt
+    kvals[live] = fx.synth.normal(0xF33, n_kv * row).reshape(n_kv, row)
+    vvals[live] = fx.synth.normal(0xF34, n_kv * row).reshape(n_kv, row)
+    dk, dv, dq = ctx.upload(kvals), ctx.upload(vvals), ctx.upload(c.q.astype(np.float32))
+    dbt, ds, out = ctx.upload(np.asarray(c.bt, np.uint32)), ctx.upload(c.sinks), ctx.alloc(c.H * c.D * 4)
+    ctx.attn_decode_ext(out, dq, dk, dv, dbt, ds, c.H, c.G, c.D, kv_begin, n_kv, c.pt, float(c.scale),
+                        KvType.F32)
+    got = ctx.download(out, np.float32, c.H * c.D)
+    want = oracle.attn_decode(c.q, kvals, vvals, c.bt, c.H, c.G, c.D, kv_begin, n_kv, c.pt,
+                              float(c.scale), kv_type=0, sinks=c.sinks)
+    _report(f"f32 KV decode n_kv={n_kv} begin={kv_begin}", got, want, TOL_NS)
+
+
 def test_single_key_closed_form_with_sink(ctx):
     # one key: out = V * sigmoid(s - sink)
     c = fx.north_star_case(77, 1, pt=32)
