@@ -141,6 +141,33 @@ def test_fused_append_equals_rope_then_append(ctx, pt, kv, G):
         assert np.all(err <= tol)
 
 
+def test_fused_append_config4_chunk(ctx):
+    # a config-4 chunk's keys and values (2048 tokens at positions 1000 .. 3047, 8 KV heads,
+    # 256-token pages through a random permutation) against the oracle's rope-then-append
+    n_tok, D, G, pt = 2048, 64, 8, 256
+    k, v, pos, pages, slots, n_pages = _chunk(n_tok, G, D, pt, 0x4C4)
+    nbytes = n_pages * pt * G * D * 2
+    kp, vp = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    ctx.zero(kp, nbytes // 4)
+    ctx.zero(vp, nbytes // 4)
+    sc = _yarn()
+    ctx.rope_kv_append_chunk(kp, vp, ctx.upload(k), ctx.upload(v), ctx.upload(pos), ctx.upload(pages),
+                             ctx.upload(slots), n_tok, G, D, pt, D, GPT["freq_base"], scaling=sc,
+                             kind=RopeKind.NEOX, kv=KvType.F16)
+    gk, gv = ctx.download(kp, np.uint16, nbytes // 2), ctx.download(vp, np.uint16, nbytes // 2)
+    ok = np.zeros(nbytes // 2, np.uint16)
+    ov = np.zeros_like(ok)
+    oracle.rope_kv_append_chunk(ok, ov, k, v, pos, pages, slots, n_tok, G, D, pt, D, GPT["freq_base"],
+                                sc.args(), True, 1)
+    assert np.array_equal(gv, ov), "V must be stored exactly"
+    wk = oracle.f16_to_f32(ok)
+    # angles up to ~3050 rad: f32 angle error ~16 ulp of the angle times |k|, plus one f16 ulp
+    tol = 16.0 * 3050.0 * 2 * U * 5.0 * 1.35 + np.abs(wk) * 2.0 ** -10 + 1e-7
+    err = np.abs(oracle.f16_to_f32(gk).astype(np.float64) - wk)
+    print(f"fused append, config-4 chunk: max |gpu - oracle| = {err.max():.3e}", flush=True)
+    assert np.all(err <= tol)
+
+
 def test_refusals(ctx):
     src, pos = fx.rope_reference_inputs()
     dsrc, dpos, ddst = ctx.upload(src), ctx.upload(pos), ctx.alloc(src.nbytes)
