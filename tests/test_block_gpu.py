@@ -224,6 +224,39 @@ def test_fused_launches_equal_separate_ones(monkeypatch, dims):
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
 
 
+def test_wide_tile_products_in_the_block(monkeypatch):
+    # The block's q/k/v product is one launch over three matrices (segments of row tiles); with
+    # MOEARC_MM_WIDE=1 it and the output projection run on the eight-wave 128 x 256 tiles (as a
+    # 2048-token chunk's q/k/v product does by default). Without split-K the block's outputs and
+    # pools equal the 128 x 128 tiles' to the bit; with it, the oracle's bar.
+    from moearc_amd import Context
+    monkeypatch.setenv("MOEARC_MM_SPLIT_WG", "0")
+    got = {}
+    for wide in ("1", "0"):
+        monkeypatch.setenv("MOEARC_MM_WIDE", wide)
+        with Context() as cx:
+            blk = Block(cx, (8, 8, 8, 8), 0xB80C, n_ctx=512, chunk=160, dims=GPT_OSS, x_scale=0.03,
+                        scaling=RopeScaling.yarn(64, 4096, 150000.0, 32.0), freq_base=150000.0)
+            outs = []
+            for n, seed in ((160, 41), (97, 43), (1, 45)):
+                x = (fx.synth.normal(seed, n * blk.E) * blk.x_scale).astype(np.float32).reshape(n, blk.E)
+                h = fx.synth.normal(seed + 1, n * blk.E).astype(np.float32).reshape(n, blk.E)
+                pages, slots, table = blk.places(n)
+                outs.append(blk.gpu_chunk(cx, h, x, pages, slots, table))
+                blk.n += n
+            outs.append(cx.download(blk.d_kp, np.uint16, blk.kp.shape))
+        got[wide] = outs
+    for name, a, b in zip(("chunk 1", "chunk 2", "decode step", "K pool"), got["1"], got["0"]):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"wide tiles changed the block's {name}"
+    monkeypatch.delenv("MOEARC_MM_SPLIT_WG")
+    monkeypatch.setenv("MOEARC_MM_WIDE", "1")
+    with Context() as cx:
+        blk = Block(cx, (8, 8, 8, 8), 0xB90C, n_ctx=512, chunk=160, dims=GPT_OSS, x_scale=0.03,
+                    scaling=RopeScaling.yarn(64, 4096, 150000.0, 32.0), freq_base=150000.0)
+        blk.step(cx, 160, 51, "gpt-oss full, wide tiles with split-K, chunk 1")
+        blk.step(cx, 1, 53, "gpt-oss full, wide tiles with split-K, decode step")
+
+
 def test_refusals(ctx):
     blk = Block(ctx, (8, 8, 8, 8), 0xB40C)
     d = blk.desc(ctx, ctx.upload(np.arange(4, dtype=np.uint32)))
