@@ -1440,12 +1440,16 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     const bool mm2 = (ty == 1u || ty == 12u || ty == 13u || ty == 14u || (pairs && (n_cols / 32) % 2 == 0)) &&
                      n_tok >= 64;
     // F16, Q8_0 and MXFP4 take work-groups of eight waves over 128 tokens x 256 rows (one per CU)
-    // when those tiles alone cover every CU: each k-block's copies into LDS then serve twice the
-    // rows, and the copies' volume is what the CU pays for beside the MFMAs (at gpt-oss's attn_q
-    // over 2048 tokens F16 -20%, Q8_0 -4%, MXFP4 -6%; with fewer tiles than CUs, and for the
-    // K-quants, the 128 x 128 form is as fast or faster).
+    // when those tiles alone cover every CU in whole rounds, the last at least three quarters
+    // full: each k-block's copies into LDS then serve twice the rows, and the copies' volume is
+    // what the CU pays for beside the MFMAs (at gpt-oss's attn_q over 2048 tokens, 256 tiles: F16
+    // -20%, Q8_0 -4%, MXFP4 -6%). With fewer tiles than CUs, for the K-quants, and for a last
+    // round mostly empty (the 2048-token block's q/k/v product, 320 tiles: +7% per block, its 64
+    // last work-groups each alone on a CU for a whole wide tile) the 128 x 128 form is faster.
+    const uint64_t wt = tiles256 * ((n_tok + 127) / 128);
     const bool wide = mm2 && (ty == 1u || ty == 8u || ty == 39u) &&
-                      (c->mm_wide > 0 || (c->mm_wide < 0 && tiles256 * ((n_tok + 127) / 128) >= kMmCUs));
+                      (c->mm_wide > 0 ||
+                       (c->mm_wide < 0 && wt >= kMmCUs && (wt % kMmCUs == 0 || wt % kMmCUs >= kMmCUs * 3 / 4)));
     unsigned threads = 256;
     const int mm2_i = ty == 8u ? 0 : ty == 1u ? 1 : ty == 12u ? 2 : ty == 13u ? 3 : ty == 14u ? 4 : 5;
     if (wide) {
