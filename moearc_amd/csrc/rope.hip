@@ -197,16 +197,37 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
 // them once per 4 heads). Each lane stores 8 bytes of K and of V -- a row is one 128-byte line --
 // written through to the device-coherent level. Same results as moearc_rope_kv_append_chunk_k.
 //
+// p[0 .. 3] summed over n >= 1 slices `stride` floats apart, in slice order, then + bias[0 .. 3]
+// when given: per element the additions, in the order, of moearc_matmul_reduce_k, so the values
+// equal what it stores for a chunk product's split-K sums. All loads leave before the first add.
+__device__ __forceinline__ float4_t slice_sum4(const float *p, uint64_t stride, uint32_t n, const float *bias) {
+    float4_t s = *(const float4_t *) p;
+    for (uint32_t z = 1; z < n; z += 4u) {
+        float4_t v[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) v[k] = *(const float4_t *) (p + (uint64_t) min(z + k, n - 1u) * stride);
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k)
+            if (z + k < n) s = s + v[k];
+    }
+    return bias ? s + *(const float4_t *) bias : s;
+}
+
 // Rows of 64 channels, 16 per work-group (row = (token, head) of n_heads rows per token, with
 // n_heads dividing 16 or a multiple of 16, so the work-group's rows cover T <= 16 whole or
 // partial tokens). KV: the rows are K (rotated) and V, appended at (page_ids[t], slots[t]); else
-// the rows are q, rotated into q_out (binary16 when q_f16, f32 otherwise).
-template <bool KV>
+// the rows are q, rotated into q_out (binary16 when q_f16, f32 otherwise). SUMS: x and v are slice
+// 0 of a chunk product's split-K sums (n_slices slices `stride` floats apart, [t][head * 64 + ch]
+// in each), added here with the product's bias (bx, bv: [head * 64 + ch], or null) instead of being
+// read as finished rows.
+template <bool KV, bool SUMS = false>
 __device__ __forceinline__ void rope64_rows(uint32_t b, uint32_t nh, const float *x, const float *v,
                                             void *q_out, uint32_t q_f16, uint16_t *k_pages,
                                             uint16_t *v_pages, const int *pos, const uint32_t *page_ids,
                                             const uint32_t *slots, uint64_t n_tok, uint64_t page_tokens,
-                                            const RopeParams &r, uint32_t *err, float2_t *cs_tab) {
+                                            const RopeParams &r, uint32_t *err, float2_t *cs_tab,
+                                            const float *bx = nullptr, const float *bv = nullptr,
+                                            uint64_t stride = 0, uint32_t n_slices = 1) {
     const uint32_t tid = threadIdx.x, c = tid & 15u;
     // tokens the 16 rows touch: 16 / nh whole ones, or one (32-bit divisions only)
     const bool few = nh <= 16u;
@@ -219,9 +240,15 @@ __device__ __forceinline__ void rope64_rows(uint32_t b, uint32_t nh, const float
     float4_t kx = {}, vx = {};
     uint32_t slot = 0, page = 0;
     if (live) {
-        kx = *(const float4_t *) (x + row * 64u + 4u * c);
+        if constexpr (SUMS) {
+            const uint64_t bo = (row - t * nh) * 64u + 4u * c;
+            kx = slice_sum4(x + row * 64u + 4u * c, stride, n_slices, bx ? bx + bo : nullptr);
+            if constexpr (KV) vx = slice_sum4(v + row * 64u + 4u * c, stride, n_slices, bv ? bv + bo : nullptr);
+        } else {
+            kx = *(const float4_t *) (x + row * 64u + 4u * c);
+            if constexpr (KV) vx = *(const float4_t *) (v + row * 64u + 4u * c);
+        }
         if constexpr (KV) {
-            vx = *(const float4_t *) (v + row * 64u + 4u * c);
             slot = slots[t];
             page = page_ids[t];
         }
@@ -287,4 +314,24 @@ extern "C" __global__ void __launch_bounds__(256) moearc_rope_qkv_chunk64_k(
     else
         rope64_rows<true>(blockIdx.x - nb_q, n_kv_heads, k, v, nullptr, 0u, k_pages, v_pages, pos, page_ids,
                           slots, n_tok, page_tokens, r, err, cs_tab);
+}
+
+// The same from a q/k/v chunk product's split-K sums, in place of its reduction launch: q, k and v
+// point at slice 0 of each matrix's sums (n_slices >= 2 slices, part_stride floats apart), bq, bk
+// and bv are the projections' biases (or null). Results equal moearc_matmul_reduce_k followed by
+// moearc_rope_qkv_chunk64_k.
+extern "C" __global__ void __launch_bounds__(256) moearc_rope_qkv_sums64_k(
+    void *q_out, const float *q, uint32_t n_heads, uint32_t q_f16, uint32_t nb_q,
+    uint16_t *k_pages, uint16_t *v_pages, const float *k, const float *v, const int *pos,
+    const uint32_t *page_ids, const uint32_t *slots, uint64_t n_tok, uint32_t n_kv_heads,
+    uint64_t page_tokens, RopeParams r, uint32_t *err, const float *bq, const float *bk, const float *bv,
+    uint64_t part_stride, uint32_t n_slices) {
+    __shared__ float2_t cs_tab[16 * 32];
+    if (blockIdx.x < nb_q)
+        rope64_rows<false, true>(blockIdx.x, n_heads, q, nullptr, q_out, q_f16, nullptr, nullptr, pos, nullptr,
+                                 nullptr, n_tok, 0u, r, err, cs_tab, bq, nullptr, part_stride, n_slices);
+    else
+        rope64_rows<true, true>(blockIdx.x - nb_q, n_kv_heads, k, v, nullptr, 0u, k_pages, v_pages, pos,
+                                page_ids, slots, n_tok, page_tokens, r, err, cs_tab, bk, bv, part_stride,
+                                n_slices);
 }

@@ -81,6 +81,7 @@ struct moearc_ctx {
     hipFunction_t f_zero = nullptr, f_quant = nullptr, f_append = nullptr, f_append_chunk = nullptr;
     hipFunction_t f_rope = nullptr, f_rope_f16 = nullptr, f_rope_append_chunk = nullptr, f_rope_append64 = nullptr;
     hipFunction_t f_rope_qkv64 = nullptr;  // RoPE of q and the fused K/V append in one launch
+    hipFunction_t f_rope_sums64 = nullptr;  // the same from the q/k/v product's split-K sums
     bool block_fused = true;  // MOEARC_BLOCK_FUSED=0: the attention block's fused steps as separate launches
     hipFunction_t f_dec_general = nullptr;
     hipFunction_t f_dec_fast[2] = {};  // split kernels (kDecodeVariants)
@@ -599,6 +600,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_rope_append_chunk, "moearc_rope_kv_append_chunk_k"},
         {&c->f_rope_append64, "moearc_rope_kv_append_chunk64_k"},
         {&c->f_rope_qkv64, "moearc_rope_qkv_chunk64_k"},
+        {&c->f_rope_sums64, "moearc_rope_qkv_sums64_k"},
         {&c->f_dec_general, "moearc_attn_decode_general_k"},
         {&c->f_dec_fast[0], "moearc_attn_decode_f16d64_k4w2t4"},
         {&c->f_dec_fast[1], "moearc_attn_decode_f16d64_k1w4t1"},
@@ -1409,11 +1411,22 @@ struct MmMat {
     unsigned long y_stride, rows;
 };
 
+// A split product's k-slice sums, left to a consumer that adds them itself (in slice order, then
+// the bias, as moearc_matmul_reduce_k does): matrix i's slice z at part + z * stride + off[i],
+// [t][r] with row stride `rows`. slices 0: the product was not split and wrote y itself.
+struct MmSums {
+    const float *part = nullptr;
+    uint64_t stride = 0, off[MOEARC_MM_MAX_SEG] = {};
+    uint32_t slices = 0;
+};
+
 // y = W x for n_mat matrices of one weight type over the same chunk x, given as its f16 split
-// (xh, xl) of n_tok x n_cols, in one launch (plus the split-K reduction).
+// (xh, xl) of n_tok x n_cols, in one launch (plus the split-K reduction, unless `sums` takes the
+// slices' sums instead; y is then not written).
 int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const uint16_t *xh, const uint16_t *xl,
               const float *xs, unsigned long n_tok, unsigned long n_cols, const char *what,
-              bool accumulate = false) {
+              bool accumulate = false, MmSums *sums = nullptr) {
+    if (sums) *sums = MmSums{};
     if (n_mat == 0 || n_mat > MOEARC_MM_MAX_SEG) return ERR;
     MatmulArgs a{};
     a.accumulate = accumulate ? 1u : 0u;
@@ -1527,7 +1540,12 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     }
     ++c->scope_depth;
     int rc = launch3d(c, f, gx, gy, (unsigned) slices, threads, a, what, n_rows, n_tok);
-    if (rc == OK) {
+    if (rc == OK && sums && !accumulate) {
+        sums->part = a.part;
+        sums->stride = a.part_stride;
+        for (unsigned i = 0; i < n_mat; ++i) sums->off[i] = a.seg[i].part_off;
+        sums->slices = (uint32_t) slices;
+    } else if (rc == OK) {
         const uint64_t n = a.part_stride;
         rc = launch2d(c, c->f_mm_reduce, (unsigned) std::min<uint64_t>((n + 255) / 256, 65536), 1, 256,
                       MmReduceLaunch{a, (uint32_t) slices, 0u}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
@@ -1657,6 +1675,23 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
     uint16_t *q16 = (uint16_t *) (qr + nq);
     float *att = qr + nq + (nq + 1) / 2, *proj = att + nq;
 
+    // RoPE of q (written as f16 for the prefill kernel when there is a chunk: the values
+    // moearc_quantize_f16 would make of the f32 rotation); RoPE of K fused with the K/V append.
+    // With NeoX over all 64 channels and head counts that divide 16 or are multiples of it, both
+    // go out as one launch (moearc_rope_qkv_chunk64_k), with the same results.
+    const bool chunk = n_tok > 1;
+    auto rows16 = [](unsigned long nh) { return nh != 0 && (16 % nh == 0 || nh % 16 == 0); };
+    void *qdst = chunk ? (void *) q16 : (void *) qr;
+    const bool rope_one = c->block_fused && D == 64 && b->n_rot == 64 && rows16(H) && rows16(G) &&
+                          H <= 0xFFFFFFFFul &&
+                          ((uintptr_t) q | (uintptr_t) qdst | (uintptr_t) k | (uintptr_t) v) % 16 == 0 &&
+                          ((uintptr_t) b->k_pages | (uintptr_t) b->v_pages) % 8 == 0 &&
+                          (n_tok * (H + G) + 15) / 16 < 0xFFFFFFFFull;
+    // When that launch follows a split q/k/v product of one weight type, it adds the product's
+    // k-slice sums and biases itself (moearc_rope_qkv_sums64_k) in place of the reduction launch:
+    // one launch less, the same values.
+    MmSums qkv_sums;
+
     // q, k, v (+ biases). A chunk of several tokens whose weights the MFMA product takes runs
     // as one matrix product per projection (the activation split once); the rest as every
     // (token, projection) pair through the batched matvec, grouped by weight type.
@@ -1682,7 +1717,9 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
                 done[j] = true;
                 mats[n++] = MmMat{b->w[j], b->bias[j], outs[j], rows[j], rows[j]};
             }
-            if (const int rc = mm_launch(c, b->w_type[i], mats, n, xh, xl, xs, n_tok, E, "attn_qkv_mm")) return rc;
+            if (const int rc = mm_launch(c, b->w_type[i], mats, n, xh, xl, xs, n_tok, E, "attn_qkv_mm", false,
+                                         rope_one && n == 3 ? &qkv_sums : nullptr))
+                return rc;
         }
     } else {
         float *outs[3] = {q, k, v};
@@ -1700,18 +1737,11 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
             if (const int rc = mv_launch_all(c, b->w_type[i], jobs, E, "attn_qkv_chunk")) return rc;
         }
     }
-    // RoPE of q (written as f16 for the prefill kernel when there is a chunk: the values
-    // moearc_quantize_f16 would make of the f32 rotation); RoPE of K fused with the K/V append.
-    // With NeoX over all 64 channels and head counts that divide 16 or are multiples of it, both
-    // go out as one launch (moearc_rope_qkv_chunk64_k), with the same results.
-    const bool chunk = n_tok > 1;
-    auto rows16 = [](unsigned long nh) { return nh != 0 && (16 % nh == 0 || nh % 16 == 0); };
-    void *qdst = chunk ? (void *) q16 : (void *) qr;
-    if (c->block_fused && D == 64 && b->n_rot == 64 && rows16(H) && rows16(G) && H <= 0xFFFFFFFFul &&
-        ((uintptr_t) q | (uintptr_t) qdst | (uintptr_t) k | (uintptr_t) v) % 16 == 0 &&
-        ((uintptr_t) b->k_pages | (uintptr_t) b->v_pages) % 8 == 0 && (n_tok * (H + G) + 15) / 16 < 0xFFFFFFFFull) {
+    if (rope_one) {
         const uint64_t nb_q = (n_tok * H + 15) / 16, nb_kv = (n_tok * G + 15) / 16;
-        struct {
+        const bool from_sums = qkv_sums.slices >= 2;
+        const float *const ps = qkv_sums.part;
+        struct Base {
             void *q_out;
             const float *q;
             uint32_t n_heads, q_f16, nb_q;
@@ -1724,14 +1754,31 @@ int moearc_attn_block_chunk(moearc_ctx *c, const moearc_attn_block *b, float *h,
             uint64_t pt;
             RopeParams r;
             uint32_t *err;
-        } a{qdst, q, (uint32_t) H, chunk ? 1u : 0u, (uint32_t) nb_q, b->k_pages, b->v_pages, k, v, pos,
-            page_ids, slots, n_tok, (uint32_t) G, b->page_tokens,
+        } a{qdst, from_sums ? ps + qkv_sums.off[0] : q, (uint32_t) H, chunk ? 1u : 0u, (uint32_t) nb_q,
+            b->k_pages, b->v_pages, from_sums ? ps + qkv_sums.off[1] : k, from_sums ? ps + qkv_sums.off[2] : v,
+            pos, page_ids, slots, n_tok, (uint32_t) G, b->page_tokens,
             rope_params(b->n_rot, b->freq_base, b->freq_scale, b->ext_factor, b->attn_factor, b->corr_lo,
                         b->corr_hi, 1),
             c->err_word};
+        // moearc_rope_qkv_sums64_k's parameters: the same, then the biases and the slices
+        struct Sums {
+            Base base;
+            const float *bq, *bk, *bv;
+            uint64_t part_stride;
+            uint32_t n_slices, pad;
+        };
+        static_assert(sizeof(Base) % 8 == 0 && offsetof(Sums, bq) == sizeof(Base), "rope_qkv_sums argument layout");
         c->err_armed = true;
-        if (const int rc = launch2d(c, c->f_rope_qkv64, (unsigned) (nb_q + nb_kv), 1, 256, a, "rope_qkv_chunk", H, D))
+        if (from_sums) {
+            // slice starts stay 16-byte aligned: every matrix has a multiple of 64 rows
+            if (((uintptr_t) a.q | (uintptr_t) a.k | (uintptr_t) a.v) % 16 != 0 || qkv_sums.stride % 4 != 0) return ERR;
+            const Sums as{a, b->bias[0], b->bias[1], b->bias[2], qkv_sums.stride, qkv_sums.slices, 0u};
+            if (const int rc = launch2d(c, c->f_rope_sums64, (unsigned) (nb_q + nb_kv), 1, 256, as, "rope_qkv_sums", H, D))
+                return rc;
+        } else if (const int rc = launch2d(c, c->f_rope_qkv64, (unsigned) (nb_q + nb_kv), 1, 256, a, "rope_qkv_chunk",
+                                           H, D)) {
             return rc;
+        }
     } else {
         if (const int rc = rope_launch(c, chunk ? c->f_rope_f16 : c->f_rope, qdst, q, pos, n_tok, H, D, b->n_rot,
                                        b->freq_base, b->freq_scale, b->ext_factor, b->attn_factor, b->corr_lo,

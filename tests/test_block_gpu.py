@@ -194,22 +194,26 @@ def test_chunk_equals_token_by_token(ctx):
     assert worst <= 1.0
 
 
-@pytest.mark.parametrize("dims", ["toy", "gpt_oss"])
+@pytest.mark.parametrize("dims", ["toy", "gpt_oss", "toy_no_biases"])
 def test_fused_launches_equal_separate_ones(monkeypatch, dims):
     # The block's fused steps (the default) against the launches they replace (MOEARC_BLOCK_FUSED=0):
-    # the RoPE of q and the K/V append as one launch (moearc_rope_qkv_chunk64_k), and the prefill
-    # writing the output projection's f16 hi + lo split instead of f32 rows and a split launch. The
-    # residual after a chunk and after a decode step, and both pools, bit-identical.
+    # the RoPE of q and the K/V append as one launch (moearc_rope_qkv_chunk64_k; after a split q/k/v
+    # product moearc_rope_qkv_sums64_k, which also adds the product's k-slice sums and biases in
+    # place of its reduction launch), and the prefill writing the output projection's f16 hi + lo
+    # split instead of f32 rows and a split launch. The residual after a 45-token chunk (the
+    # 16-token product), a 128-token one (the MFMA product) and a decode step, and both pools,
+    # bit-identical.
     from moearc_amd import Context
-    d = TOY if dims == "toy" else GPT_OSS
+    d = GPT_OSS if dims == "gpt_oss" else TOY
     got = {}
     for fused in ("1", "0"):
         monkeypatch.setenv("MOEARC_BLOCK_FUSED", fused)
         with Context() as cx:
-            blk = Block(cx, (8, 8, 8, 8), 0xB60C, n_ctx=256, chunk=64, dims=d, x_scale=0.03,
+            blk = Block(cx, (8, 8, 8, 8), 0xB60C, biases=dims != "toy_no_biases", n_ctx=256, chunk=128, dims=d,
+                        x_scale=0.03,
                         scaling=RopeScaling.yarn(64, 4096, 150000.0, 32.0), freq_base=150000.0)
             outs = []
-            for n, seed in ((45, 31), (1, 33)):
+            for n, seed in ((45, 31), (128, 35), (1, 33)):
                 x = (fx.synth.normal(seed, n * blk.E) * blk.x_scale).astype(np.float32).reshape(n, blk.E)
                 h = fx.synth.normal(seed + 1, n * blk.E).astype(np.float32).reshape(n, blk.E)
                 pages, slots, table = blk.places(n)
@@ -218,7 +222,7 @@ def test_fused_launches_equal_separate_ones(monkeypatch, dims):
             outs.append(cx.download(blk.d_kp, np.uint16, blk.kp.shape))
             outs.append(cx.download(blk.d_vp, np.uint16, blk.vp.shape))
         got[fused] = outs
-    for name, a, b in zip(("chunk", "decode step", "K pool", "V pool"), got["1"], got["0"]):
+    for name, a, b in zip(("chunk", "chunk of 128", "decode step", "K pool", "V pool"), got["1"], got["0"]):
         print(f"fused block launches, {dims}, {name}: {int(np.sum(a.view(np.uint8) != b.view(np.uint8)))} bytes differ",
               flush=True)
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
