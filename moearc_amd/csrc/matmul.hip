@@ -423,3 +423,38 @@ extern "C" __global__ void moearc_matmul_reduce_k(MatmulArgs a, uint32_t n_slice
         *yp = a.accumulate ? prev + v : v;
     }
 }
+
+// The same, four consecutive elements of a row per lane (every matrix's rows, y_stride and
+// part_off, the part stride and the y, bias and part addresses multiples of 4 floats, checked by
+// the host) and up to 16 slices' loads in flight before the first add: one round trip for the
+// slice counts the host picks. Per element the additions and their order are the scalar kernel's.
+extern "C" __global__ void moearc_matmul_reduce4_k(MatmulArgs a, uint32_t n_slices) {
+    const uint64_t n = a.part_stride;
+    for (uint64_t i = 4u * ((uint64_t) blockIdx.x * blockDim.x + threadIdx.x); i < n;
+         i += 4u * (uint64_t) gridDim.x * blockDim.x) {
+        const bool s1 = a.n_seg > 1u && i >= a.seg[1].part_off, s2 = a.n_seg > 2u && i >= a.seg[2].part_off;
+        auto pick = [&](auto f0, auto f1, auto f2) { return s2 ? f2 : s1 ? f1 : f0; };
+        const uint64_t part_off = pick(a.seg[0].part_off, a.seg[1].part_off, a.seg[2].part_off);
+        const uint32_t rows = pick(a.seg[0].rows, a.seg[1].rows, a.seg[2].rows);
+        const uint32_t y_stride = pick(a.seg[0].y_stride, a.seg[1].y_stride, a.seg[2].y_stride);
+        float *const y = pick(a.seg[0].y, a.seg[1].y, a.seg[2].y);
+        const float *const bias = pick(a.seg[0].bias, a.seg[1].bias, a.seg[2].bias);
+        const uint64_t e = i - part_off;
+        const uint32_t t = (uint32_t) (e / rows), r = (uint32_t) (e - (uint64_t) t * rows);
+        float4_t *yp = (float4_t *) (y + (uint64_t) t * y_stride + r);
+        const float4_t prev = a.accumulate ? *yp : float4_t{0.f, 0.f, 0.f, 0.f};
+        const float4_t bv = bias ? *(const float4_t *) (bias + r) : float4_t{0.f, 0.f, 0.f, 0.f};
+        float4_t s = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t z = 0; z < n_slices; z += 16u) {
+            float4_t v[16];
+#pragma unroll
+            for (uint32_t k = 0; k < 16u; ++k)
+                v[k] = *(const float4_t *) (a.part + (uint64_t) min(z + k, n_slices - 1u) * n + i);
+#pragma unroll
+            for (uint32_t k = 0; k < 16u; ++k)
+                s = z + k == 0u ? v[k] : z + k < n_slices ? s + v[k] : s;
+        }
+        const float4_t v = bias ? s + bv : s;
+        *yp = a.accumulate ? prev + v : v;
+    }
+}

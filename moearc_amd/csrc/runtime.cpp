@@ -97,6 +97,7 @@ struct moearc_ctx {
     float *mm_part = nullptr;   // the k-slices' sums of split chunk products
     size_t mm_part_floats = 0;
     hipFunction_t f_mm_reduce = nullptr;
+    hipFunction_t f_mm_reduce4 = nullptr;  // four elements per lane, when every address allows
     hipFunction_t f_prefill[4] = {};      // group 1, 2, 4, 8
     hipFunction_t f_prefill_precise[4] = {};  // the same with p split into f16 hi + lo
     bool prefill_precise = false;         // MOEARC_PREFILL_PRECISE=1: p split into f16 hi + lo
@@ -633,6 +634,7 @@ moearc_ctx *moearc_ctx_create(void) {
         {&c->f_split, "moearc_split_f16_k"},
         {&c->f_split8, "moearc_split_f16_v8_k"},
         {&c->f_mm_reduce, "moearc_matmul_reduce_k"},
+        {&c->f_mm_reduce4, "moearc_matmul_reduce4_k"},
     };
     for (auto &f : fns) {
         if (hipModuleGetFunction(f.slot, c->module, f.name) != hipSuccess) {
@@ -1547,8 +1549,13 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
         sums->slices = (uint32_t) slices;
     } else if (rc == OK) {
         const uint64_t n = a.part_stride;
-        rc = launch2d(c, c->f_mm_reduce, (unsigned) std::min<uint64_t>((n + 255) / 256, 65536), 1, 256,
-                      MmReduceLaunch{a, (uint32_t) slices, 0u}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
+        bool by4 = n % 4 == 0 && (uintptr_t) a.part % 16 == 0;
+        for (unsigned i = 0; i < n_mat; ++i)
+            by4 = by4 && m[i].rows % 4 == 0 && m[i].y_stride % 4 == 0 && (uintptr_t) m[i].y % 16 == 0 &&
+                  (uintptr_t) m[i].bias % 16 == 0;  // part_off: sums of n_tok * rows
+        const uint64_t lanes = by4 ? n / 4 : n;
+        rc = launch2d(c, by4 ? c->f_mm_reduce4 : c->f_mm_reduce, (unsigned) std::min<uint64_t>((lanes + 255) / 256, 65536),
+                      1, 256, MmReduceLaunch{a, (uint32_t) slices, 0u}, nullptr, n_rows, n_tok, 0, "matmul_reduce");
     }
     --c->scope_depth;
     if (call0) record_bracket(c, call0, what, n_rows, n_tok);

@@ -352,6 +352,26 @@ def test_chunk_matmul_activation_alignment(ctx):
     assert np.any(outs[0] != 0)
 
 
+@pytest.mark.parametrize("bias", [True, False], ids=["bias", "no_bias"])
+def test_chunk_matmul_reduction_alignment(ctx, bias):
+    # a split product's k-slice sums are added four elements per lane when y, the bias and every
+    # row allow 16-byte accesses and one element per lane otherwise (y one float off here): the
+    # same additions in the same order, so the outputs agree to the bit
+    ty, n_tok, rows, cols = QuantType.Q8_0, 128, 2880, 4096  # a 128-token chunk's attn_output: 11 slices
+    w, _ = fx.synth_blocks(int(ty), rows * cols // ty.block_elems, 0x7B1)
+    x = fx.synth.unit(0x7B2, n_tok * cols).reshape(n_tok, cols)
+    dw, dx = ctx.upload(w), ctx.upload(x)
+    db = ctx.upload(fx.synth.unit(0x7B3, rows)) if bias else None
+    outs = []
+    for off in (0, 4):
+        buf = ctx.alloc(n_tok * rows * 4 + 16)
+        y = DeviceView(buf, off, n_tok * rows * 4)
+        ctx.matmul_q(ty, y, dw, dx, db, n_tok, rows, cols)
+        outs.append(ctx.download(y, np.float32, (n_tok, rows)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.all(np.isfinite(outs[0])) and np.any(outs[0] != 0)
+
+
 def test_chunk_matmul_refusals(ctx):
     lib = ctx._lib
     buf = ctx.alloc(1 << 16)
