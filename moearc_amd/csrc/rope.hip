@@ -197,20 +197,27 @@ extern "C" __global__ void moearc_rope_kv_append_chunk_k(void *k_pages, void *v_
 // them once per 4 heads). Each lane stores 8 bytes of K and of V -- a row is one 128-byte line --
 // written through to the device-coherent level. Same results as moearc_rope_kv_append_chunk_k.
 //
-// p[0 .. 3] summed over n >= 1 slices `stride` floats apart, in slice order, then + bias[0 .. 3]
-// when given: per element the additions, in the order, of moearc_matmul_reduce_k, so the values
-// equal what it stores for a chunk product's split-K sums. All loads leave before the first add.
-__device__ __forceinline__ float4_t slice_sum4(const float *p, uint64_t stride, uint32_t n, const float *bias) {
-    float4_t s = *(const float4_t *) p;
-    for (uint32_t z = 1; z < n; z += 4u) {
-        float4_t v[4];
+// sx = px[0 .. 3] summed over n >= 1 slices `stride` floats apart, in slice order (and sv the same
+// of pv when TWO): per element the additions, in the order, of moearc_matmul_reduce_k, so with its
+// bias added after them the values equal what it stores for a chunk product's split-K sums. Eight
+// slices' loads of both rows leave before the first add (one memory round trip for up to 8).
+template <bool TWO>
+__device__ __forceinline__ void slice_sums4(const float *px, const float *pv, uint64_t stride, uint32_t n,
+                                            float4_t &sx, float4_t &sv) {
+    for (uint32_t z = 0; z < n; z += 8u) {
+        float4_t a[8], b[8];
 #pragma unroll
-        for (uint32_t k = 0; k < 4u; ++k) v[k] = *(const float4_t *) (p + (uint64_t) min(z + k, n - 1u) * stride);
+        for (uint32_t k = 0; k < 8u; ++k) {
+            const uint64_t o = (uint64_t) min(z + k, n - 1u) * stride;
+            a[k] = *(const float4_t *) (px + o);
+            if constexpr (TWO) b[k] = *(const float4_t *) (pv + o);
+        }
 #pragma unroll
-        for (uint32_t k = 0; k < 4u; ++k)
-            if (z + k < n) s = s + v[k];
+        for (uint32_t k = 0; k < 8u; ++k) {
+            sx = z + k == 0u ? a[k] : z + k < n ? sx + a[k] : sx;
+            if constexpr (TWO) sv = z + k == 0u ? b[k] : z + k < n ? sv + b[k] : sv;
+        }
     }
-    return bias ? s + *(const float4_t *) bias : s;
 }
 
 // Rows of 64 channels, 16 per work-group (row = (token, head) of n_heads rows per token, with
@@ -241,14 +248,23 @@ __device__ __forceinline__ void rope64_rows(uint32_t b, uint32_t nh, const float
     uint32_t slot = 0, page = 0;
     if (live) {
         if constexpr (SUMS) {
+            if constexpr (KV) {  // before the sums, which wait on their loads
+                slot = slots[t];
+                page = page_ids[t];
+            }
             const uint64_t bo = (row - t * nh) * 64u + 4u * c;
-            kx = slice_sum4(x + row * 64u + 4u * c, stride, n_slices, bx ? bx + bo : nullptr);
-            if constexpr (KV) vx = slice_sum4(v + row * 64u + 4u * c, stride, n_slices, bv ? bv + bo : nullptr);
+            const float4_t zero = {0.f, 0.f, 0.f, 0.f};
+            const float4_t kb = bx ? *(const float4_t *) (bx + bo) : zero;
+            float4_t vb = zero;
+            if constexpr (KV) vb = bv ? *(const float4_t *) (bv + bo) : zero;
+            slice_sums4<KV>(x + row * 64u + 4u * c, KV ? v + row * 64u + 4u * c : nullptr, stride, n_slices, kx, vx);
+            if (bx) kx = kx + kb;
+            if (KV && bv) vx = vx + vb;
         } else {
             kx = *(const float4_t *) (x + row * 64u + 4u * c);
             if constexpr (KV) vx = *(const float4_t *) (v + row * 64u + 4u * c);
         }
-        if constexpr (KV) {
+        if constexpr (KV && !SUMS) {
             slot = slots[t];
             page = page_ids[t];
         }
