@@ -1503,18 +1503,20 @@ int mm_launch(moearc_ctx *c, unsigned ty, const MmMat *m, unsigned n_mat, const 
     // each work-group walks the whole reduction (a 128-token chunk's k and v projections at gpt-oss
     // shapes are 4 work-groups), so the reduction is cut into slices of at least 4 k-blocks over a
     // third grid dimension, whose sums a second launch adds in slice order, with the bias and the
-    // residual. The slice count fills every CU at least once, aiming at one work-group per CU for
-    // chunks of one or two 128-token tiles and two above (measured on gpt-oss blocks: at 128 and 256
-    // tokens the reduction's traffic, which grows with the slices, outweighs a second work-group per
-    // CU; at 512 the reverse); MOEARC_MM_SPLIT_WG sets the aim. K-quant slices start on a
-    // 256-element super-block (a multiple of 8 k-blocks), matmul2.hip's Q8_0 and MXFP4 slices on a pair.
+    // residual. The grid takes at most `aim` work-groups per CU: one for chunks of one or two
+    // 128-token tiles and two above (measured on gpt-oss blocks: at 128 and 256 tokens the
+    // reduction's traffic, which grows with the slices, outweighs a second work-group per CU; at 512
+    // the reverse); MOEARC_MM_SPLIT_WG sets the aim. Rounding the slice count down keeps every CU's
+    // share equal: rounded up, the grid's last work-groups double up on some CUs, which then set the
+    // time (q/k/v at gpt-oss shapes, 5,120 rows: 256 tokens 41.7-42.2 -> 37.7-39.3 µs, 128 tokens
+    // 27.0-27.7 -> 25.8-26.9). K-quant slices start on a 256-element super-block (a multiple of 8
+    // k-blocks), matmul2.hip's Q8_0 and MXFP4 slices on a pair.
     const uint64_t nb = n_cols / 32, tiles = (uint64_t) gx * gy;
     const uint64_t gran = (ty == 12u || ty == 13u || ty == 14u) ? 8 : (mm2 && pairs) ? 2 : 1;
     uint64_t slices = 1, kb_per = nb;
     const uint64_t aim = c->mm_split_wg >= 0 ? (uint64_t) c->mm_split_wg : (gy <= 2 || wide) ? 1 : 2;
     if (tiles <= kMmCUs && nb >= 8 && aim) {
-        const uint64_t fill = (kMmCUs + tiles - 1) / tiles;  // slices for one work-group on every CU
-        const uint64_t want = std::max<uint64_t>(1, std::min<uint64_t>(std::max(fill, aim * kMmCUs / tiles), nb / 4));
+        const uint64_t want = std::max<uint64_t>(1, std::min<uint64_t>(aim * kMmCUs / tiles, nb / 4));
         kb_per = (nb + want - 1) / want;
         kb_per = (kb_per + gran - 1) / gran * gran;
         slices = (nb + kb_per - 1) / kb_per;
